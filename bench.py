@@ -1,0 +1,342 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X quantized compute path (one GPU).
+
+Headline (the timed region): LLaMA-7B decode, batch 1 -- one step is the
+decoder-layer matvec set (Wq, Wk, Wv, Wo, W_gate, W_up in Q4_K, W_down in
+Q6_K) of all 32 layers, 224 launches captured in one HIP graph.  Every layer
+has its own copy of the weights in HBM (4.0 GB per step, far beyond the
+256 MB Infinity Cache), activations are resident before timing starts.
+``value`` is algorithmic GB/s = (packed weight bytes + activations read +
+outputs written) / step time; tok/s = batch / step time.
+
+After the timed region, bench.py reports (in "extra"): the same step at
+batch 4 and 16, the roofline of the dominant kernel (the Q4_K GEMV, timed per
+launch with HIP events on its stream), 16-tenant multi-LoRA overhead
+(config 3), prefill TFLOP/s (config 2, Q4_K and Q8_0 with bf16 activations)
+and the CPU baseline (the oracle's restatement of realm-compute-cpu, timed on
+this host).  All inputs are synthetic and seeded (realm_amd/synth.py).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, REPO)
+
+from realm_amd import synth  # noqa: E402
+from realm_amd.formats import GGML_Q4_K, GGML_Q6_K, GGML_Q8_0, weight_bytes  # noqa: E402
+
+METRIC = "Q4_K dequant-GEMV HBM GB/s (% peak) + tok/s at 7B; multi-LoRA overhead %"
+HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
+LAYERS = 32
+LAYER = [("wq", GGML_Q4_K, 4096, 4096), ("wk", GGML_Q4_K, 4096, 4096),
+         ("wv", GGML_Q4_K, 4096, 4096), ("wo", GGML_Q4_K, 4096, 4096),
+         ("w_gate", GGML_Q4_K, 11008, 4096), ("w_up", GGML_Q4_K, 11008, 4096),
+         ("w_down", GGML_Q6_K, 4096, 11008)]
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def alg_bytes(t: int, n: int, k: int, m: int, act_bytes: int = 4) -> int:
+    return weight_bytes(t, n, k) + act_bytes * m * k + 4 * m * n
+
+
+class Model7B:
+    """32 layers of distinct device copies of one seeded LLaMA-7B layer."""
+
+    def __init__(self, be, layers: int, max_m: int):
+        self.be = be
+        g = synth.rng(1)
+        host = [(name, t, n, k, synth.blocks(g, t, n, k)) for name, t, n, k in LAYER]
+        self.layers = []
+        for _ in range(layers):
+            self.layers.append([(name, t, n, k, be.register_weights(t, b, n, k))
+                                for name, t, n, k, b in host])
+        self.x = {k: be.alloc(max_m * k * 4).upload(synth.activations(g, max_m, k))
+                  for k in (4096, 11008)}
+        self.y = {name: be.alloc(max_m * n * 4) for name, _, n, _ in LAYER}
+
+    def step(self, m: int, stream: int, only_q4k: bool = False) -> None:
+        for layer in self.layers:
+            for name, t, n, k, h in layer:
+                if only_q4k and t != GGML_Q4_K:
+                    continue
+                self.be.matmul_dev(h, self.x[k].ptr, m, self.y[name].ptr, stream=stream)
+
+    def bytes_per_step(self, m: int, only_q4k: bool = False) -> int:
+        return len(self.layers) * sum(alg_bytes(t, n, k, m) for _, t, n, k in LAYER
+                                      if not only_q4k or t == GGML_Q4_K)
+
+    def close(self):
+        for layer in self.layers:
+            for *_, h in layer:
+                self.be.release_weights(h)
+        for b in list(self.x.values()) + list(self.y.values()):
+            b.close()
+
+
+def capture(be, stream: int, fn) -> int:
+    fn()  # eager run sizes the library's scratch buffers
+    be.synchronize()
+    be.graph_begin(stream)
+    fn()
+    return be.graph_end(stream)
+
+
+def time_graph(be, graph: int, stream: int, reps: int) -> float:
+    """Mean ms per replay, HIP events on `stream`."""
+    e0, e1 = be.event(), be.event()
+    be.record(e0, stream)
+    for _ in range(reps):
+        be.graph_launch(graph, stream)
+    be.record(e1, stream)
+    return be.elapsed_ms(e0, e1) / reps
+
+
+def per_launch_ms(be, stream: int, launches) -> list[float]:
+    """Duration of each launch, HIP events recorded right around it."""
+    evs = [(be.event(), be.event()) for _ in launches]
+    for (a, b), fn in zip(evs, launches):
+        be.record(a, stream)
+        fn()
+        be.record(b, stream)
+    be.synchronize()
+    return [be.elapsed_ms(a, b) for a, b in evs]
+
+
+def decode_roofline(be, model: Model7B, stream: int) -> dict:
+    """Q4_K GEMV (batch 1) over the 6 Q4_K matrices of all 32 layers."""
+    launches, nbytes = [], []
+    for layer in model.layers:
+        for name, t, n, k, h in layer:
+            if t != GGML_Q4_K:
+                continue
+            launches.append(lambda h=h, k=k, name=name: be.matmul_dev(
+                h, model.x[k].ptr, 1, model.y[name].ptr, stream=stream))
+            nbytes.append(alg_bytes(t, n, k, 1))
+    per_launch_ms(be, stream, launches)  # warm
+    ms = per_launch_ms(be, stream, launches)
+    avg_ms = float(np.mean(ms))
+    avg_bytes = float(np.mean(nbytes))
+    achieved = avg_bytes / (avg_ms * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": "realm_gemv_q4k_l64_u1_r4", "launches": len(ms),
+            "avg_launch_us": round(avg_ms * 1e3, 3), "avg_alg_bytes_per_launch": int(avg_bytes),
+            "shape_mix": "4 x (4096x4096) + 2 x (11008x4096) per layer, 32 layers"}
+
+
+def lora_overhead(be, stream: int, reps: int) -> dict:
+    """Config 3: q_proj and v_proj (Q4_K 4096x4096) for 64 tokens, 16 adapters
+    with ranks from {8,16,64}, Zipf(1.1) tenant ids, 10% without adapter.
+    warm: the same weights and adapters every replay; cold: 8 rotated copies
+    (base + adapters), 8 x 47 MB, so the adapters are re-read from HBM."""
+    g = synth.rng(3)
+    n = k = 4096
+    m = 64
+    copies = 8
+    base_host = [synth.q4k_blocks(g, n, k) for _ in range(2)]
+    ranks = [int(r) for r in g.choice([8, 16, 64], 16)]
+    ad_host = [[synth.lora_adapter(g, r, k, n) for r in ranks] for _ in range(2)]
+    ids = synth.adapter_ids(g, m, 16)
+    x = be.alloc(m * k * 4).upload(synth.activations(g, m, k))
+    d_ids = be.alloc(m * 4).upload(ids)
+    y = [be.alloc(m * n * 4) for _ in range(2)]
+    sets, weights, adapters = [], [], []
+    for _c in range(copies):
+        ws, ss = [], []
+        for p in range(2):
+            ws.append(be.register_weights(GGML_Q4_K, base_host[p], n, k))
+            hs = [be.lora_register(a, b, r, 16.0, k, n) for (a, b), r in zip(ad_host[p], ranks)]
+            adapters += hs
+            ss.append(be.lora_set_create(hs))
+        weights.append(ws)
+        sets.append(ss)
+
+    def base(c):
+        for p in range(2):
+            be.matmul_dev(weights[c][p], x.ptr, m, y[p].ptr, stream=stream)
+
+    def lora(c):
+        for p in range(2):
+            be.multi_lora_matmul_dev(weights[c][p], sets[c][p], x.ptr, m, d_ids.ptr, y[p].ptr,
+                                     stream=stream)
+
+    res = {}
+    for mode, cs in (("warm", [0]), ("cold", list(range(copies)))):
+        gb = capture(be, stream, lambda: [base(c) for c in cs])
+        gl = capture(be, stream, lambda: [lora(c) for c in cs])
+        time_graph(be, gb, stream, 5)
+        time_graph(be, gl, stream, 5)
+        tb = time_graph(be, gb, stream, reps) / len(cs)
+        tl = time_graph(be, gl, stream, reps) / len(cs)
+        be.graph_release(gb)
+        be.graph_release(gl)
+        res[mode] = {"base_us": round(tb * 1e3, 2), "lora_us": round(tl * 1e3, 2),
+                     "overhead_pct": round((tl / tb - 1) * 100, 1)}
+    distinct = sorted({int(i) for i in ids if i >= 0})
+    res["distinct_adapters"] = len(distinct)
+    res["adapter_bytes_per_proj"] = int(sum(2 * 2 * ranks[i] * (k + n) // 2 for i in distinct))
+    for ss in sets:
+        for s in ss:
+            be.lora_set_release(s)
+    for h in adapters:
+        be.lora_release(h)
+    for ws in weights:
+        for w in ws:
+            be.release_weights(w)
+    for b in [x, d_ids] + y:
+        b.close()
+    return res
+
+
+def prefill(be, stream: int, reps: int) -> dict:
+    """Config 2: M=512, K=4096 -> N=11008, bf16 activations, f32 output."""
+    g = synth.rng(2)
+    m, n, k = 512, 11008, 4096
+    xb = be.alloc(m * k * 2).upload(synth.activations_bf16(g, m, k))
+    y = be.alloc(m * n * 4)
+    out = {}
+    for t, name in ((GGML_Q4_K, "q4k"), (GGML_Q8_0, "q80")):
+        h = be.register_weights(t, synth.blocks(g, t, n, k), n, k)
+        gr = capture(be, stream, lambda: be.matmul_dev(h, xb.ptr, m, y.ptr, stream=stream,
+                                                       bf16=True))
+        time_graph(be, gr, stream, 3)
+        ms = time_graph(be, gr, stream, reps)
+        be.graph_release(gr)
+        be.release_weights(h)
+        tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+        out[name] = {"us": round(ms * 1e3, 1), "tflops": round(tf, 1),
+                     "frac_mfma_peak": round(tf / MFMA_F16_PEAK_TFLOPS, 4)}
+    xb.close()
+    y.close()
+    return out
+
+
+def cpu_baseline(seconds: float) -> tuple[dict, dict]:
+    """The oracle's C restatement of realm-compute-cpu on this host's cores:
+    Q4_K 4096x4096 matvec (batch 1), dequantize-row-then-dot on all cores, and
+    fused.rs semantics on one core.  Bounded to about `seconds` each."""
+    from oracle import oracle as o  # checker/baseline only
+    g = synth.rng(1)
+    n = k = 4096
+    blocks = synth.q4k_blocks(g, n, k)
+    x = synth.activations(g, 1, k)
+    nbytes = alg_bytes(GGML_Q4_K, n, k, 1)
+    threads = len(os.sched_getaffinity(0))
+    used, _ = o.fused_parallel(GGML_Q4_K, blocks, x, 1, n, k, threads)
+    t0, reps = time.perf_counter(), 0
+    while time.perf_counter() - t0 < seconds:
+        o.fused_parallel(GGML_Q4_K, blocks, x, 1, n, k, threads)
+        reps += 1
+    par = nbytes * reps / (time.perf_counter() - t0) / 1e9
+    t0, reps1 = time.perf_counter(), 0
+    while time.perf_counter() - t0 < seconds:
+        o.fused(GGML_Q4_K, blocks, x, 1, n, k)
+        reps1 += 1
+    one = nbytes * reps1 / (time.perf_counter() - t0) / 1e9
+    base = {"value": round(par, 3), "unit": "GB/s", "cores": int(used), "kind": "port",
+            "sample": f"Q4_K 4096x4096 matvec, batch 1, dequantize row + f32 dot "
+                      f"(CandleCpuBackend semantics), {reps} reps in ~{seconds:.0f}s on {used} "
+                      f"threads; oracle/realm_oracle.c"}
+    single = {"value": round(one, 3), "unit": "GB/s", "cores": 1,
+              "sample": f"same matvec with fused.rs semantics, {reps1} reps, 1 thread"}
+    return base, single
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--layers", type=int, default=LAYERS)
+    ap.add_argument("--cpu-seconds", type=float, default=8.0)
+    ap.add_argument("--skip-extra", action="store_true",
+                    help="only the timed decode step and the roofline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
+              "(this build has no multi-GPU path)", file=sys.stderr)
+        return 2
+
+    from realm_amd.backend import HipGpuBackend
+    be = HipGpuBackend(0)
+    stream = be.stream()
+    log(f"registering {args.layers} LLaMA-7B layers")
+    model = Model7B(be, args.layers, 16)
+
+    # ---- timed region: batch-1 decode steps replayed from one HIP graph
+    m = 1
+    graph = capture(be, stream, lambda: model.step(m, stream))
+    for _ in range(args.warmup):
+        be.graph_launch(graph, stream)
+    be.synchronize()
+    e0, e1 = be.event(), be.event()
+    t0 = time.perf_counter()
+    be.record(e0, stream)
+    for _ in range(args.steps):
+        be.graph_launch(graph, stream)
+    be.record(e1, stream)
+    be.synchronize()
+    wall = (time.perf_counter() - t0) / args.steps
+    ev_ms = be.elapsed_ms(e0, e1) / args.steps
+    be.graph_release(graph)
+    step_bytes = model.bytes_per_step(m)
+    value = step_bytes / wall / 1e9
+    log(f"decode b1: {wall * 1e3:.3f} ms/step (events {ev_ms:.3f}), {value:.1f} GB/s")
+
+    extra = {"decode": {"b1": {"ms_per_step": round(wall * 1e3, 4),
+                               "tok_per_s": round(m / wall, 1),
+                               "gb_per_s": round(value, 1)}}}
+    roof = decode_roofline(be, model, stream)
+    log(f"roofline: {roof['achieved']} GB/s ({roof['frac'] * 100:.1f}% of peak)")
+    if not args.skip_extra:
+        for mb in (4, 16):
+            gr = capture(be, stream, lambda: model.step(mb, stream))
+            time_graph(be, gr, stream, 2)
+            ms = time_graph(be, gr, stream, max(5, args.steps // 2))
+            be.graph_release(gr)
+            gbs = model.bytes_per_step(mb) / (ms * 1e-3) / 1e9
+            extra["decode"][f"b{mb}"] = {"ms_per_step": round(ms, 4),
+                                         "tok_per_s": round(mb / (ms * 1e-3), 1),
+                                         "gb_per_s": round(gbs, 1)}
+            log(f"decode b{mb}: {ms:.3f} ms/step, {gbs:.1f} GB/s")
+    model.close()
+    cpu, cpu1 = None, None
+    if not args.skip_extra:
+        extra["multi_lora_config3"] = lora_overhead(be, stream, 50)
+        log(f"multi-LoRA: {extra['multi_lora_config3']}")
+        extra["prefill_config2"] = prefill(be, stream, 10)
+        log(f"prefill: {extra['prefill_config2']}")
+        cpu, cpu1 = cpu_baseline(args.cpu_seconds)
+        extra["cpu_baseline_1thread"] = cpu1
+        log(f"cpu baseline: {cpu}")
+
+    line = {
+        "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall * 1e3, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded, realm_amd/synth.py)",
+        "config": {"workload": "config1: LLaMA-7B decoder-layer matvec set (Q4_K Wq/Wk/Wv/Wo/"
+                               "W_gate/W_up, Q6_K W_down) x 32 layers, decode batch 1",
+                   "layers": args.layers, "batch": m, "alg_bytes_per_step": step_bytes,
+                   "tok_per_s": round(m / wall, 1), "hbm_frac": round(value / HBM_PEAK_GBS, 4)},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,236 @@
+/*
+ * realm_hip.h -- C ABI of the MI355X (gfx950) quantized compute path.
+ *
+ * This is the drop-in boundary for Realm's quantized dequant x matmul path.
+ * The Rust host binds it with `extern "C"` behind its
+ * existing GpuBackendTrait and candle_matmul host functions.  All pointers are
+ * plain C pointers; sizes are element counts unless named *_bytes / nbytes.
+ *
+ * Conventions (all entry points):
+ *  - Return a realm_status (0 = Ok).  On failure a message is stored in a
+ *    thread-local slot read with realm_hip_last_error(), as the reference's
+ *    C ABI does (crates/realm-runtime/src/lib.rs:137-150).
+ *  - Inputs are borrowed for the duration of the call; outputs are allocated
+ *    by the caller.  Host-pointer entry points are synchronous.
+ *  - Weight layout on the host is the reference's: N rows of K/QK packed
+ *    blocks, row-major by output feature (crates/realm-compute-cpu/src/
+ *    fused.rs:266), blocks byte-identical to crates/realm-core/src/quant.rs
+ *    (Q8_0 34 B :52-59, Q4_K 144 B :97-107, Q6_K 210 B :191-198).
+ *  - Matmul semantics: out[b*n + j] = sum_k W[j,k] * input[b*k + k]
+ *    (x . W^T), f32 output.
+ *  - Any thread may call; each thread gets its own HIP stream.  The weight
+ *    and adapter registries are guarded by a mutex.
+ */
+#ifndef REALM_HIP_H
+#define REALM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define REALM_HIP_ABI_VERSION 1
+
+/* Error codes: crates/realm-runtime/src/lib.rs:110-135 (ErrorCode) and the
+ * From<realm_core::Error> mapping there: InvalidShape -> InvalidArgument,
+ * BackendError -> BackendUnsupported, Runtime -> GenericFailure. */
+typedef enum realm_status {
+    REALM_OK = 0,
+    REALM_GENERIC_FAILURE = 1,
+    REALM_OUT_OF_MEMORY = 2,
+    REALM_INVALID_ARGUMENT = 3,
+    REALM_MODEL_PARSE_ERROR = 4,
+    REALM_BACKEND_UNSUPPORTED = 5,
+    REALM_SHADER_COMPILE_ERROR = 6,
+    REALM_IO_ERROR = 7
+} realm_status;
+
+/* ggml tensor type ids (crates/realm-core/src/formats/gguf.rs:458-480). */
+#define REALM_GGML_F32 0
+#define REALM_GGML_Q8_0 8
+#define REALM_GGML_Q4_K 12
+#define REALM_GGML_Q6_K 14
+
+/* Adapter storage dtypes for LoRA A/B. */
+#define REALM_DTYPE_F32 0
+#define REALM_DTYPE_F16 1
+
+/* ------------------------------------------------------------ lifecycle */
+
+/* Select the device, load the gfx950 code object (hipModuleLoadData) and
+ * resolve every kernel.  Idempotent; other entry points call it lazily on
+ * device 0.  Replaces backend construction in Memory64Runtime::
+ * create_gpu_backend (crates/realm-runtime/src/memory64_host.rs:446-465). */
+int realm_hip_init(int device);
+
+/* Thread-local message of the last failed call on this thread ("" if none).
+ * crates/realm-runtime/src/lib.rs:137-150 (set_last_error/take_last_error). */
+const char *realm_hip_last_error(void);
+
+/* GpuBackendTrait::name (crates/realm-compute-gpu/src/gpu_backend_trait.rs:142). */
+const char *realm_hip_backend_name(void);
+
+/* fused.rs replaces NaN/Inf super-block scales by constants
+ * (crates/realm-compute-cpu/src/fused.rs:276-285, 1171-1175); quant.rs and
+ * the Candle backends do not.  0 (default) = quant.rs behaviour, 1 = fused.rs
+ * behaviour.  Process-wide. */
+int realm_hip_set_nan_fallback(int enable);
+
+/* ------------------------------------------- GpuBackendTrait (host slices) */
+
+/* GpuBackendTrait::matmul (gpu_backend_trait.rs:18-20): C = A @ B with A
+ * [m,k], B [k,n] row-major f32; out has m*n elements. */
+int realm_hip_matmul(const float *a, size_t a_len, const float *b, size_t b_len,
+                     uint32_t m, uint32_t k, uint32_t n, float *out);
+
+/* GpuBackendTrait::fused_dequant_matmul_q4k / _q6k / _q80
+ * (gpu_backend_trait.rs:22-29, 42-49, 122-129).  Validation as in the
+ * reference backends (crates/realm-compute-gpu/src/candle_backend.rs:448-464,
+ * 1115-1131; lib.rs:339-345): k % 256 == 0 (k % 32 == 0 for Q8_0), n_blocks
+ * == n*k/QK and input_len == batch_size*k, else REALM_INVALID_ARGUMENT.
+ * out has batch_size*n elements.  Weights are uploaded for this call only;
+ * use realm_hip_weights_register for device-resident weights. */
+int realm_hip_fused_dequant_matmul_q4k(const void *blocks, size_t n_blocks,
+                                       const float *input, size_t input_len,
+                                       size_t batch_size, size_t n, size_t k,
+                                       float *out);
+int realm_hip_fused_dequant_matmul_q6k(const void *blocks, size_t n_blocks,
+                                       const float *input, size_t input_len,
+                                       size_t batch_size, size_t n, size_t k,
+                                       float *out);
+int realm_hip_fused_dequant_matmul_q80(const void *blocks, size_t n_blocks,
+                                       const float *input, size_t input_len,
+                                       size_t batch_size, size_t n, size_t k,
+                                       float *out);
+
+/* Format-generic form of the three above (ggml_type 8, 12 or 14).  Every
+ * other fused_dequant_matmul_* of the trait (Q2_K..Q8_1, Q5_K, Q8_K) returns
+ * REALM_BACKEND_UNSUPPORTED so that dispatch_matmul falls back to the CPU
+ * (crates/realm-models/src/matmul_dispatch.rs:72-88). */
+int realm_hip_fused_dequant_matmul(int ggml_type, const void *blocks, size_t n_blocks,
+                                   const float *input, size_t input_len,
+                                   size_t batch_size, size_t n, size_t k, float *out);
+
+/* ----------------------------------------- candle_matmul host functions */
+
+/* env.candle_matmul / env.candle_matmul_transposed
+ * (crates/realm-runtime/src/memory64_host.rs:853-969, 971-1086) over a
+ * tenant's linear memory `mem` of mem_len bytes.  A [m,k] at a_ptr, B [k,n]
+ * (or [n,k] when transposed) at b_ptr, C [m,n] written at result_ptr, all
+ * little-endian f32.  Returns m*n on success, -3 when A is out of bounds, -4
+ * when B is, -5 on a compute failure, -6 when C does not fit (the reference's
+ * -2 "no memory export" has no counterpart: the caller passes the memory). */
+int32_t realm_hip_candle_matmul(uint8_t *mem, size_t mem_len, uint32_t a_ptr,
+                                uint32_t b_ptr, uint32_t result_ptr, uint32_t m,
+                                uint32_t k, uint32_t n);
+int32_t realm_hip_candle_matmul_transposed(uint8_t *mem, size_t mem_len, uint32_t a_ptr,
+                                           uint32_t b_ptr, uint32_t result_ptr,
+                                           uint32_t m, uint32_t k, uint32_t n);
+
+/* --------------------------------------------------------- dequantize */
+
+/* dequantize_tensor (crates/realm-core/src/quant.rs:663-770) on the GPU,
+ * bit-exact with dequantize_q4_k / _q6_k / _q8_0 (quant.rs:127-187, 393-451,
+ * 371-387).  Q4_K: nbytes % 144 != 0 -> REALM_MODEL_PARSE_ERROR, element
+ * count mismatch -> REALM_INVALID_ARGUMENT.  Q6_K / Q8_0 ignore a trailing
+ * partial block and zero-fill elements past the last block; an
+ * element_count smaller than the blocks' output (a panic in the reference)
+ * is REALM_INVALID_ARGUMENT. */
+int realm_hip_dequantize(int ggml_type, const void *data, size_t nbytes,
+                         size_t element_count, float *out);
+
+/* -------------------------------------------- device-resident weights */
+
+/* Upload a [n,k] quantized matrix once and keep it in HBM in the device
+ * layout (repacked on the GPU).  Replaces the per-call f32 upload of
+ * CandleGpuBackend (candle_backend.rs:484-490) for the weights that
+ * realm_forward_layer reads every call (memory64_host.rs:1958-2225).
+ * ggml_type is 12 (Q4_K), 14 (Q6_K) or 8 (Q8_0). */
+int realm_hip_weights_register(int ggml_type, const void *blocks, size_t nbytes,
+                               size_t n, size_t k, uint64_t *handle);
+int realm_hip_weights_release(uint64_t handle);
+int realm_hip_weights_info(uint64_t handle, int *ggml_type, size_t *n, size_t *k,
+                           size_t *device_bytes);
+
+/* y = x . W^T with resident W; host x [batch,k] f32 in, host y [batch,n] out. */
+int realm_hip_weights_matmul(uint64_t handle, const float *input, size_t batch,
+                             float *out);
+
+/* Same with device pointers on a caller stream (NULL = this thread's stream);
+ * asynchronous.  x is f32 [batch,k]; y is f32 [batch,n]. */
+int realm_hip_weights_matmul_dev(uint64_t handle, const float *d_input, size_t batch,
+                                 float *d_out, void *stream);
+
+/* Prefill form with bf16 activations (raw bf16 bits, [batch,k]). */
+int realm_hip_weights_matmul_bf16_dev(uint64_t handle, const uint16_t *d_input,
+                                      size_t batch, float *d_out, void *stream);
+
+/* ----------------------------------------------------------- multi-LoRA */
+
+/* Register one adapter's factors for one projection: A [rank, in_dim] and
+ * B [out_dim, rank] row-major (the LoRAWeights lora_a / lora_b of
+ * crates/realm-runtime/src/lora.rs:10-23), scale alpha/rank (lora.rs:49-52).
+ * dtype is REALM_DTYPE_F32 or REALM_DTYPE_F16 (raw binary16 bits); the
+ * device keeps the given dtype.  rank must be 1..256. */
+int realm_hip_lora_register(int dtype, const void *lora_a, const void *lora_b,
+                            size_t rank, float alpha, size_t in_dim, size_t out_dim,
+                            uint64_t *handle);
+int realm_hip_lora_release(uint64_t handle);
+
+/* Group adapters into a device-resident table; slot i of the set is
+ * lora_handles[i].  All adapters of a set share in_dim, out_dim and dtype. */
+int realm_hip_lora_set_create(const uint64_t *lora_handles, size_t count,
+                              uint64_t *set_handle);
+int realm_hip_lora_set_release(uint64_t set_handle);
+
+/* Multi-tenant matmul: for every token t
+ *   y[t] = W x[t] + (alpha_a/r_a) * B_a (A_a x[t])   with a = adapter_ids[t]
+ * and y[t] = W x[t] when adapter_ids[t] < 0 (no adapter).  Equal, up to f32
+ * rounding, to the reference's merged form W + scale*(B@A)
+ * (crates/realm-runtime/src/lora.rs:91-144) applied per tenant.  Host
+ * pointers, synchronous. */
+int realm_hip_multi_lora_matmul(uint64_t weight_handle, uint64_t set_handle,
+                                const float *input, size_t batch,
+                                const int32_t *adapter_ids, float *out);
+
+/* Device-pointer form, asynchronous on `stream` (NULL = this thread's). */
+int realm_hip_multi_lora_matmul_dev(uint64_t weight_handle, uint64_t set_handle,
+                                    const float *d_input, size_t batch,
+                                    const int32_t *d_adapter_ids, float *d_out,
+                                    void *stream);
+
+/* -------------------------------------------------------- HIP graphs */
+
+/* Capture the device-pointer calls issued on `stream` (not NULL) between
+ * begin and end into a replayable HIP graph, for launch-bound loops such as a
+ * decode step.  Run the same calls once eagerly before capturing so that the
+ * library's scratch buffers are already sized (nothing may allocate during a
+ * capture).  No memset is recorded into a graph. */
+int realm_hip_graph_begin(void *stream);
+int realm_hip_graph_end(void *stream, uint64_t *graph_handle);
+int realm_hip_graph_launch(uint64_t graph_handle, void *stream);
+int realm_hip_graph_release(uint64_t graph_handle);
+
+/* ----------------------------------------- device memory and timing */
+
+/* Plumbing for callers without another GPU runtime (tests, bench): device
+ * buffers, copies, streams and events on this library's HIP runtime. */
+int realm_hip_malloc(void **d_ptr, size_t nbytes);
+int realm_hip_free(void *d_ptr);
+int realm_hip_memcpy_htod(void *d_dst, const void *h_src, size_t nbytes);
+int realm_hip_memcpy_dtoh(void *h_dst, const void *d_src, size_t nbytes);
+int realm_hip_memcpy_dtod(void *d_dst, const void *d_src, size_t nbytes);
+int realm_hip_stream(void **stream);            /* this thread's stream */
+int realm_hip_stream_synchronize(void *stream); /* NULL = this thread's */
+int realm_hip_device_synchronize(void);
+int realm_hip_event_create(void **event);
+int realm_hip_event_destroy(void *event);
+int realm_hip_event_record(void *event, void *stream);
+int realm_hip_event_elapsed_ms(void *start, void *stop, float *ms);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* REALM_HIP_H */

@@ -1,0 +1,293 @@
+"""Python mirror of Realm's GpuBackendTrait over the HIP C ABI.
+
+``HipGpuBackend`` exposes the trait's method names and argument meaning
+(crates/realm-compute-gpu/src/gpu_backend_trait.rs:17-143): ``matmul(a, b, m,
+k, n)`` and ``fused_dequant_matmul_{q4k,q6k,q80}(blocks, input, batch_size, n,
+k)``, returning an owned f32 array of ``batch_size * n`` elements or raising
+``RealmError`` (the ``realm_core::Error`` of crates/realm-core/src/error.rs:4-34,
+mapped from the C ABI's ErrorCode).  The trait's other fused formats raise
+``BackendError`` so a dispatcher falls back to the CPU, as
+crates/realm-models/src/matmul_dispatch.rs:72-88 does on any Err.
+
+Beyond the trait: GPU dequantization, device-resident weights, multi-tenant
+LoRA, the candle_matmul host-function surface, and device-buffer plumbing.
+"""
+from __future__ import annotations
+
+from ctypes import byref, c_float, c_int, c_size_t, c_uint64, c_void_p
+
+import numpy as np
+
+from . import _lib
+from .formats import DTYPES, GGML_Q4_K, GGML_Q6_K, GGML_Q8_0
+
+OK, GENERIC_FAILURE, OUT_OF_MEMORY, INVALID_ARGUMENT = 0, 1, 2, 3
+MODEL_PARSE_ERROR, BACKEND_UNSUPPORTED = 4, 5
+DTYPE_F32, DTYPE_F16 = 0, 1
+
+
+class RealmError(RuntimeError):
+    """A non-zero realm_status; ``code`` is the ErrorCode value."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(f"[{code}] {message}")
+        self.code = code
+        self.message = message
+
+
+class InvalidShape(RealmError):
+    pass
+
+
+class BackendError(RealmError):
+    pass
+
+
+_ERRORS = {INVALID_ARGUMENT: InvalidShape, BACKEND_UNSUPPORTED: BackendError}
+
+
+def _ptr(a: np.ndarray | None) -> c_void_p:
+    return c_void_p(0 if a is None else a.ctypes.data)
+
+
+class DeviceBuffer:
+    """A device allocation owned by the HIP library (freed on close)."""
+
+    def __init__(self, backend: "HipGpuBackend", nbytes: int):
+        self._b = backend
+        p = c_void_p()
+        backend._check(backend.lib.realm_hip_malloc(byref(p), nbytes))
+        self.ptr = p.value
+        self.nbytes = nbytes
+
+    def upload(self, a: np.ndarray) -> "DeviceBuffer":
+        a = np.ascontiguousarray(a)
+        assert a.nbytes <= self.nbytes
+        self._b._check(self._b.lib.realm_hip_memcpy_htod(c_void_p(self.ptr), _ptr(a), a.nbytes))
+        return self
+
+    def download(self, dtype, count: int) -> np.ndarray:
+        out = np.empty(count, dtype)
+        assert out.nbytes <= self.nbytes
+        self._b._check(self._b.lib.realm_hip_memcpy_dtoh(_ptr(out), c_void_p(self.ptr), out.nbytes))
+        return out
+
+    def close(self) -> None:
+        if self.ptr:
+            self._b._check(self._b.lib.realm_hip_free(c_void_p(self.ptr)))
+            self.ptr = None
+
+    def __del__(self):  # best effort
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class HipGpuBackend:
+    """GpuBackendTrait implemented on gfx950 through librealm_hip.so."""
+
+    def __init__(self, device: int = 0):
+        self.lib = _lib.load()
+        self._check(self.lib.realm_hip_init(device))
+
+    # ------------------------------------------------------------ errors
+    def last_error(self) -> str:
+        return self.lib.realm_hip_last_error().decode()
+
+    def _check(self, rc: int) -> None:
+        if rc != OK:
+            raise _ERRORS.get(rc, RealmError)(rc, self.last_error())
+
+    # ----------------------------------------------------- trait methods
+    def name(self) -> str:
+        return self.lib.realm_hip_backend_name().decode()
+
+    def matmul(self, a, b, m: int, k: int, n: int) -> np.ndarray:
+        a = np.ascontiguousarray(a, np.float32)
+        b = np.ascontiguousarray(b, np.float32)
+        out = np.empty(m * n, np.float32)
+        self._check(self.lib.realm_hip_matmul(_ptr(a), a.size, _ptr(b), b.size, m, k, n,
+                                              _ptr(out)))
+        return out
+
+    def _fused(self, ggml_type: int, blocks, input, batch_size: int, n: int, k: int):
+        blocks = np.ascontiguousarray(blocks)
+        if blocks.dtype != DTYPES[ggml_type]:
+            blocks = blocks.view(DTYPES[ggml_type])
+        x = np.ascontiguousarray(input, np.float32)
+        out = np.empty(batch_size * n, np.float32)
+        self._check(self.lib.realm_hip_fused_dequant_matmul(
+            ggml_type, _ptr(blocks), blocks.size, _ptr(x), x.size, batch_size, n, k, _ptr(out)))
+        return out
+
+    def fused_dequant_matmul_q4k(self, blocks, input, batch_size, n, k):
+        return self._fused(GGML_Q4_K, blocks, input, batch_size, n, k)
+
+    def fused_dequant_matmul_q6k(self, blocks, input, batch_size, n, k):
+        return self._fused(GGML_Q6_K, blocks, input, batch_size, n, k)
+
+    def fused_dequant_matmul_q80(self, blocks, input, batch_size, n, k):
+        return self._fused(GGML_Q8_0, blocks, input, batch_size, n, k)
+
+    def _unsupported(self, fmt: str):
+        raise BackendError(BACKEND_UNSUPPORTED, f"{fmt} is not supported by the HIP backend")
+
+    def fused_dequant_matmul_q5k(self, *a):
+        self._unsupported("Q5_K")
+
+    def fused_dequant_matmul_q8k(self, *a):
+        self._unsupported("Q8_K")
+
+    def fused_dequant_matmul_q2k(self, *a):
+        self._unsupported("Q2_K")
+
+    def fused_dequant_matmul_q3k(self, *a):
+        self._unsupported("Q3_K")
+
+    def fused_dequant_matmul_q40(self, *a):
+        self._unsupported("Q4_0")
+
+    def fused_dequant_matmul_q41(self, *a):
+        self._unsupported("Q4_1")
+
+    def fused_dequant_matmul_q50(self, *a):
+        self._unsupported("Q5_0")
+
+    def fused_dequant_matmul_q51(self, *a):
+        self._unsupported("Q5_1")
+
+    def fused_dequant_matmul_q81(self, *a):
+        self._unsupported("Q8_1")
+
+    # ------------------------------------------------------------ extras
+    def set_nan_fallback(self, enable: bool) -> None:
+        self._check(self.lib.realm_hip_set_nan_fallback(1 if enable else 0))
+
+    def dequantize(self, ggml_type: int, data, element_count: int) -> np.ndarray:
+        raw = np.ascontiguousarray(data).view(np.uint8).reshape(-1)
+        out = np.empty(element_count, np.float32)
+        self._check(self.lib.realm_hip_dequantize(ggml_type, _ptr(raw), raw.size,
+                                                  element_count, _ptr(out)))
+        return out
+
+    def candle_matmul(self, mem: np.ndarray, a_ptr, b_ptr, result_ptr, m, k, n,
+                      transposed=False) -> int:
+        assert mem.dtype == np.uint8 and mem.flags.c_contiguous
+        fn = (self.lib.realm_hip_candle_matmul_transposed if transposed
+              else self.lib.realm_hip_candle_matmul)
+        return fn(_ptr(mem), mem.size, a_ptr, b_ptr, result_ptr, m, k, n)
+
+    def register_weights(self, ggml_type: int, blocks, n: int, k: int) -> int:
+        raw = np.ascontiguousarray(blocks).view(np.uint8).reshape(-1)
+        h = c_uint64()
+        self._check(self.lib.realm_hip_weights_register(ggml_type, _ptr(raw), raw.size, n, k,
+                                                        byref(h)))
+        return h.value
+
+    def release_weights(self, handle: int) -> None:
+        self._check(self.lib.realm_hip_weights_release(handle))
+
+    def weights_info(self, handle: int):
+        t, n, k, nb = c_int(), c_size_t(), c_size_t(), c_size_t()
+        self._check(self.lib.realm_hip_weights_info(handle, byref(t), byref(n), byref(k),
+                                                    byref(nb)))
+        return t.value, n.value, k.value, nb.value
+
+    def weights_matmul(self, handle: int, x) -> np.ndarray:
+        _, n, k, _ = self.weights_info(handle)
+        x = np.ascontiguousarray(x, np.float32).reshape(-1, k)
+        out = np.empty((x.shape[0], n), np.float32)
+        self._check(self.lib.realm_hip_weights_matmul(handle, _ptr(x), x.shape[0], _ptr(out)))
+        return out
+
+    def lora_register(self, a, b, rank: int, alpha: float, in_dim: int, out_dim: int) -> int:
+        a = np.ascontiguousarray(a)
+        b = np.ascontiguousarray(b)
+        if a.dtype == np.float16:
+            dt = DTYPE_F16
+            b = b.astype(np.float16)
+        else:
+            dt = DTYPE_F32
+            a = a.astype(np.float32)
+            b = b.astype(np.float32)
+        h = c_uint64()
+        self._check(self.lib.realm_hip_lora_register(dt, _ptr(a), _ptr(b), rank, alpha, in_dim,
+                                                     out_dim, byref(h)))
+        return h.value
+
+    def lora_release(self, handle: int) -> None:
+        self._check(self.lib.realm_hip_lora_release(handle))
+
+    def lora_set_create(self, handles) -> int:
+        arr = (c_uint64 * len(handles))(*handles)
+        h = c_uint64()
+        self._check(self.lib.realm_hip_lora_set_create(arr, len(handles), byref(h)))
+        return h.value
+
+    def lora_set_release(self, handle: int) -> None:
+        self._check(self.lib.realm_hip_lora_set_release(handle))
+
+    def multi_lora_matmul(self, weight_handle: int, set_handle: int, x, ids) -> np.ndarray:
+        _, n, k, _ = self.weights_info(weight_handle)
+        x = np.ascontiguousarray(x, np.float32).reshape(-1, k)
+        ids = np.ascontiguousarray(ids, np.int32)
+        out = np.empty((x.shape[0], n), np.float32)
+        self._check(self.lib.realm_hip_multi_lora_matmul(weight_handle, set_handle, _ptr(x),
+                                                         x.shape[0], _ptr(ids), _ptr(out)))
+        return out
+
+    # --------------------------------------------------------- plumbing
+    def alloc(self, nbytes: int) -> DeviceBuffer:
+        return DeviceBuffer(self, nbytes)
+
+    def stream(self) -> int:
+        s = c_void_p()
+        self._check(self.lib.realm_hip_stream(byref(s)))
+        return s.value
+
+    def synchronize(self) -> None:
+        self._check(self.lib.realm_hip_device_synchronize())
+
+    def event(self) -> int:
+        e = c_void_p()
+        self._check(self.lib.realm_hip_event_create(byref(e)))
+        return e.value
+
+    def record(self, event: int, stream: int | None = None) -> None:
+        self._check(self.lib.realm_hip_event_record(c_void_p(event), c_void_p(stream or 0)))
+
+    def elapsed_ms(self, start: int, stop: int) -> float:
+        ms = c_float()
+        self._check(self.lib.realm_hip_event_elapsed_ms(c_void_p(start), c_void_p(stop),
+                                                        byref(ms)))
+        return ms.value
+
+    def matmul_dev(self, handle: int, d_x: int, batch: int, d_y: int, stream=None,
+                   bf16: bool = False) -> None:
+        fn = (self.lib.realm_hip_weights_matmul_bf16_dev if bf16
+              else self.lib.realm_hip_weights_matmul_dev)
+        self._check(fn(handle, c_void_p(d_x), batch, c_void_p(d_y), c_void_p(stream or 0)))
+
+    def graph_begin(self, stream: int) -> None:
+        self._check(self.lib.realm_hip_graph_begin(c_void_p(stream)))
+
+    def graph_end(self, stream: int) -> int:
+        h = c_uint64()
+        self._check(self.lib.realm_hip_graph_end(c_void_p(stream), byref(h)))
+        return h.value
+
+    def graph_launch(self, graph: int, stream: int | None = None) -> None:
+        self._check(self.lib.realm_hip_graph_launch(graph, c_void_p(stream or 0)))
+
+    def graph_release(self, graph: int) -> None:
+        self._check(self.lib.realm_hip_graph_release(graph))
+
+    def multi_lora_matmul_dev(self, wh: int, sh: int, d_x: int, batch: int, d_ids: int,
+                              d_y: int, stream=None) -> None:
+        self._check(self.lib.realm_hip_multi_lora_matmul_dev(
+            wh, sh, c_void_p(d_x), batch, c_void_p(d_ids), c_void_p(d_y), c_void_p(stream or 0)))
+
+
+__all__ = ["HipGpuBackend", "RealmError", "InvalidShape", "BackendError", "DeviceBuffer",
+           "DTYPE_F32", "DTYPE_F16"]

@@ -1,0 +1,1209 @@
+// Host side of the MI355X quantized compute path: the C ABI of
+// include/realm_hip.h on top of the HIP runtime.  The gfx950 code object is
+// embedded in this library at build time and loaded with hipModuleLoadData;
+// every kernel is launched with hipModuleLaunchKernel.
+//
+// Mirrors, for this path, the reference's GpuBackendTrait
+// (crates/realm-compute-gpu/src/gpu_backend_trait.rs:17-143) and its
+// candle_matmul host functions (crates/realm-runtime/src/memory64_host.rs:
+// 853-1087), plus what the reference lacks: device-resident weights and a
+// batched multi-adapter LoRA.
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
+#include <atomic>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "kernel_args.h"
+#include "realm_hip.h"
+
+#define REALM_STR2(x) #x
+#define REALM_STR(x) REALM_STR2(x)
+
+// The code object, embedded at link time.
+__asm__(".pushsection .rodata.realm_hsaco,\"a\",@progbits\n"
+        ".balign 4096\n"
+        ".globl realm_hsaco_begin\n"
+        ".hidden realm_hsaco_begin\n"
+        "realm_hsaco_begin:\n"
+        ".incbin \"" REALM_STR(REALM_HSACO_FILE) "\"\n"
+        ".globl realm_hsaco_end\n"
+        ".hidden realm_hsaco_end\n"
+        "realm_hsaco_end:\n"
+        ".byte 0\n"
+        ".popsection\n");
+extern "C" const unsigned char realm_hsaco_begin[];
+extern "C" const unsigned char realm_hsaco_end[];
+
+#define REALM_API extern "C" __attribute__((visibility("default")))
+
+using realm::GemmArgs;
+using realm::LoraEntry;
+
+namespace {
+
+// ------------------------------------------------------------------ errors
+
+thread_local std::string t_last_error;
+
+int fail(int code, const std::string &msg)
+{
+    t_last_error = msg;
+    return code;
+}
+
+int hip_code(hipError_t e)
+{
+    return e == hipErrorOutOfMemory ? REALM_OUT_OF_MEMORY : REALM_GENERIC_FAILURE;
+}
+
+#define HIP_TRY(expr)                                                                     \
+    do {                                                                                  \
+        hipError_t e_ = (expr);                                                           \
+        if (e_ != hipSuccess)                                                             \
+            return fail(hip_code(e_), std::string(#expr) + ": " + hipGetErrorString(e_)); \
+    } while (0)
+
+#define CHECK(expr)            \
+    do {                       \
+        int rc_ = (expr);      \
+        if (rc_ != REALM_OK)   \
+            return rc_;        \
+    } while (0)
+
+constexpr int GGML_Q8_0 = REALM_GGML_Q8_0, GGML_Q4_K = REALM_GGML_Q4_K,
+              GGML_Q6_K = REALM_GGML_Q6_K;
+
+size_t block_bytes(int t) { return t == GGML_Q4_K ? 144 : t == GGML_Q6_K ? 210 : 34; }
+size_t block_elems(int t) { return t == GGML_Q8_0 ? 32 : 256; }
+size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
+size_t round_up(size_t v, size_t m) { return (v + m - 1) / m * m; }
+const char *fmt_name(int t) { return t == GGML_Q4_K ? "q4k" : t == GGML_Q6_K ? "q6k" : "q80"; }
+
+// ------------------------------------------------------------------ device
+
+struct Device {
+    bool ready = false;
+    int id = 0;
+    int cu_count = 256;
+    size_t max_lds = 65536;
+    hipModule_t module = nullptr;
+    std::unordered_map<std::string, hipFunction_t> fns;
+};
+
+std::mutex g_mu; // device init, function cache, registries, workspaces
+Device g_dev;
+std::atomic<int> g_nan_fb{0};
+
+int init_locked(int device)
+{
+    if (g_dev.ready) {
+        if (device != g_dev.id)
+            return fail(REALM_INVALID_ARGUMENT, "realm_hip already initialised on device " +
+                                                    std::to_string(g_dev.id));
+        return REALM_OK;
+    }
+    int count = 0;
+    HIP_TRY(hipGetDeviceCount(&count));
+    if (device < 0 || device >= count)
+        return fail(REALM_INVALID_ARGUMENT, "device " + std::to_string(device) +
+                                                " out of range (" + std::to_string(count) + ")");
+    HIP_TRY(hipSetDevice(device));
+    hipDeviceProp_t prop;
+    HIP_TRY(hipGetDeviceProperties(&prop, device));
+    if (std::string(prop.gcnArchName).find("gfx950") == std::string::npos)
+        return fail(REALM_BACKEND_UNSUPPORTED,
+                    std::string("code object is built for gfx950, device is ") + prop.gcnArchName);
+    g_dev.cu_count = prop.multiProcessorCount;
+    g_dev.max_lds = prop.sharedMemPerBlock;
+    HIP_TRY(hipModuleLoadData(&g_dev.module, realm_hsaco_begin));
+    g_dev.id = device;
+    g_dev.ready = true;
+    return REALM_OK;
+}
+
+int ensure_init()
+{
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (g_dev.ready) {
+        HIP_TRY(hipSetDevice(g_dev.id));
+        return REALM_OK;
+    }
+    return init_locked(0);
+}
+
+int get_fn(const std::string &name, hipFunction_t *out)
+{
+    std::lock_guard<std::mutex> lk(g_mu);
+    auto it = g_dev.fns.find(name);
+    if (it != g_dev.fns.end()) {
+        *out = it->second;
+        return REALM_OK;
+    }
+    hipFunction_t f;
+    hipError_t e = hipModuleGetFunction(&f, g_dev.module, name.c_str());
+    if (e != hipSuccess)
+        return fail(REALM_GENERIC_FAILURE, "kernel " + name + " not found: " + hipGetErrorString(e));
+    g_dev.fns[name] = f;
+    *out = f;
+    return REALM_OK;
+}
+
+int launch(const std::string &name, dim3 grid, dim3 block, size_t lds, hipStream_t s,
+           void **args)
+{
+    if (grid.x == 0 || grid.y == 0 || grid.z == 0)
+        return REALM_OK;
+    hipFunction_t f;
+    CHECK(get_fn(name, &f));
+    HIP_TRY(hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z,
+                                  (unsigned)lds, s, args, nullptr));
+    return REALM_OK;
+}
+
+// ------------------------------------------------------------ streams etc.
+
+thread_local hipStream_t t_stream = nullptr;
+
+int thread_stream(hipStream_t *s)
+{
+    if (!t_stream)
+        HIP_TRY(hipStreamCreateWithFlags(&t_stream, hipStreamNonBlocking));
+    *s = t_stream;
+    return REALM_OK;
+}
+
+int pick_stream(void *user, hipStream_t *s)
+{
+    if (user) {
+        *s = (hipStream_t)user;
+        return REALM_OK;
+    }
+    return thread_stream(s);
+}
+
+// Per-stream scratch buffers (grow-only).  Work on one stream is ordered, so
+// reusing a stream's buffers for its next call is safe.
+enum Slot { WS_RAW, WS_WEIGHT, WS_X, WS_Y, WS_XH, WS_XL, WS_XM, WS_TS, WS_U, WS_IDS, WS_N };
+
+struct Workspace {
+    void *buf[WS_N] = {};
+    size_t cap[WS_N] = {};
+};
+std::unordered_map<hipStream_t, std::unique_ptr<Workspace>> g_ws;
+
+int ws_get(hipStream_t s, Slot slot, size_t bytes, void **out)
+{
+    Workspace *w;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        auto &p = g_ws[s];
+        if (!p)
+            p.reset(new Workspace);
+        w = p.get();
+    }
+    bytes = std::max<size_t>(bytes, 256);
+    if (w->cap[slot] < bytes) {
+        if (w->buf[slot]) {
+            HIP_TRY(hipStreamSynchronize(s));
+            HIP_TRY(hipFree(w->buf[slot]));
+            w->buf[slot] = nullptr;
+            w->cap[slot] = 0;
+        }
+        size_t cap = align256(bytes + bytes / 4);
+        HIP_TRY(hipMalloc(&w->buf[slot], cap));
+        w->cap[slot] = cap;
+    }
+    *out = w->buf[slot];
+    return REALM_OK;
+}
+
+// ----------------------------------------------------------------- weights
+
+struct Weight {
+    int type = 0;
+    size_t n = 0, k = 0, kx = 0; // kx: padded K of the device layout
+    size_t bytes = 0;
+    void *dev = nullptr;          // owned allocation (null for a per-call weight)
+    const void *w0 = nullptr, *w1 = nullptr, *w2 = nullptr;
+    bool wide = false;            // Q6_K with some |sub-scale| > 63
+};
+
+std::unordered_map<uint64_t, Weight> g_weights;
+uint64_t g_next_handle = 1;
+
+// Byte offsets of the streams of the device layout (see kernels/common.h).
+size_t layout(int type, size_t n, size_t k, size_t off[3], size_t *kx)
+{
+    size_t B = k / 256;
+    if (type == GGML_Q4_K) {
+        off[0] = 0;
+        off[1] = align256(n * B * 16);
+        off[2] = 0;
+        *kx = k;
+        return off[1] + n * (k / 2);
+    }
+    if (type == GGML_Q6_K) {
+        off[0] = 0;
+        off[1] = align256(n * B * 2);
+        off[2] = off[1] + align256(n * B * 16);
+        *kx = k;
+        return off[2] + n * B * 192;
+    }
+    size_t kp = round_up(k, 64);
+    off[0] = 0;
+    off[1] = align256(n * (kp / 32) * 2);
+    off[2] = 0;
+    *kx = kp;
+    return off[1] + n * kp;
+}
+
+bool q6k_wide(const uint8_t *blocks, size_t nblocks)
+{
+    for (size_t b = 0; b < nblocks; ++b) {
+        const int8_t *sc = reinterpret_cast<const int8_t *>(blocks + b * 210 + 192);
+        for (int i = 0; i < 16; ++i)
+            if (sc[i] > 63 || sc[i] < -63)
+                return true;
+    }
+    return false;
+}
+
+// Upload reference-layout blocks and repack them into `dst` (device layout).
+int upload_repack(int type, const void *blocks, size_t n, size_t k, void *dst, Weight *w,
+                  hipStream_t s)
+{
+    size_t nblocks = n * (k / block_elems(type));
+    size_t raw_bytes = nblocks * block_bytes(type);
+    size_t off[3], kx;
+    size_t total = layout(type, n, k, off, &kx);
+    w->type = type;
+    w->n = n;
+    w->k = k;
+    w->kx = kx;
+    w->bytes = total;
+    uint8_t *base = (uint8_t *)dst;
+    w->w0 = base + off[0];
+    w->w1 = base + off[1];
+    w->w2 = type == GGML_Q6_K ? base + off[2] : nullptr;
+    w->wide = type == GGML_Q6_K && q6k_wide((const uint8_t *)blocks, nblocks);
+    if (nblocks == 0)
+        return REALM_OK;
+    void *raw;
+    CHECK(ws_get(s, WS_RAW, raw_bytes, &raw));
+    HIP_TRY(hipMemcpyAsync(raw, blocks, raw_bytes, hipMemcpyHostToDevice, s));
+    long long nb = (long long)nblocks;
+    if (type == GGML_Q4_K) {
+        void *hdr = (void *)w->w0, *qs = (void *)w->w1;
+        void *args[] = {&raw, &hdr, &qs, &nb};
+        CHECK(launch("realm_repack_q4k", dim3((unsigned)((nblocks * 9 + 255) / 256)), dim3(256),
+                     0, s, args));
+    } else if (type == GGML_Q6_K) {
+        void *dq = (void *)w->w0, *scq = (void *)w->w1, *qq = (void *)w->w2;
+        void *args[] = {&raw, &dq, &scq, &qq, &nb};
+        CHECK(launch("realm_repack_q6k", dim3((unsigned)((nblocks * 64 + 255) / 256)),
+                     dim3(256), 0, s, args));
+    } else {
+        HIP_TRY(hipMemsetAsync(dst, 0, total, s));
+        void *dq = (void *)w->w0, *qq = (void *)w->w1;
+        int kbr = (int)(k / 32), kp = (int)kx;
+        void *args[] = {&raw, &dq, &qq, &nb, &kbr, &kp};
+        CHECK(launch("realm_repack_q80", dim3((unsigned)((nblocks * 32 + 255) / 256)),
+                     dim3(256), 0, s, args));
+    }
+    return REALM_OK;
+}
+
+// ------------------------------------------------------------------ LoRA
+
+struct Adapter {
+    int dtype = 0;
+    void *a = nullptr, *b = nullptr;
+    size_t rank = 0, in = 0, out = 0;
+    float alpha = 0.f;
+    int uses = 0; // number of sets holding it
+};
+struct AdapterSet {
+    void *table = nullptr;
+    size_t count = 0, in = 0, out = 0;
+    int rmax = 0;
+    std::vector<uint64_t> members;
+};
+std::unordered_map<uint64_t, Adapter> g_adapters;
+std::unordered_map<uint64_t, AdapterSet> g_sets;
+
+struct LoraCall {
+    const AdapterSet *set;
+    const int32_t *d_ids;
+};
+
+// --------------------------------------------------------------- dispatch
+
+// M = 1, f32 activations: the VALU GEMV.  Returns BACKEND_UNSUPPORTED when
+// the row is too long for its register budget (the caller then uses MFMA).
+int run_gemv(const Weight &w, const float *d_x, float *d_y, hipStream_t s)
+{
+    int U = (int)(w.kx / 64);
+    int lpr = U <= 16 ? 16 : (U <= 32 ? 32 : 64);
+    int upl = (U + lpr - 1) / lpr;
+    if (upl > 8 || w.kx * 4 > g_dev.max_lds)
+        return REALM_BACKEND_UNSUPPORTED;
+    // rows per pass: as many as keep >= 4 waves per CU busy
+    int rpw = 64 / lpr;
+    int maxr = upl == 1 ? 4 : (upl <= 3 ? 2 : 1);
+    if (lpr < 64 && upl > 1)
+        maxr = std::min(maxr, 2);
+    int r = maxr;
+    while (r > 1 && (long)((w.n + rpw * r - 1) / (rpw * r)) < 4L * g_dev.cu_count)
+        r >>= 1;
+    long npass = (long)((w.n + rpw * r - 1) / (rpw * r));
+    long wgs = (npass + 3) / 4;
+    // waves per CU the kernel can hold: LDS-bound (x is staged per workgroup)
+    long per_cu = std::max<long>(1, (long)(160 * 1024 / std::max<size_t>(w.kx * 4, 1)));
+    wgs = std::min<long>(wgs, std::max<long>(1, per_cu) * g_dev.cu_count * 2);
+    std::string name = std::string("realm_gemv_") + fmt_name(w.type) + "_l" +
+                       std::to_string(lpr) + "_u" + std::to_string(upl) + "_r" +
+                       std::to_string(r);
+    int N = (int)w.n, K = (int)w.k, nan_fb = g_nan_fb.load();
+    size_t lds = w.kx * 4;
+    if (w.type == GGML_Q4_K) {
+        const void *hdr = w.w0, *qs = w.w1;
+        void *args[] = {&hdr, &qs, &d_x, &d_y, &N, &K, &nan_fb};
+        return launch(name, dim3((unsigned)wgs), dim3(256), lds, s, args);
+    }
+    if (w.type == GGML_Q6_K) {
+        const void *dq = w.w0, *scq = w.w1, *qq = w.w2;
+        void *args[] = {&dq, &scq, &qq, &d_x, &d_y, &N, &K, &nan_fb};
+        return launch(name, dim3((unsigned)wgs), dim3(256), lds, s, args);
+    }
+    const void *dq = w.w0, *qq = w.w1;
+    int KP = (int)w.kx;
+    void *args[] = {&dq, &qq, &d_x, &d_y, &N, &K, &KP};
+    return launch(name, dim3((unsigned)wgs), dim3(256), lds, s, args);
+}
+
+// Any M: activation prep, optional LoRA shrink, then the MFMA kernel.
+int run_gemm(const Weight &w, const void *d_x, bool bf16, size_t M, float *d_y, hipStream_t s,
+             const LoraCall *lora)
+{
+    if (M == 0 || w.n == 0)
+        return REALM_OK;
+    // tile choice: decode tiles (16 rows x 16/32/64 tokens, K split over 4
+    // waves) or the prefill tile (128 rows x 64 tokens)
+    size_t M16 = round_up(M, 16);
+    std::string tile;
+    unsigned rows_per_wg, toks_per_wg;
+    if (M16 >= 128) {
+        tile = "p4";
+        rows_per_wg = 128;
+        toks_per_wg = 64;
+    } else if (M16 <= 16) {
+        tile = "d1";
+        rows_per_wg = 16;
+        toks_per_wg = 16;
+    } else if (M16 <= 32 && !bf16) {
+        tile = "d2";
+        rows_per_wg = 16;
+        toks_per_wg = 32;
+    } else {
+        tile = "d4";
+        rows_per_wg = 16;
+        toks_per_wg = 64;
+    }
+    // every token a workgroup reads must exist in the prepared activations
+    size_t Mp = round_up(M, toks_per_wg);
+    size_t B = w.k / 256;
+    void *xh, *xl = nullptr, *xm = nullptr, *ts;
+    CHECK(ws_get(s, WS_XH, Mp * w.kx * 2, &xh));
+    if (!bf16)
+        CHECK(ws_get(s, WS_XL, Mp * w.kx * 2, &xl));
+    if (w.type == GGML_Q4_K)
+        CHECK(ws_get(s, WS_XM, Mp * B * 64, &xm));
+    CHECK(ws_get(s, WS_TS, Mp * 4, &ts));
+    {
+        int ibf = bf16 ? 1 : 0, iM = (int)M, iK = (int)w.k, iKX = (int)w.kx;
+        void *args[] = {(void *)&d_x, &ibf, &xh, &xl, &xm, &ts, &iM, &iK, &iKX};
+        CHECK(launch(std::string("realm_xprep_") + fmt_name(w.type), dim3((unsigned)Mp),
+                     dim3(256), 0, s, args));
+    }
+    void *u = nullptr;
+    if (lora) {
+        const AdapterSet &set = *lora->set;
+        CHECK(ws_get(s, WS_U, Mp * (size_t)set.rmax * 4, &u));
+        const void *table = set.table;
+        const int32_t *ids = lora->d_ids;
+        int iM = (int)M, iK = (int)w.k, iKX = (int)w.kx, rmax = set.rmax;
+        void *args[] = {&xh, &xl, &ts, (void *)&ids, (void *)&table, &u, &iM, &iK, &iKX, &rmax};
+        std::string name = std::string("realm_lora_shrink_") + fmt_name(w.type) +
+                           (bf16 ? "_bf16" : "_f32");
+        CHECK(launch(name,
+                     dim3((unsigned)set.count, (unsigned)((set.rmax + 15) / 16),
+                          (unsigned)((M + 15) / 16)),
+                     dim3(256), 0, s, args));
+    }
+    std::string fmt = fmt_name(w.type);
+    if (w.type == GGML_Q6_K && w.wide)
+        fmt = "q6kw";
+    std::string name = "realm_gemm_" + fmt + "_" + tile + (bf16 ? "_bf16" : "_f32") +
+                       (lora ? "_lora" : "");
+    GemmArgs g;
+    std::memset(&g, 0, sizeof g);
+    g.w0 = w.w0;
+    g.w1 = w.w1;
+    g.w2 = w.w2;
+    g.xh = xh;
+    g.xl = xl;
+    g.xm = xm;
+    g.tscale = (const float *)ts;
+    g.y = d_y;
+    g.N = (int)w.n;
+    g.K = (int)w.k;
+    g.KX = (int)w.kx;
+    g.M = (int)M;
+    g.nan_fb = g_nan_fb.load();
+    if (lora) {
+        g.ids = lora->d_ids;
+        g.table = (const LoraEntry *)lora->set->table;
+        g.n_adapters = (int)lora->set->count;
+        g.u = (const float *)u;
+        g.rmax = lora->set->rmax;
+    }
+    void *args[] = {&g};
+    dim3 grid((unsigned)((w.n + rows_per_wg - 1) / rows_per_wg),
+              (unsigned)((Mp + toks_per_wg - 1) / toks_per_wg));
+    return launch(name, grid, dim3(256), 0, s, args);
+}
+
+int run_matmul(const Weight &w, const void *d_x, bool bf16, size_t M, float *d_y,
+               hipStream_t s, const LoraCall *lora)
+{
+    if (M == 1 && !bf16 && !lora) {
+        int rc = run_gemv(w, (const float *)d_x, d_y, s);
+        if (rc != REALM_BACKEND_UNSUPPORTED)
+            return rc;
+    }
+    return run_gemm(w, d_x, bf16, M, d_y, s, lora);
+}
+
+int get_weight(uint64_t h, Weight *out)
+{
+    std::lock_guard<std::mutex> lk(g_mu);
+    auto it = g_weights.find(h);
+    if (it == g_weights.end())
+        return fail(REALM_INVALID_ARGUMENT, "unknown weight handle " + std::to_string(h));
+    *out = it->second;
+    return REALM_OK;
+}
+
+// Validation of GpuBackendTrait::fused_dequant_matmul_* (candle_backend.rs:
+// 448-464 and 1115-1131; lib.rs:339-345).
+int validate_fused(int type, size_t n_blocks, size_t input_len, size_t batch, size_t n,
+                   size_t k)
+{
+    size_t qk = block_elems(type);
+    if (k % qk)
+        return fail(REALM_INVALID_ARGUMENT, "K dimension " + std::to_string(k) +
+                                                " must be multiple of " + std::to_string(qk));
+    size_t expected = n * (k / qk);
+    if (n_blocks != expected)
+        return fail(REALM_INVALID_ARGUMENT, "Expected " + std::to_string(expected) + " " +
+                                                (type == GGML_Q4_K   ? "Q4_K"
+                                                 : type == GGML_Q6_K ? "Q6_K"
+                                                                     : "Q8_0") +
+                                                " blocks, got " + std::to_string(n_blocks));
+    if (input_len != batch * k)
+        return fail(REALM_INVALID_ARGUMENT, "Input size mismatch: expected " +
+                                                std::to_string(batch * k) + ", got " +
+                                                std::to_string(input_len));
+    if (k > (size_t)INT32_MAX || n > (size_t)INT32_MAX || batch > (size_t)INT32_MAX)
+        return fail(REALM_INVALID_ARGUMENT, "dimension exceeds 2^31-1");
+    return REALM_OK;
+}
+
+int fused_host(int type, const void *blocks, size_t n_blocks, const float *input,
+               size_t input_len, size_t batch, size_t n, size_t k, float *out)
+{
+    if (type != GGML_Q4_K && type != GGML_Q6_K && type != GGML_Q8_0)
+        return fail(REALM_BACKEND_UNSUPPORTED,
+                    "ggml type " + std::to_string(type) + " is not supported by the HIP backend");
+    CHECK(validate_fused(type, n_blocks, input_len, batch, n, k));
+    CHECK(ensure_init());
+    if (batch == 0 || n == 0)
+        return REALM_OK;
+    if (k == 0) {
+        std::memset(out, 0, batch * n * sizeof(float));
+        return REALM_OK;
+    }
+    hipStream_t s;
+    CHECK(thread_stream(&s));
+    size_t off[3], kx;
+    size_t total = layout(type, n, k, off, &kx);
+    void *wbuf, *dx, *dy;
+    CHECK(ws_get(s, WS_WEIGHT, total, &wbuf));
+    Weight w;
+    CHECK(upload_repack(type, blocks, n, k, wbuf, &w, s));
+    CHECK(ws_get(s, WS_X, batch * k * 4, &dx));
+    CHECK(ws_get(s, WS_Y, batch * n * 4, &dy));
+    HIP_TRY(hipMemcpyAsync(dx, input, batch * k * 4, hipMemcpyHostToDevice, s));
+    CHECK(run_matmul(w, dx, false, batch, (float *)dy, s, nullptr));
+    HIP_TRY(hipMemcpyAsync(out, dy, batch * n * 4, hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipStreamSynchronize(s));
+    return REALM_OK;
+}
+
+// Dense f32 C = A @ B (or A @ B^T) with host pointers.
+int dense_host(const float *a, const float *b, float *c, size_t m, size_t k, size_t n, int bt)
+{
+    CHECK(ensure_init());
+    if (m == 0 || n == 0)
+        return REALM_OK;
+    if (k == 0) {
+        std::memset(c, 0, m * n * sizeof(float));
+        return REALM_OK;
+    }
+    if (m > (size_t)INT32_MAX || n > (size_t)INT32_MAX || k > (size_t)INT32_MAX)
+        return fail(REALM_INVALID_ARGUMENT, "dimension exceeds 2^31-1");
+    hipStream_t s;
+    CHECK(thread_stream(&s));
+    void *da, *db, *dc;
+    CHECK(ws_get(s, WS_X, m * k * 4, &da));
+    CHECK(ws_get(s, WS_WEIGHT, k * n * 4, &db));
+    CHECK(ws_get(s, WS_Y, m * n * 4, &dc));
+    HIP_TRY(hipMemcpyAsync(da, a, m * k * 4, hipMemcpyHostToDevice, s));
+    HIP_TRY(hipMemcpyAsync(db, b, k * n * 4, hipMemcpyHostToDevice, s));
+    int M = (int)m, N = (int)n, K = (int)k;
+    void *args[] = {&da, &db, &dc, &M, &N, &K, &bt};
+    CHECK(launch("realm_dense_f32", dim3((unsigned)((n + 63) / 64), (unsigned)((m + 63) / 64)),
+                 dim3(256), 0, s, args));
+    HIP_TRY(hipMemcpyAsync(c, dc, m * n * 4, hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipStreamSynchronize(s));
+    return REALM_OK;
+}
+
+int32_t candle_matmul_impl(uint8_t *mem, size_t mem_len, uint32_t a_ptr, uint32_t b_ptr,
+                           uint32_t r_ptr, uint32_t m, uint32_t k, uint32_t n, int bt)
+{
+    size_t a_bytes = (size_t)m * k * 4, b_bytes = (size_t)k * n * 4, r_bytes = (size_t)m * n * 4;
+    if (!mem || (size_t)a_ptr + a_bytes > mem_len) {
+        fail(REALM_INVALID_ARGUMENT, "Failed to read matrix A: out of bounds");
+        return -3;
+    }
+    if ((size_t)b_ptr + b_bytes > mem_len) {
+        fail(REALM_INVALID_ARGUMENT, "Failed to read matrix B: out of bounds");
+        return -4;
+    }
+    // linear memory offsets need not be 4-byte aligned: copy out first
+    std::vector<float> A((size_t)m * k), B((size_t)k * n), C((size_t)m * n);
+    if (a_bytes)
+        std::memcpy(A.data(), mem + a_ptr, a_bytes);
+    if (b_bytes)
+        std::memcpy(B.data(), mem + b_ptr, b_bytes);
+    if (dense_host(A.data(), B.data(), C.data(), m, k, n, bt) != REALM_OK)
+        return -5;
+    if ((size_t)r_ptr + r_bytes > mem_len) {
+        fail(REALM_INVALID_ARGUMENT, "Failed to write result: out of bounds");
+        return -6;
+    }
+    if (r_bytes)
+        std::memcpy(mem + r_ptr, C.data(), r_bytes);
+    return (int32_t)((size_t)m * n);
+}
+
+} // namespace
+
+// ======================================================================= ABI
+
+REALM_API int realm_hip_init(int device)
+{
+    std::lock_guard<std::mutex> lk(g_mu);
+    return init_locked(device);
+}
+
+REALM_API const char *realm_hip_last_error(void) { return t_last_error.c_str(); }
+
+REALM_API const char *realm_hip_backend_name(void) { return "HIP (gfx950)"; }
+
+REALM_API int realm_hip_set_nan_fallback(int enable)
+{
+    g_nan_fb.store(enable ? 1 : 0);
+    return REALM_OK;
+}
+
+REALM_API int realm_hip_matmul(const float *a, size_t a_len, const float *b, size_t b_len,
+                               uint32_t m, uint32_t k, uint32_t n, float *out)
+{
+    // CandleGpuBackend::matmul fails in tensor creation on a size mismatch
+    // (candle_backend.rs:419-425), an Error::Runtime.
+    if (a_len != (size_t)m * k || b_len != (size_t)k * n)
+        return fail(REALM_GENERIC_FAILURE, "Candle GPU tensor creation failed: shape mismatch");
+    return dense_host(a, b, out, m, k, n, 0);
+}
+
+REALM_API int realm_hip_fused_dequant_matmul_q4k(const void *blocks, size_t n_blocks,
+                                                 const float *input, size_t input_len,
+                                                 size_t batch_size, size_t n, size_t k,
+                                                 float *out)
+{
+    return fused_host(GGML_Q4_K, blocks, n_blocks, input, input_len, batch_size, n, k, out);
+}
+
+REALM_API int realm_hip_fused_dequant_matmul_q6k(const void *blocks, size_t n_blocks,
+                                                 const float *input, size_t input_len,
+                                                 size_t batch_size, size_t n, size_t k,
+                                                 float *out)
+{
+    return fused_host(GGML_Q6_K, blocks, n_blocks, input, input_len, batch_size, n, k, out);
+}
+
+REALM_API int realm_hip_fused_dequant_matmul_q80(const void *blocks, size_t n_blocks,
+                                                 const float *input, size_t input_len,
+                                                 size_t batch_size, size_t n, size_t k,
+                                                 float *out)
+{
+    return fused_host(GGML_Q8_0, blocks, n_blocks, input, input_len, batch_size, n, k, out);
+}
+
+REALM_API int realm_hip_fused_dequant_matmul(int ggml_type, const void *blocks, size_t n_blocks,
+                                             const float *input, size_t input_len,
+                                             size_t batch_size, size_t n, size_t k, float *out)
+{
+    return fused_host(ggml_type, blocks, n_blocks, input, input_len, batch_size, n, k, out);
+}
+
+REALM_API int32_t realm_hip_candle_matmul(uint8_t *mem, size_t mem_len, uint32_t a_ptr,
+                                          uint32_t b_ptr, uint32_t result_ptr, uint32_t m,
+                                          uint32_t k, uint32_t n)
+{
+    return candle_matmul_impl(mem, mem_len, a_ptr, b_ptr, result_ptr, m, k, n, 0);
+}
+
+REALM_API int32_t realm_hip_candle_matmul_transposed(uint8_t *mem, size_t mem_len,
+                                                     uint32_t a_ptr, uint32_t b_ptr,
+                                                     uint32_t result_ptr, uint32_t m,
+                                                     uint32_t k, uint32_t n)
+{
+    return candle_matmul_impl(mem, mem_len, a_ptr, b_ptr, result_ptr, m, k, n, 1);
+}
+
+REALM_API int realm_hip_dequantize(int type, const void *data, size_t nbytes,
+                                   size_t element_count, float *out)
+{
+    if (type != GGML_Q4_K && type != GGML_Q6_K && type != GGML_Q8_0)
+        return fail(REALM_BACKEND_UNSUPPORTED,
+                    "ggml type " + std::to_string(type) + " is not supported by the HIP backend");
+    size_t bb = block_bytes(type), qk = block_elems(type);
+    size_t nb = nbytes / bb;
+    if (type == GGML_Q4_K) {
+        if (nbytes % bb)
+            return fail(REALM_MODEL_PARSE_ERROR, "Q4_K data size " + std::to_string(nbytes) +
+                                                     " is not a multiple of block size 144");
+        if (element_count != nb * qk)
+            return fail(REALM_INVALID_ARGUMENT, "Element count mismatch: expected " +
+                                                    std::to_string(nb * qk) + ", got " +
+                                                    std::to_string(element_count));
+    } else if (nb * qk > element_count) {
+        return fail(REALM_INVALID_ARGUMENT, "element_count " + std::to_string(element_count) +
+                                                " is smaller than the " + std::to_string(nb) +
+                                                " blocks' output");
+    }
+    CHECK(ensure_init());
+    if (element_count > nb * qk)
+        std::memset(out + nb * qk, 0, (element_count - nb * qk) * sizeof(float));
+    if (nb == 0)
+        return REALM_OK;
+    hipStream_t s;
+    CHECK(thread_stream(&s));
+    void *raw, *dy;
+    CHECK(ws_get(s, WS_RAW, nb * bb, &raw));
+    CHECK(ws_get(s, WS_Y, nb * qk * 4, &dy));
+    HIP_TRY(hipMemcpyAsync(raw, data, nb * bb, hipMemcpyHostToDevice, s));
+    long long lnb = (long long)nb;
+    void *args[] = {&raw, &dy, &lnb};
+    size_t threads = nb * (type == GGML_Q4_K ? 128 : type == GGML_Q6_K ? 64 : 32);
+    CHECK(launch(std::string("realm_dequant_") + fmt_name(type),
+                 dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, args));
+    HIP_TRY(hipMemcpyAsync(out, dy, nb * qk * 4, hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipStreamSynchronize(s));
+    return REALM_OK;
+}
+
+REALM_API int realm_hip_weights_register(int type, const void *blocks, size_t nbytes, size_t n,
+                                         size_t k, uint64_t *handle)
+{
+    if (!handle)
+        return fail(REALM_INVALID_ARGUMENT, "handle is null");
+    if (type != GGML_Q4_K && type != GGML_Q6_K && type != GGML_Q8_0)
+        return fail(REALM_BACKEND_UNSUPPORTED,
+                    "ggml type " + std::to_string(type) + " is not supported by the HIP backend");
+    size_t qk = block_elems(type);
+    if (k == 0 || n == 0 || k % qk)
+        return fail(REALM_INVALID_ARGUMENT, "K dimension " + std::to_string(k) +
+                                                " must be a positive multiple of " +
+                                                std::to_string(qk));
+    if (nbytes != n * (k / qk) * block_bytes(type))
+        return fail(REALM_INVALID_ARGUMENT, "nbytes " + std::to_string(nbytes) +
+                                                " does not match n*k/" + std::to_string(qk) +
+                                                " blocks");
+    if (k > (size_t)INT32_MAX || n > (size_t)INT32_MAX)
+        return fail(REALM_INVALID_ARGUMENT, "dimension exceeds 2^31-1");
+    CHECK(ensure_init());
+    hipStream_t s;
+    CHECK(thread_stream(&s));
+    size_t off[3], kx;
+    size_t total = layout(type, n, k, off, &kx);
+    void *dev;
+    HIP_TRY(hipMalloc(&dev, total));
+    Weight w;
+    int rc = upload_repack(type, blocks, n, k, dev, &w, s);
+    if (rc == REALM_OK && hipStreamSynchronize(s) != hipSuccess)
+        rc = fail(REALM_GENERIC_FAILURE, "repack failed");
+    if (rc != REALM_OK) {
+        (void)hipFree(dev);
+        return rc;
+    }
+    w.dev = dev;
+    std::lock_guard<std::mutex> lk(g_mu);
+    uint64_t h = g_next_handle++;
+    g_weights[h] = w;
+    *handle = h;
+    return REALM_OK;
+}
+
+REALM_API int realm_hip_weights_release(uint64_t handle)
+{
+    void *dev = nullptr;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        auto it = g_weights.find(handle);
+        if (it == g_weights.end())
+            return fail(REALM_INVALID_ARGUMENT, "unknown weight handle " + std::to_string(handle));
+        dev = it->second.dev;
+        g_weights.erase(it);
+    }
+    HIP_TRY(hipDeviceSynchronize());
+    HIP_TRY(hipFree(dev));
+    return REALM_OK;
+}
+
+REALM_API int realm_hip_weights_info(uint64_t handle, int *type, size_t *n, size_t *k,
+                                     size_t *device_bytes)
+{
+    Weight w;
+    CHECK(get_weight(handle, &w));
+    if (type)
+        *type = w.type;
+    if (n)
+        *n = w.n;
+    if (k)
+        *k = w.k;
+    if (device_bytes)
+        *device_bytes = w.bytes;
+    return REALM_OK;
+}
+
+REALM_API int realm_hip_weights_matmul(uint64_t handle, const float *input, size_t batch,
+                                       float *out)
+{
+    Weight w;
+    CHECK(get_weight(handle, &w));
+    CHECK(ensure_init());
+    if (batch == 0)
+        return REALM_OK;
+    if (batch > (size_t)INT32_MAX)
+        return fail(REALM_INVALID_ARGUMENT, "batch exceeds 2^31-1");
+    hipStream_t s;
+    CHECK(thread_stream(&s));
+    void *dx, *dy;
+    CHECK(ws_get(s, WS_X, batch * w.k * 4, &dx));
+    CHECK(ws_get(s, WS_Y, batch * w.n * 4, &dy));
+    HIP_TRY(hipMemcpyAsync(dx, input, batch * w.k * 4, hipMemcpyHostToDevice, s));
+    CHECK(run_matmul(w, dx, false, batch, (float *)dy, s, nullptr));
+    HIP_TRY(hipMemcpyAsync(out, dy, batch * w.n * 4, hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipStreamSynchronize(s));
+    return REALM_OK;
+}
+
+REALM_API int realm_hip_weights_matmul_dev(uint64_t handle, const float *d_input, size_t batch,
+                                           float *d_out, void *stream)
+{
+    Weight w;
+    CHECK(get_weight(handle, &w));
+    CHECK(ensure_init());
+    if (batch > (size_t)INT32_MAX)
+        return fail(REALM_INVALID_ARGUMENT, "batch exceeds 2^31-1");
+    hipStream_t s;
+    CHECK(pick_stream(stream, &s));
+    return run_matmul(w, d_input, false, batch, d_out, s, nullptr);
+}
+
+REALM_API int realm_hip_weights_matmul_bf16_dev(uint64_t handle, const uint16_t *d_input,
+                                                size_t batch, float *d_out, void *stream)
+{
+    Weight w;
+    CHECK(get_weight(handle, &w));
+    CHECK(ensure_init());
+    if (batch > (size_t)INT32_MAX)
+        return fail(REALM_INVALID_ARGUMENT, "batch exceeds 2^31-1");
+    hipStream_t s;
+    CHECK(pick_stream(stream, &s));
+    return run_gemm(w, d_input, true, batch, d_out, s, nullptr);
+}
+
+REALM_API int realm_hip_lora_register(int dtype, const void *lora_a, const void *lora_b,
+                                      size_t rank, float alpha, size_t in_dim, size_t out_dim,
+                                      uint64_t *handle)
+{
+    if (!handle || !lora_a || !lora_b)
+        return fail(REALM_INVALID_ARGUMENT, "null pointer argument");
+    if (dtype != REALM_DTYPE_F32 && dtype != REALM_DTYPE_F16)
+        return fail(REALM_INVALID_ARGUMENT, "dtype must be REALM_DTYPE_F32 or REALM_DTYPE_F16");
+    if (rank == 0 || rank > 256)
+        return fail(REALM_INVALID_ARGUMENT, "rank must be 1..256");
+    if (in_dim == 0 || out_dim == 0 || in_dim > (size_t)INT32_MAX || out_dim > (size_t)INT32_MAX)
+        return fail(REALM_INVALID_ARGUMENT, "bad adapter dimensions");
+    CHECK(ensure_init());
+    size_t es = dtype == REALM_DTYPE_F16 ? 2 : 4;
+    size_t abytes = rank * in_dim * es, bbytes = out_dim * rank * es;
+    Adapter ad;
+    ad.dtype = dtype;
+    ad.rank = rank;
+    ad.alpha = alpha;
+    ad.in = in_dim;
+    ad.out = out_dim;
+    HIP_TRY(hipMalloc(&ad.a, abytes));
+    if (hipMalloc(&ad.b, bbytes) != hipSuccess) {
+        (void)hipFree(ad.a);
+        return fail(REALM_OUT_OF_MEMORY, "hipMalloc of LoRA B failed");
+    }
+    if (hipMemcpy(ad.a, lora_a, abytes, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(ad.b, lora_b, bbytes, hipMemcpyHostToDevice) != hipSuccess) {
+        (void)hipFree(ad.a);
+        (void)hipFree(ad.b);
+        return fail(REALM_GENERIC_FAILURE, "upload of LoRA factors failed");
+    }
+    std::lock_guard<std::mutex> lk(g_mu);
+    uint64_t h = g_next_handle++;
+    g_adapters[h] = ad;
+    *handle = h;
+    return REALM_OK;
+}
+
+REALM_API int realm_hip_lora_release(uint64_t handle)
+{
+    Adapter ad;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        auto it = g_adapters.find(handle);
+        if (it == g_adapters.end())
+            return fail(REALM_INVALID_ARGUMENT, "unknown adapter handle " + std::to_string(handle));
+        if (it->second.uses > 0)
+            return fail(REALM_INVALID_ARGUMENT, "adapter is still part of an adapter set");
+        ad = it->second;
+        g_adapters.erase(it);
+    }
+    HIP_TRY(hipDeviceSynchronize());
+    HIP_TRY(hipFree(ad.a));
+    HIP_TRY(hipFree(ad.b));
+    return REALM_OK;
+}
+
+REALM_API int realm_hip_lora_set_create(const uint64_t *lora_handles, size_t count,
+                                        uint64_t *set_handle)
+{
+    if (!set_handle || (!lora_handles && count))
+        return fail(REALM_INVALID_ARGUMENT, "null pointer argument");
+    if (count == 0 || count > 65535)
+        return fail(REALM_INVALID_ARGUMENT, "adapter set needs 1..65535 adapters");
+    CHECK(ensure_init());
+    std::vector<LoraEntry> table(count);
+    AdapterSet set;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        for (size_t i = 0; i < count; ++i) {
+            auto it = g_adapters.find(lora_handles[i]);
+            if (it == g_adapters.end())
+                return fail(REALM_INVALID_ARGUMENT,
+                            "unknown adapter handle " + std::to_string(lora_handles[i]));
+            const Adapter &ad = it->second;
+            if (i == 0) {
+                set.in = ad.in;
+                set.out = ad.out;
+            } else if (ad.in != set.in || ad.out != set.out) {
+                return fail(REALM_INVALID_ARGUMENT, "adapters of a set must share in/out dims");
+            }
+            table[i].a = ad.a;
+            table[i].b = ad.b;
+            table[i].rank = (int32_t)ad.rank;
+            table[i].dtype = ad.dtype;
+            table[i].scale = ad.alpha / (float)ad.rank; // lora.rs:49-52
+            table[i].pad = 0;
+            set.rmax = std::max(set.rmax, (int)ad.rank);
+        }
+        for (size_t i = 0; i < count; ++i)
+            g_adapters[lora_handles[i]].uses++;
+    }
+    set.count = count;
+    set.members.assign(lora_handles, lora_handles + count);
+    int rc = REALM_OK;
+    if (hipMalloc(&set.table, count * sizeof(LoraEntry)) != hipSuccess)
+        rc = fail(REALM_OUT_OF_MEMORY, "hipMalloc of adapter table failed");
+    else if (hipMemcpy(set.table, table.data(), count * sizeof(LoraEntry),
+                       hipMemcpyHostToDevice) != hipSuccess)
+        rc = fail(REALM_GENERIC_FAILURE, "upload of adapter table failed");
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (rc != REALM_OK) {
+        if (set.table)
+            (void)hipFree(set.table);
+        for (size_t i = 0; i < count; ++i)
+            g_adapters[lora_handles[i]].uses--;
+        return rc;
+    }
+    uint64_t h = g_next_handle++;
+    g_sets[h] = set;
+    *set_handle = h;
+    return REALM_OK;
+}
+
+REALM_API int realm_hip_lora_set_release(uint64_t set_handle)
+{
+    void *table;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        auto it = g_sets.find(set_handle);
+        if (it == g_sets.end())
+            return fail(REALM_INVALID_ARGUMENT, "unknown adapter set " + std::to_string(set_handle));
+        for (uint64_t m : it->second.members) {
+            auto a = g_adapters.find(m);
+            if (a != g_adapters.end())
+                a->second.uses--;
+        }
+        table = it->second.table;
+        g_sets.erase(it);
+    }
+    HIP_TRY(hipDeviceSynchronize());
+    HIP_TRY(hipFree(table));
+    return REALM_OK;
+}
+
+namespace {
+int lora_lookup(uint64_t wh, uint64_t sh, size_t batch, Weight *w, AdapterSet *set)
+{
+    CHECK(get_weight(wh, w));
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        auto it = g_sets.find(sh);
+        if (it == g_sets.end())
+            return fail(REALM_INVALID_ARGUMENT, "unknown adapter set " + std::to_string(sh));
+        *set = it->second;
+    }
+    if (set->in != w->k || set->out != w->n)
+        return fail(REALM_INVALID_ARGUMENT, "adapter set dims do not match the weight");
+    if (batch > 1024)
+        return fail(REALM_INVALID_ARGUMENT, "multi-LoRA batch is limited to 1024 tokens");
+    return REALM_OK;
+}
+} // namespace
+
+REALM_API int realm_hip_multi_lora_matmul_dev(uint64_t weight_handle, uint64_t set_handle,
+                                              const float *d_input, size_t batch,
+                                              const int32_t *d_adapter_ids, float *d_out,
+                                              void *stream)
+{
+    Weight w;
+    AdapterSet set;
+    CHECK(lora_lookup(weight_handle, set_handle, batch, &w, &set));
+    CHECK(ensure_init());
+    hipStream_t s;
+    CHECK(pick_stream(stream, &s));
+    LoraCall lc{&set, d_adapter_ids};
+    return run_gemm(w, d_input, false, batch, d_out, s, &lc);
+}
+
+REALM_API int realm_hip_multi_lora_matmul(uint64_t weight_handle, uint64_t set_handle,
+                                          const float *input, size_t batch,
+                                          const int32_t *adapter_ids, float *out)
+{
+    Weight w;
+    AdapterSet set;
+    CHECK(lora_lookup(weight_handle, set_handle, batch, &w, &set));
+    CHECK(ensure_init());
+    if (batch == 0)
+        return REALM_OK;
+    hipStream_t s;
+    CHECK(thread_stream(&s));
+    void *dx, *dy, *di;
+    CHECK(ws_get(s, WS_X, batch * w.k * 4, &dx));
+    CHECK(ws_get(s, WS_Y, batch * w.n * 4, &dy));
+    CHECK(ws_get(s, WS_IDS, batch * 4, &di));
+    HIP_TRY(hipMemcpyAsync(dx, input, batch * w.k * 4, hipMemcpyHostToDevice, s));
+    HIP_TRY(hipMemcpyAsync(di, adapter_ids, batch * 4, hipMemcpyHostToDevice, s));
+    LoraCall lc{&set, (const int32_t *)di};
+    CHECK(run_gemm(w, dx, false, batch, (float *)dy, s, &lc));
+    HIP_TRY(hipMemcpyAsync(out, dy, batch * w.n * 4, hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipStreamSynchronize(s));
+    return REALM_OK;
+}
+
+// ------------------------------------------------------------ HIP graphs
+
+namespace {
+std::unordered_map<uint64_t, hipGraphExec_t> g_graphs;
+}
+
+REALM_API int realm_hip_graph_begin(void *stream)
+{
+    if (!stream)
+        return fail(REALM_INVALID_ARGUMENT, "graph capture needs an explicit stream");
+    CHECK(ensure_init());
+    HIP_TRY(hipStreamBeginCapture((hipStream_t)stream, hipStreamCaptureModeThreadLocal));
+    return REALM_OK;
+}
+
+REALM_API int realm_hip_graph_end(void *stream, uint64_t *graph_handle)
+{
+    if (!stream || !graph_handle)
+        return fail(REALM_INVALID_ARGUMENT, "null argument");
+    hipGraph_t graph;
+    HIP_TRY(hipStreamEndCapture((hipStream_t)stream, &graph));
+    hipGraphExec_t exec;
+    hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (e != hipSuccess)
+        return fail(hip_code(e), std::string("hipGraphInstantiate: ") + hipGetErrorString(e));
+    std::lock_guard<std::mutex> lk(g_mu);
+    uint64_t h = g_next_handle++;
+    g_graphs[h] = exec;
+    *graph_handle = h;
+    return REALM_OK;
+}
+
+REALM_API int realm_hip_graph_launch(uint64_t graph_handle, void *stream)
+{
+    hipGraphExec_t exec;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        auto it = g_graphs.find(graph_handle);
+        if (it == g_graphs.end())
+            return fail(REALM_INVALID_ARGUMENT, "unknown graph " + std::to_string(graph_handle));
+        exec = it->second;
+    }
+    hipStream_t s;
+    CHECK(pick_stream(stream, &s));
+    HIP_TRY(hipGraphLaunch(exec, s));
+    return REALM_OK;
+}
+
+REALM_API int realm_hip_graph_release(uint64_t graph_handle)
+{
+    hipGraphExec_t exec;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        auto it = g_graphs.find(graph_handle);
+        if (it == g_graphs.end())
+            return fail(REALM_INVALID_ARGUMENT, "unknown graph " + std::to_string(graph_handle));
+        exec = it->second;
+        g_graphs.erase(it);
+    }
+    HIP_TRY(hipDeviceSynchronize());
+    HIP_TRY(hipGraphExecDestroy(exec));
+    return REALM_OK;
+}
+
+// ------------------------------------------------------------- plumbing
+
+REALM_API int realm_hip_malloc(void **d_ptr, size_t nbytes)
+{
+    CHECK(ensure_init());
+    HIP_TRY(hipMalloc(d_ptr, std::max<size_t>(nbytes, 1)));
+    return REALM_OK;
+}
+
+REALM_API int realm_hip_free(void *d_ptr)
+{
+    CHECK(ensure_init());
+    HIP_TRY(hipFree(d_ptr));
+    return REALM_OK;
+}
+
+REALM_API int realm_hip_memcpy_htod(void *d_dst, const void *h_src, size_t nbytes)
+{
+    CHECK(ensure_init());
+    HIP_TRY(hipMemcpy(d_dst, h_src, nbytes, hipMemcpyHostToDevice));
+    return REALM_OK;
+}
+
+REALM_API int realm_hip_memcpy_dtoh(void *h_dst, const void *d_src, size_t nbytes)
+{
+    CHECK(ensure_init());
+    HIP_TRY(hipMemcpy(h_dst, d_src, nbytes, hipMemcpyDeviceToHost));
+    return REALM_OK;
+}
+
+REALM_API int realm_hip_memcpy_dtod(void *d_dst, const void *d_src, size_t nbytes)
+{
+    CHECK(ensure_init());
+    HIP_TRY(hipMemcpy(d_dst, d_src, nbytes, hipMemcpyDeviceToDevice));
+    return REALM_OK;
+}
+
+REALM_API int realm_hip_stream(void **stream)
+{
+    CHECK(ensure_init());
+    hipStream_t s;
+    CHECK(thread_stream(&s));
+    *stream = s;
+    return REALM_OK;
+}
+
+REALM_API int realm_hip_stream_synchronize(void *stream)
+{
+    CHECK(ensure_init());
+    hipStream_t s;
+    CHECK(pick_stream(stream, &s));
+    HIP_TRY(hipStreamSynchronize(s));
+    return REALM_OK;
+}
+
+REALM_API int realm_hip_device_synchronize(void)
+{
+    CHECK(ensure_init());
+    HIP_TRY(hipDeviceSynchronize());
+    return REALM_OK;
+}
+
+REALM_API int realm_hip_event_create(void **event)
+{
+    CHECK(ensure_init());
+    hipEvent_t e;
+    HIP_TRY(hipEventCreate(&e));
+    *event = e;
+    return REALM_OK;
+}
+
+REALM_API int realm_hip_event_destroy(void *event)
+{
+    HIP_TRY(hipEventDestroy((hipEvent_t)event));
+    return REALM_OK;
+}
+
+REALM_API int realm_hip_event_record(void *event, void *stream)
+{
+    hipStream_t s;
+    CHECK(pick_stream(stream, &s));
+    HIP_TRY(hipEventRecord((hipEvent_t)event, s));
+    return REALM_OK;
+}
+
+REALM_API int realm_hip_event_elapsed_ms(void *start, void *stop, float *ms)
+{
+    HIP_TRY(hipEventSynchronize((hipEvent_t)stop));
+    HIP_TRY(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)stop));
+    return REALM_OK;
+}

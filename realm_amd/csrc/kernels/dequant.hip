@@ -1,0 +1,158 @@
+// Dequantization (bit-exact with the reference CPU dequantizer) and the
+// repack of reference-layout blocks into the device layout described in
+// common.h.  Both read the reference's packed blocks as raw bytes.
+#include "common.h"
+
+using namespace realm;
+
+// The reference never contracts `d1 * x - m1` into an FMA
+// (crates/realm-core/src/quant.rs:175,182); neither may we.
+#pragma clang fp contract(off)
+
+// quant.rs:127-187.  One thread per qs byte: 128 threads per block, two
+// outputs each (low nibble -> k = 64g + j, high nibble -> k = 64g + 32 + j).
+extern "C" __global__ __launch_bounds__(256) void realm_dequant_q4k(
+    const uint8_t *__restrict__ raw, float *__restrict__ out, long long nblocks)
+{
+    long long gid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    long long b = gid >> 7;
+    if (b >= nblocks)
+        return;
+    int byte = (int)(gid & 127);
+    int g = byte >> 5, j = byte & 31;
+    const uint8_t *blk = raw + b * Q4K_BLOCK_BYTES;
+    uint32_t dbits = blk[0] | (blk[1] << 8);
+    uint32_t mbits = blk[2] | (blk[3] << 8);
+    const uint8_t *s = blk + 4;
+    uint32_t s0 = s[0] | (s[1] << 8) | (s[2] << 16) | ((uint32_t)s[3] << 24);
+    uint32_t s1 = s[4] | (s[5] << 8) | (s[6] << 16) | ((uint32_t)s[7] << 24);
+    uint32_t s2 = s[8] | (s[9] << 8) | (s[10] << 16) | ((uint32_t)s[11] << 24);
+    uint32_t sc_lo, m_lo, sc_hi, m_hi;
+    q4k_scale_min_pair(s0, s1, s2, g, sc_lo, m_lo, sc_hi, m_hi);
+    float d = f16_bits_to_f32(dbits);
+    float dmin = f16_bits_to_f32(mbits);
+    float d1 = d * (float)sc_lo, m1 = dmin * (float)m_lo;
+    float d2 = d * (float)sc_hi, m2 = dmin * (float)m_hi;
+    uint32_t q = blk[16 + byte];
+    float *y = out + b * QK_K + 64 * g;
+    y[j] = d1 * (float)(q & 0xF) - m1;
+    y[32 + j] = d2 * (float)(q >> 4) - m2;
+}
+
+// quant.rs:393-451.  One thread per (block, half h, l): four outputs
+// y[128h + l + 32t] = (d * sc[8h + l/16 + 2t]) * q_t.
+extern "C" __global__ __launch_bounds__(256) void realm_dequant_q6k(
+    const uint8_t *__restrict__ raw, float *__restrict__ out, long long nblocks)
+{
+    long long gid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    long long b = gid >> 6;
+    if (b >= nblocks)
+        return;
+    int h = (int)((gid >> 5) & 1), l = (int)(gid & 31);
+    const uint8_t *blk = raw + b * Q6K_BLOCK_BYTES;
+    const uint8_t *ql = blk + 64 * h;
+    const uint8_t *qh = blk + 128 + 32 * h;
+    const int8_t *sc = reinterpret_cast<const int8_t *>(blk + 192) + 8 * h;
+    float d = f16_bits_to_f32(blk[208] | (blk[209] << 8));
+    int is = l >> 4;
+    uint32_t a = ql[l], bq = ql[l + 32], hb = qh[l];
+    int q1 = (int)((a & 0xF) | ((hb & 3) << 4)) - 32;
+    int q2 = (int)((bq & 0xF) | (((hb >> 2) & 3) << 4)) - 32;
+    int q3 = (int)((a >> 4) | (((hb >> 4) & 3) << 4)) - 32;
+    int q4 = (int)((bq >> 4) | (((hb >> 6) & 3) << 4)) - 32;
+    float *y = out + b * QK_K + 128 * h + l;
+    y[0] = d * (float)sc[is] * (float)q1;
+    y[32] = d * (float)sc[is + 2] * (float)q2;
+    y[64] = d * (float)sc[is + 4] * (float)q3;
+    y[96] = d * (float)sc[is + 6] * (float)q4;
+}
+
+// quant.rs:371-387: y = q * d, one thread per element.
+extern "C" __global__ __launch_bounds__(256) void realm_dequant_q80(
+    const uint8_t *__restrict__ raw, float *__restrict__ out, long long nblocks)
+{
+    long long gid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    long long b = gid >> 5;
+    if (b >= nblocks)
+        return;
+    int i = (int)(gid & 31);
+    const uint8_t *blk = raw + b * Q80_BLOCK_BYTES;
+    float d = f16_bits_to_f32(blk[0] | (blk[1] << 8));
+    out[gid] = (float)(int8_t)blk[2 + i] * d;
+}
+
+// ------------------------------------------------------------------ repack
+
+// Q4_K: a 144-byte block is nine 16-byte pieces (the raw buffer is 256-byte
+// aligned and 144 = 9*16): piece 0 -> hdr, pieces 1..8 -> qs.
+extern "C" __global__ __launch_bounds__(256) void realm_repack_q4k(
+    const uint8_t *__restrict__ raw, uint8_t *__restrict__ hdr, uint8_t *__restrict__ qs,
+    long long nblocks)
+{
+    long long gid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    long long b = gid / 9;
+    if (b >= nblocks)
+        return;
+    int piece = (int)(gid - b * 9);
+    uint4 v = ldg16(raw + b * Q4K_BLOCK_BYTES + 16 * piece);
+    if (piece == 0)
+        *reinterpret_cast<uint4 *>(hdr + b * 16) = v;
+    else
+        *reinterpret_cast<uint4 *>(qs + b * 128 + 16 * (piece - 1)) = v;
+}
+
+// Q6_K: 64 threads per block.  Thread t writes quant bytes t, t+64, t+128 of
+// the block's 192 regrouped bytes, threads 0..15 the regrouped scales and
+// thread 0 the f16 scale.
+extern "C" __global__ __launch_bounds__(256) void realm_repack_q6k(
+    const uint8_t *__restrict__ raw, uint8_t *__restrict__ dq, int8_t *__restrict__ scq,
+    uint8_t *__restrict__ qq, long long nblocks)
+{
+    long long gid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    long long b = gid >> 6;
+    if (b >= nblocks)
+        return;
+    int t = (int)(gid & 63);
+    const uint8_t *blk = raw + b * Q6K_BLOCK_BYTES;
+    for (int o = t; o < 192; o += 64) {
+        int v = o / 48, r = o - 48 * v;       // unit v, byte r of its 48
+        int h = v >> 1, is = v & 1;
+        uint8_t val;
+        if (r < 16)
+            val = blk[64 * h + 16 * is + r];          // ql_a
+        else if (r < 32)
+            val = blk[64 * h + 32 + 16 * is + (r - 16)]; // ql_b
+        else
+            val = blk[128 + 32 * h + 16 * is + (r - 32)]; // qh
+        qq[b * 192 + o] = val;
+    }
+    if (t < 16) {
+        int v = t >> 2, tt = t & 3;
+        int h = v >> 1, is = v & 1;
+        scq[b * 16 + t] = (int8_t)blk[192 + 8 * h + is + 2 * tt];
+    }
+    if (t == 0) {
+        dq[2 * b] = blk[208];
+        dq[2 * b + 1] = blk[209];
+    }
+}
+
+// Q8_0: one thread per quant byte.  Block (row n, kb) goes to row n of the
+// padded [N][Kp] layout; the destination is zeroed beforehand so the padding
+// holds zero quants and zero scales.
+extern "C" __global__ __launch_bounds__(256) void realm_repack_q80(
+    const uint8_t *__restrict__ raw, uint8_t *__restrict__ dq, int8_t *__restrict__ qq,
+    long long nblocks, int kb_per_row, int kp)
+{
+    long long gid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    long long b = gid >> 5;
+    if (b >= nblocks)
+        return;
+    int i = (int)(gid & 31);
+    long long n = b / kb_per_row;
+    int kb = (int)(b - n * kb_per_row);
+    const uint8_t *blk = raw + b * Q80_BLOCK_BYTES;
+    qq[n * kp + 32 * kb + i] = (int8_t)blk[2 + i];
+    if (i < 2)
+        dq[(n * (kp / 32) + kb) * 2 + i] = blk[i];
+}

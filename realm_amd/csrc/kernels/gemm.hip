@@ -1,0 +1,622 @@
+// Batched decode (M >= 2) and prefill: Y[t, n] = sum_k X[t,k] W[n,k] on MFMA
+// (v_mfma_f32_16x16x32_f16, f32 accumulate) for resident Q4_K / Q6_K / Q8_0
+// weights, plus the multi-LoRA shrink and the fused LoRA expand epilogue.
+//
+// Exactness: every MFMA operand is exact in f16.
+//  * Activations: xprep rescales each token by an exact power of two 2^-e_t
+//    (max |x| lands in [512, 1024)) and splits it into f16 hi + lo parts
+//    (lo = 0 for bf16 input, which is exact in f16 after the rescale).  The
+//    output is multiplied back by 2^e_t.
+//  * Q4_K weights: sc*q with sc <= 63, q <= 15 (<= 945 < 2^11); per 256-block
+//    the MFMA sum is scaled by d, and the min term dmin * sum_s m_s Sx_s runs
+//    as one extra MFMA whose K slots hold (Sx hi, Sx lo) against (m, m).
+//  * Q6_K weights: (q-32)*sc when every |sc| <= 63 (<= 2016 < 2^11); otherwise
+//    sc = 16*sh + sl and two exact operands (q-32)*sl and (q-32)*16*sh.
+//  * Q8_0 weights: q itself; each 32-block's MFMA sum is scaled by d.
+//
+// MFMA roles: A = activations (16 tokens x 32 k), B = weights (32 k x 16
+// rows), D[token][row].  Lane l supplies A[l%16][kslot(l/16, e)] and
+// B[kslot(l/16, e)][l%16]; the k slots of a lane group c = l/16 are chosen
+// per format so that a lane reads contiguous weight bytes of its own row, and
+// xprep writes activations in exactly that slot order.  D lane l holds rows
+// 4(l/16)+v (tokens) of column l%16 (a row n), so each lane scales its own
+// row's results with the block scale it decoded itself.
+#include "common.h"
+#include "kernel_args.h"
+
+using namespace realm;
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+#define FMT_Q4K 0
+#define FMT_Q6K 1
+#define FMT_Q80 2
+
+namespace {
+
+// Slot order inside an 8-slot group: nibble/byte pairs (0,2),(1,3),(4,6),(5,7)
+// come out of one mask each, so slot e holds element PI[e] of its window.
+REALM_DEV int pi8(int e) { return (e & 4) | ((e & 1) << 1) | ((e >> 1) & 1); }
+
+// Start (8-aligned) of the k window behind position group pg = p/8.
+template <int FMT>
+REALM_DEV int kwin(int pg)
+{
+    if (FMT == FMT_Q80)
+        return 8 * pg;
+    int b = pg >> 5, i = (pg >> 2) & 7, c = pg & 3;
+    if (FMT == FMT_Q4K)
+        return 256 * b + 64 * c + 32 * (i >> 2) + 8 * (i & 3);
+    return 256 * b + 128 * (c >> 1) + 16 * (c & 1) + 32 * (i >> 1) + 8 * (i & 1);
+}
+
+REALM_DEV half2_t h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
+REALM_DEV uint32_t u32(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
+REALM_DEV half8_t h8(uint32_t a, uint32_t b, uint32_t c, uint32_t d)
+{
+    uint4 v = make_uint4(a, b, c, d);
+    return __builtin_bit_cast(half8_t, v);
+}
+REALM_DEV half8_t ld_h8(const _Float16 *p) { return __builtin_bit_cast(half8_t, ldg16(p)); }
+REALM_DEV half2_t splat2(float v)
+{
+    _Float16 h = (_Float16)v;
+    half2_t r = {h, h};
+    return r;
+}
+
+REALM_DEV floatx4 mfma(half8_t a, half8_t b, floatx4 c)
+{
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+REALM_DEV float load_x(const void *x, int bf16, size_t i)
+{
+    if (bf16)
+        return __uint_as_float((uint32_t)reinterpret_cast<const uint16_t *>(x)[i] << 16);
+    return reinterpret_cast<const float *>(x)[i];
+}
+
+} // namespace
+
+// ------------------------------------------------------------------ xprep
+//
+// One workgroup per (padded) token.  Writes, for token t:
+//   xh[t][p], xl[t][p]  f16 hi/lo of x[t][k(p)] * 2^-e_t, p in [0, KX)
+//   xm[t][b][c][8]      Q4_K only: (Sxh(2c), Sxh(2c+1), Sxl(2c), Sxl(2c+1), 0...)
+//   tscale[t] = 2^e_t
+// Tokens t >= M get zeros.
+template <int FMT>
+REALM_DEV void xprep(const void *__restrict__ x, int bf16, _Float16 *__restrict__ xh,
+                     _Float16 *__restrict__ xl, _Float16 *__restrict__ xm,
+                     float *__restrict__ tscale, int M, int K, int KX)
+{
+    __shared__ float red[4];
+    const int t = blockIdx.x;
+    const bool live = t < M;
+    const size_t xrow = (size_t)t * K;
+    float amax = 0.f;
+    if (live)
+        for (int k = threadIdx.x; k < K; k += blockDim.x)
+            amax = fmaxf(amax, fabsf(load_x(x, bf16, xrow + k)));
+    for (int off = 32; off > 0; off >>= 1)
+        amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+    if ((threadIdx.x & 63) == 0)
+        red[threadIdx.x >> 6] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    int e = 0;
+    if (amax > 0.f && __builtin_isfinite(amax)) {
+        int ex;
+        frexpf(amax, &ex); // amax = m * 2^ex, m in [0.5, 1)
+        e = ex - 10;
+    }
+    const float down = ldexpf(1.f, -e);
+    if (threadIdx.x == 0)
+        tscale[t] = ldexpf(1.f, e);
+
+    const size_t orow = (size_t)t * KX;
+    for (int pg = threadIdx.x; pg < KX / 8; pg += blockDim.x) {
+        int k0 = kwin<FMT>(pg);
+        _Float16 hv[8], lv[8];
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            int k = k0 + pi8(s);
+            float v = (live && k < K) ? load_x(x, bf16, xrow + k) * down : 0.f;
+            _Float16 h = (_Float16)v;
+            hv[s] = h;
+            lv[s] = (_Float16)(v - (float)h);
+        }
+        *reinterpret_cast<uint4 *>(xh + orow + 8 * pg) = __builtin_bit_cast(uint4, hv);
+        if (xl)
+            *reinterpret_cast<uint4 *>(xl + orow + 8 * pg) = __builtin_bit_cast(uint4, lv);
+    }
+    if (FMT == FMT_Q4K) {
+        const int B = K >> 8;
+        for (int bc = threadIdx.x; bc < B * 4; bc += blockDim.x) {
+            int b = bc >> 2, c = bc & 3;
+            float s[2] = {0.f, 0.f};
+            if (live)
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    size_t k0 = xrow + 256 * b + 64 * c + 32 * h;
+                    float acc = 0.f;
+                    for (int j = 0; j < 32; ++j)
+                        acc += load_x(x, bf16, k0 + j) * down;
+                    s[h] = acc;
+                }
+            _Float16 h0 = (_Float16)s[0], h1 = (_Float16)s[1];
+            _Float16 v[8] = {h0, h1, (_Float16)(s[0] - (float)h0), (_Float16)(s[1] - (float)h1),
+                             (_Float16)0.f, (_Float16)0.f, (_Float16)0.f, (_Float16)0.f};
+            *reinterpret_cast<uint4 *>(xm + ((size_t)t * B + b) * 32 + 8 * c) =
+                __builtin_bit_cast(uint4, v);
+        }
+    }
+}
+
+#define DEF_XPREP(NAME, FMT)                                                               \
+    extern "C" __global__ __launch_bounds__(256) void realm_xprep_##NAME(                 \
+        const void *x, int bf16, _Float16 *xh, _Float16 *xl, _Float16 *xm, float *tscale, \
+        int M, int K, int KX)                                                              \
+    {                                                                                      \
+        xprep<FMT>(x, bf16, xh, xl, xm, tscale, M, K, KX);                                 \
+    }
+DEF_XPREP(q4k, FMT_Q4K)
+DEF_XPREP(q6k, FMT_Q6K)
+DEF_XPREP(q80, FMT_Q80)
+
+// --------------------------------------------------------- LoRA adapter table
+
+REALM_DEV float lora_elem(const void *p, int dtype, size_t i)
+{
+    if (dtype)
+        return (float)reinterpret_cast<const _Float16 *>(p)[i];
+    return reinterpret_cast<const float *>(p)[i];
+}
+
+// ------------------------------------------------------------- main kernel
+
+template <int FMT, int TN, int TM, int KSPLIT, bool LO, bool WIDE, bool LORA>
+REALM_DEV void gemm_body(const GemmArgs &g)
+{
+    constexpr int WN = 4 / KSPLIT; // waves along rows
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wn = wave / KSPLIT, wk = wave % KSPLIT;
+    const int r16 = lane & 15, c = lane >> 4;
+    const int n0 = blockIdx.x * (WN * 16 * TN) + wn * 16 * TN;
+    const int t0 = blockIdx.y * (16 * TM);
+    const int K = g.K, KX = g.KX, N = g.N;
+
+    floatx4 acc[TN][TM];
+#pragma unroll
+    for (int a = 0; a < TN; ++a)
+#pragma unroll
+        for (int b = 0; b < TM; ++b)
+            acc[a][b] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    // activation row pointers for this lane's token in each token tile
+    const _Float16 *xrow_h[TM];
+    const _Float16 *xrow_l[TM];
+#pragma unroll
+    for (int b = 0; b < TM; ++b) {
+        size_t tok = (size_t)(t0 + 16 * b + r16);
+        xrow_h[b] = (const _Float16 *)g.xh + tok * KX + 8 * c;
+        xrow_l[b] = LO ? (const _Float16 *)g.xl + tok * KX + 8 * c : nullptr;
+    }
+
+    if (FMT == FMT_Q4K) {
+        const int B = K >> 8;
+        const uint8_t *hdr = (const uint8_t *)g.w0, *qs = (const uint8_t *)g.w1;
+        for (int b = wk; b < B; b += KSPLIT) {
+            uint32_t w[TN][8];
+            float d[TN], dm[TN];
+            half2_t sc2[TN][2], cc2[TN][2];
+            uint32_t mfrag[TN];
+#pragma unroll
+            for (int a = 0; a < TN; ++a) {
+                int row = n0 + 16 * a + r16;
+                uint4 q0 = make_uint4(0, 0, 0, 0), q1 = q0, hd = q0;
+                if (row < N) {
+                    const uint8_t *qp = qs + (size_t)row * (K >> 1) + 128 * b + 32 * c;
+                    q0 = ldg16(qp);
+                    q1 = ldg16(qp + 16);
+                    hd = ldg16(hdr + ((size_t)row * B + b) * 16);
+                }
+                w[a][0] = q0.x; w[a][1] = q0.y; w[a][2] = q0.z; w[a][3] = q0.w;
+                w[a][4] = q1.x; w[a][5] = q1.y; w[a][6] = q1.z; w[a][7] = q1.w;
+                d[a] = fix_scale(f16_bits_to_f32(hd.x), 0.00000006f, g.nan_fb);
+                dm[a] = fix_scale(f16_bits_to_f32(hd.x >> 16), 0.00000024f, g.nan_fb);
+                // scale/min pair of sub-blocks 2c (low nibbles) and 2c+1 (high)
+                int sh = 16 * (c & 1);
+                uint32_t a0 = hd.y >> sh, a1 = hd.z >> sh, a2 = hd.w >> sh;
+                uint32_t sl, ml, shh, mh;
+                if (c < 2) {
+                    sl = a0 & 63u; ml = a1 & 63u;
+                    shh = (a0 >> 8) & 63u; mh = (a1 >> 8) & 63u;
+                } else {
+                    sl = (a2 & 0xFu) | (((a0 >> 6) & 3u) << 4);
+                    ml = ((a2 >> 4) & 0xFu) | (((a1 >> 6) & 3u) << 4);
+                    shh = ((a2 >> 8) & 0xFu) | (((a0 >> 14) & 3u) << 4);
+                    mh = ((a2 >> 12) & 0xFu) | (((a1 >> 14) & 3u) << 4);
+                }
+                sc2[a][0] = splat2((float)sl);
+                cc2[a][0] = splat2(-1024.f * (float)sl);
+                sc2[a][1] = splat2((float)shh);
+                cc2[a][1] = splat2(-1024.f * (float)shh);
+                half2_t mm = {(_Float16)(float)ml, (_Float16)(float)mh};
+                mfrag[a] = u32(mm);
+            }
+            floatx4 P[TN][TM];
+#pragma unroll
+            for (int a = 0; a < TN; ++a)
+#pragma unroll
+                for (int bb = 0; bb < TM; ++bb)
+                    P[a][bb] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                half8_t ah[TM], al[TM];
+#pragma unroll
+                for (int bb = 0; bb < TM; ++bb) {
+                    ah[bb] = ld_h8(xrow_h[bb] + 256 * b + 32 * i);
+                    if (LO)
+                        al[bb] = ld_h8(xrow_l[bb] + 256 * b + 32 * i);
+                }
+#pragma unroll
+                for (int a = 0; a < TN; ++a) {
+                    const int ch = i & 3, hi = i >> 2, shf = 4 * hi;
+                    uint32_t wa = w[a][2 * ch], wb = w[a][2 * ch + 1];
+                    uint32_t p0 = ((wa >> shf) & 0x000F000Fu) | 0x64006400u;
+                    uint32_t p1 = ((wa >> (shf + 8)) & 0x000F000Fu) | 0x64006400u;
+                    uint32_t p2 = ((wb >> shf) & 0x000F000Fu) | 0x64006400u;
+                    uint32_t p3 = ((wb >> (shf + 8)) & 0x000F000Fu) | 0x64006400u;
+                    half2_t s2 = sc2[a][hi], k2 = cc2[a][hi];
+                    half8_t bf = h8(u32(__builtin_elementwise_fma(h2(p0), s2, k2)),
+                                    u32(__builtin_elementwise_fma(h2(p1), s2, k2)),
+                                    u32(__builtin_elementwise_fma(h2(p2), s2, k2)),
+                                    u32(__builtin_elementwise_fma(h2(p3), s2, k2)));
+#pragma unroll
+                    for (int bb = 0; bb < TM; ++bb) {
+                        P[a][bb] = mfma(ah[bb], bf, P[a][bb]);
+                        if (LO)
+                            P[a][bb] = mfma(al[bb], bf, P[a][bb]);
+                    }
+                }
+            }
+            // min term: one MFMA on (Sx hi, Sx lo) x (m, m) slots
+#pragma unroll
+            for (int bb = 0; bb < TM; ++bb) {
+                size_t tok = (size_t)(t0 + 16 * bb + r16);
+                half8_t am = ld_h8((const _Float16 *)g.xm + (tok * B + b) * 32 + 8 * c);
+#pragma unroll
+                for (int a = 0; a < TN; ++a) {
+                    half8_t bm = h8(mfrag[a], mfrag[a], 0u, 0u);
+                    floatx4 Q = mfma(am, bm, floatx4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+                    for (int v = 0; v < 4; ++v)
+                        acc[a][bb][v] += d[a] * P[a][bb][v] - dm[a] * Q[v];
+                }
+            }
+        }
+    } else if (FMT == FMT_Q6K) {
+        const int B = K >> 8;
+        const uint8_t *dq = (const uint8_t *)g.w0;
+        const int8_t *scq = (const int8_t *)g.w1;
+        const uint8_t *qq = (const uint8_t *)g.w2;
+        for (int b = wk; b < B; b += KSPLIT) {
+            uint32_t qa[TN][4], qb[TN][4], qh[TN][4];
+            float d[TN];
+            half2_t s2[TN][4], s2h[TN][4];
+#pragma unroll
+            for (int a = 0; a < TN; ++a) {
+                int row = n0 + 16 * a + r16;
+                uint4 A = make_uint4(0, 0, 0, 0), Bq = A, H = A;
+                uint32_t scw = 0, dbits = 0;
+                if (row < N) {
+                    size_t blk = (size_t)row * B + b;
+                    const uint8_t *qp = qq + (blk * 4 + c) * 48;
+                    A = ldg16(qp);
+                    Bq = ldg16(qp + 16);
+                    H = ldg16(qp + 32);
+                    scw = ldg4(scq + blk * 16 + 4 * c);
+                    dbits = *reinterpret_cast<const uint16_t *>(dq + blk * 2);
+                }
+                qa[a][0] = A.x; qa[a][1] = A.y; qa[a][2] = A.z; qa[a][3] = A.w;
+                qb[a][0] = Bq.x; qb[a][1] = Bq.y; qb[a][2] = Bq.z; qb[a][3] = Bq.w;
+                qh[a][0] = H.x; qh[a][1] = H.y; qh[a][2] = H.z; qh[a][3] = H.w;
+                d[a] = fix_scale(f16_bits_to_f32(dbits), 0.00000006f, g.nan_fb);
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    int sc = (int)(int8_t)(scw >> (8 * t));
+                    if (WIDE) {
+                        s2[a][t] = splat2((float)(sc & 15));
+                        s2h[a][t] = splat2(16.f * (float)(sc >> 4));
+                    } else {
+                        s2[a][t] = splat2((float)sc);
+                    }
+                }
+            }
+            floatx4 P[TN][TM];
+#pragma unroll
+            for (int a = 0; a < TN; ++a)
+#pragma unroll
+                for (int bb = 0; bb < TM; ++bb)
+                    P[a][bb] = floatx4{0.f, 0.f, 0.f, 0.f};
+            const half2_t off2 = splat2(-1056.f);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int t = i >> 1, jh = i & 1;
+                half8_t ah[TM], al[TM];
+#pragma unroll
+                for (int bb = 0; bb < TM; ++bb) {
+                    ah[bb] = ld_h8(xrow_h[bb] + 256 * b + 32 * i);
+                    if (LO)
+                        al[bb] = ld_h8(xrow_l[bb] + 256 * b + 32 * i);
+                }
+#pragma unroll
+                for (int a = 0; a < TN; ++a) {
+                    uint32_t v[2];
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        uint32_t src = (t & 1) ? qb[a][2 * jh + h] : qa[a][2 * jh + h];
+                        uint32_t lo4 = (src >> ((t & 2) ? 4 : 0)) & 0x0F0F0F0Fu;
+                        uint32_t hi2 = ((qh[a][2 * jh + h] >> (2 * t)) & 0x03030303u) << 4;
+                        v[h] = lo4 | hi2;
+                    }
+                    half2_t q0 = h2((v[0] & 0x00FF00FFu) | 0x64006400u) + off2;
+                    half2_t q1 = h2(((v[0] >> 8) & 0x00FF00FFu) | 0x64006400u) + off2;
+                    half2_t q2 = h2((v[1] & 0x00FF00FFu) | 0x64006400u) + off2;
+                    half2_t q3 = h2(((v[1] >> 8) & 0x00FF00FFu) | 0x64006400u) + off2;
+                    half2_t s = s2[a][t];
+                    half8_t bf = h8(u32(q0 * s), u32(q1 * s), u32(q2 * s), u32(q3 * s));
+                    half8_t bh;
+                    if (WIDE) {
+                        half2_t sh = s2h[a][t];
+                        bh = h8(u32(q0 * sh), u32(q1 * sh), u32(q2 * sh), u32(q3 * sh));
+                    }
+#pragma unroll
+                    for (int bb = 0; bb < TM; ++bb) {
+                        P[a][bb] = mfma(ah[bb], bf, P[a][bb]);
+                        if (LO)
+                            P[a][bb] = mfma(al[bb], bf, P[a][bb]);
+                        if (WIDE) {
+                            P[a][bb] = mfma(ah[bb], bh, P[a][bb]);
+                            if (LO)
+                                P[a][bb] = mfma(al[bb], bh, P[a][bb]);
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (int a = 0; a < TN; ++a)
+#pragma unroll
+                for (int bb = 0; bb < TM; ++bb)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v)
+                        acc[a][bb][v] += d[a] * P[a][bb][v];
+        }
+    } else { // Q8_0
+        const int B32 = KX >> 5;
+        const uint8_t *dq = (const uint8_t *)g.w0;
+        const int8_t *qq = (const int8_t *)g.w1;
+        const half2_t off2 = splat2(-1152.f);
+        for (int kb = wk; kb < B32; kb += KSPLIT) {
+            half8_t ah[TM], al[TM];
+#pragma unroll
+            for (int bb = 0; bb < TM; ++bb) {
+                ah[bb] = ld_h8(xrow_h[bb] + 32 * kb);
+                if (LO)
+                    al[bb] = ld_h8(xrow_l[bb] + 32 * kb);
+            }
+#pragma unroll
+            for (int a = 0; a < TN; ++a) {
+                int row = n0 + 16 * a + r16;
+                uint2 q = make_uint2(0, 0);
+                uint32_t dbits = 0;
+                if (row < N) {
+                    q = ldg8(qq + (size_t)row * KX + 32 * kb + 8 * c);
+                    dbits = *reinterpret_cast<const uint16_t *>(dq + ((size_t)row * B32 + kb) * 2);
+                }
+                float d = f16_bits_to_f32(dbits);
+                uint32_t ua = q.x ^ 0x80808080u, ub = q.y ^ 0x80808080u;
+                half2_t q0 = h2((ua & 0x00FF00FFu) | 0x64006400u) + off2;
+                half2_t q1 = h2(((ua >> 8) & 0x00FF00FFu) | 0x64006400u) + off2;
+                half2_t q2 = h2((ub & 0x00FF00FFu) | 0x64006400u) + off2;
+                half2_t q3 = h2(((ub >> 8) & 0x00FF00FFu) | 0x64006400u) + off2;
+                half8_t bf = h8(u32(q0), u32(q1), u32(q2), u32(q3));
+#pragma unroll
+                for (int bb = 0; bb < TM; ++bb) {
+                    floatx4 P = mfma(ah[bb], bf, floatx4{0.f, 0.f, 0.f, 0.f});
+                    if (LO)
+                        P = mfma(al[bb], bf, P);
+#pragma unroll
+                    for (int v = 0; v < 4; ++v)
+                        acc[a][bb][v] += d * P[v];
+                }
+            }
+        }
+    }
+
+    // ---- reduce the KSPLIT partial sums through LDS
+    if (KSPLIT > 1) {
+        __shared__ float red[4][TN * TM * 4][64];
+        if (wk != 0)
+#pragma unroll
+            for (int a = 0; a < TN; ++a)
+#pragma unroll
+                for (int bb = 0; bb < TM; ++bb)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v)
+                        red[wave][(a * TM + bb) * 4 + v][lane] = acc[a][bb][v];
+        __syncthreads();
+        if (wk != 0)
+            return;
+#pragma unroll
+        for (int s = 1; s < KSPLIT; ++s)
+#pragma unroll
+            for (int a = 0; a < TN; ++a)
+#pragma unroll
+                for (int bb = 0; bb < TM; ++bb)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v)
+                        acc[a][bb][v] += red[wave + s][(a * TM + bb) * 4 + v][lane];
+    }
+
+    // ---- epilogue: undo the token rescale, add the LoRA expand, store
+#pragma unroll
+    for (int bb = 0; bb < TM; ++bb)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            int tok = t0 + 16 * bb + 4 * c + v;
+            if (tok >= g.M)
+                continue;
+            float ts = g.tscale[tok];
+            int aid = -1;
+            LoraEntry ent;
+            if (LORA) {
+                aid = g.ids[tok];
+                if (aid >= 0 && aid < g.n_adapters)
+                    ent = g.table[aid];
+                else
+                    aid = -1;
+            }
+#pragma unroll
+            for (int a = 0; a < TN; ++a) {
+                int row = n0 + 16 * a + r16;
+                if (row >= N)
+                    continue;
+                float out = acc[a][bb][v] * ts;
+                if (LORA && aid >= 0) {
+                    const float *ut = g.u + (size_t)tok * g.rmax;
+                    float s = 0.f;
+                    for (int j = 0; j < ent.rank; ++j)
+                        s += lora_elem(ent.b, ent.dtype, (size_t)row * ent.rank + j) * ut[j];
+                    out += ent.scale * s;
+                }
+                g.y[(size_t)tok * N + row] = out;
+            }
+        }
+}
+
+#define GEMM_KERNEL(NAME, FMT, TN, TM, KS, LO, WIDE, LORA)                                \
+    extern "C" __global__ __launch_bounds__(256) void realm_gemm_##NAME(GemmArgs g)       \
+    {                                                                                     \
+        gemm_body<FMT, TN, TM, KS, LO, WIDE, LORA>(g);                                    \
+    }
+
+// Instantiation set: (TN, TM, KSPLIT) tiles for decode (KSPLIT 4, TN 1) and
+// prefill (KSPLIT 1, TN 2); LO = f32 activations; Q6_K narrow/wide scales.
+#define GEMM_TILES(FNAME, FMT, WIDE, LORA, SUF)                                           \
+    GEMM_KERNEL(FNAME##_d1_f32##SUF, FMT, 1, 1, 4, true, WIDE, LORA)                      \
+    GEMM_KERNEL(FNAME##_d2_f32##SUF, FMT, 1, 2, 4, true, WIDE, LORA)                      \
+    GEMM_KERNEL(FNAME##_d4_f32##SUF, FMT, 1, 4, 4, true, WIDE, LORA)                      \
+    GEMM_KERNEL(FNAME##_p4_f32##SUF, FMT, 2, 4, 1, true, WIDE, LORA)                      \
+    GEMM_KERNEL(FNAME##_d1_bf16##SUF, FMT, 1, 1, 4, false, WIDE, LORA)                    \
+    GEMM_KERNEL(FNAME##_d4_bf16##SUF, FMT, 1, 4, 4, false, WIDE, LORA)                    \
+    GEMM_KERNEL(FNAME##_p4_bf16##SUF, FMT, 2, 4, 1, false, WIDE, LORA)
+
+GEMM_TILES(q4k, FMT_Q4K, false, false, )
+GEMM_TILES(q6k, FMT_Q6K, false, false, )
+GEMM_TILES(q6kw, FMT_Q6K, true, false, )
+GEMM_TILES(q80, FMT_Q80, false, false, )
+GEMM_TILES(q4k, FMT_Q4K, false, true, _lora)
+GEMM_TILES(q6k, FMT_Q6K, false, true, _lora)
+GEMM_TILES(q6kw, FMT_Q6K, true, true, _lora)
+GEMM_TILES(q80, FMT_Q80, false, true, _lora)
+
+// ------------------------------------------------------------ LoRA shrink
+//
+// u[t][j] = sum_k A_a[j][k] x[t][k] for the tokens t whose adapter is a,
+// j < rank_a.  Grid (adapter, 16-row chunk of A, 16-token chunk of the
+// adapter's tokens); the four waves split K and meet in LDS.  Activations are
+// the xprep fragments of the base matmul (same slot order), adapter rows are
+// read at the matching k and split into f16 hi/lo (exact for f16 adapters,
+// whose lo part is zero).
+template <int FMT, bool LO>
+REALM_DEV void lora_shrink(const _Float16 *__restrict__ xh, const _Float16 *__restrict__ xl,
+                           const float *__restrict__ tscale, const int *__restrict__ ids,
+                           const LoraEntry *__restrict__ table, float *__restrict__ u, int M,
+                           int K, int KX, int rmax)
+{
+    __shared__ int toks[1024];
+    __shared__ int count;
+    __shared__ float red[4][4][64];
+    const int a = blockIdx.x;
+    if (threadIdx.x == 0) {
+        int n = 0;
+        for (int t = 0; t < M; ++t)
+            if (ids[t] == a && n < 1024)
+                toks[n++] = t;
+        count = n;
+    }
+    __syncthreads();
+    const LoraEntry e = table[a];
+    const int jc = blockIdx.y * 16, tc = blockIdx.z * 16;
+    if (tc >= count || jc >= e.rank)
+        return;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int r16 = lane & 15, c = lane >> 4;
+    const int ti = tc + r16;
+    const int tok = ti < count ? toks[ti] : -1;
+    const int j = jc + r16;
+    floatx4 P = {0.f, 0.f, 0.f, 0.f};
+    const int steps = KX / 32;
+    for (int s = wave; s < steps; s += 4) {
+        half8_t ah = {}, al = {};
+        if (tok >= 0) {
+            ah = ld_h8(xh + (size_t)tok * KX + 32 * s + 8 * c);
+            if (LO)
+                al = ld_h8(xl + (size_t)tok * KX + 32 * s + 8 * c);
+        }
+        int k0 = kwin<FMT>(4 * s + c);
+        half8_t bh = {}, bl = {};
+        if (j < e.rank) {
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                int k = k0 + pi8(q);
+                float v = k < K ? lora_elem(e.a, e.dtype, (size_t)j * K + k) : 0.f;
+                _Float16 h = (_Float16)v;
+                bh[q] = h;
+                bl[q] = (_Float16)(v - (float)h);
+            }
+        }
+        P = mfma(ah, bh, P);
+        P = mfma(ah, bl, P);
+        if (LO)
+            P = mfma(al, bh, P);
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+        red[wave][v][lane] = P[v];
+    __syncthreads();
+    if (wave != 0)
+        return;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        float s = red[0][v][lane] + red[1][v][lane] + red[2][v][lane] + red[3][v][lane];
+        // D[token slot 4c+v][adapter row r16]
+        int tj = tc + 4 * c + v;
+        if (tj < count && j < e.rank) {
+            int t = toks[tj];
+            u[(size_t)t * rmax + j] = s * tscale[t];
+        }
+    }
+}
+
+#define DEF_SHRINK(NAME, FMT)                                                              \
+    extern "C" __global__ __launch_bounds__(256) void realm_lora_shrink_##NAME##_f32(     \
+        const _Float16 *xh, const _Float16 *xl, const float *tscale, const int *ids,      \
+        const LoraEntry *table, float *u, int M, int K, int KX, int rmax)                 \
+    {                                                                                      \
+        lora_shrink<FMT, true>(xh, xl, tscale, ids, table, u, M, K, KX, rmax);             \
+    }                                                                                      \
+    extern "C" __global__ __launch_bounds__(256) void realm_lora_shrink_##NAME##_bf16(    \
+        const _Float16 *xh, const _Float16 *xl, const float *tscale, const int *ids,      \
+        const LoraEntry *table, float *u, int M, int K, int KX, int rmax)                 \
+    {                                                                                      \
+        lora_shrink<FMT, false>(xh, xl, tscale, ids, table, u, M, K, KX, rmax);            \
+    }
+DEF_SHRINK(q4k, FMT_Q4K)
+DEF_SHRINK(q6k, FMT_Q6K)
+DEF_SHRINK(q80, FMT_Q80)

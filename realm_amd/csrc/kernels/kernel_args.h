@@ -1,0 +1,44 @@
+// Kernel-argument structs shared by the host library (g++) and the gfx950
+// kernels (hipcc): plain C layouts, passed by value through
+// hipModuleLaunchKernel.
+#pragma once
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+namespace realm {
+#endif
+
+// One registered LoRA adapter, as the kernels read it from the device table.
+struct LoraEntry {
+    const void *a; // [rank][in_dim], f32 or f16
+    const void *b; // [out_dim][rank], f32 or f16
+    int32_t rank;
+    int32_t dtype; // 0 f32, 1 f16
+    float scale;   // alpha / rank
+    int32_t pad;
+};
+
+// Arguments of the realm_gemm_* kernels.
+struct GemmArgs {
+    const void *w0;     // Q4_K hdr | Q6_K d  | Q8_0 d
+    const void *w1;     // Q4_K qs  | Q6_K sc | Q8_0 q
+    const void *w2;     // Q6_K q
+    const void *xh;     // f16 activations, hi part [Mp][KX]
+    const void *xl;     // f16 lo part (null for bf16 input)
+    const void *xm;     // Q4_K min fragments [Mp][K/256][4][8] f16
+    const float *tscale;
+    float *y;           // [M][N]
+    int32_t N, K, KX, M;
+    int32_t nan_fb;
+    int32_t n_adapters;
+    const int32_t *ids;           // LoRA: adapter slot per token (-1 none)
+    const LoraEntry *table;       // LoRA: device table
+    const float *u;               // LoRA: shrink output [Mp][rmax]
+    int32_t rmax;
+    int32_t pad;
+};
+
+#ifdef __cplusplus
+} // namespace realm
+#endif

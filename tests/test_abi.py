@@ -1,0 +1,60 @@
+"""The C-ABI library loads and exports exactly what include/realm_hip.h
+declares, and the ctypes binding matches the header.  No GPU calls."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from conftest import REPO
+
+HEADER = os.path.join(REPO, "include", "realm_hip.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b(realm_hip_\w+)\s*\(", text))
+
+
+def test_header_declares_the_boundary():
+    names = declared_functions()
+    for n in ("realm_hip_init", "realm_hip_last_error", "realm_hip_backend_name",
+              "realm_hip_matmul", "realm_hip_fused_dequant_matmul_q4k",
+              "realm_hip_fused_dequant_matmul_q6k", "realm_hip_fused_dequant_matmul_q80",
+              "realm_hip_candle_matmul", "realm_hip_candle_matmul_transposed",
+              "realm_hip_dequantize", "realm_hip_weights_register",
+              "realm_hip_multi_lora_matmul", "realm_hip_lora_register"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    from realm_amd import _lib
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("library not built")
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    for name in sorted(declared_functions()):
+        assert hasattr(lib, name), name
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (realm_hip_\w+)", out))
+    assert exported == declared_functions()
+
+
+def test_ctypes_binding_matches_header():
+    from realm_amd import _lib
+    assert set(_lib.SIGNATURES) == declared_functions()
+
+
+def test_code_object_is_embedded_for_gfx950():
+    from realm_amd import _lib, build
+    if not os.path.exists(build.HSACO):
+        pytest.skip("code object not built")
+    blob = open(build.HSACO, "rb").read()
+    assert blob[:4] == b"\x7fELF" and b"gfx950" in blob
+    lib = open(_lib.LIB_PATH, "rb").read()
+    assert blob[:4096] in lib  # embedded verbatim
+    for k in (b"realm_gemv_q4k_l64_u1_r4", b"realm_gemm_q4k_p4_bf16", b"realm_dequant_q6k",
+              b"realm_lora_shrink_q4k_f32", b"realm_dense_f32"):
+        assert k in blob

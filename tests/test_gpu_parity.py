@@ -1,0 +1,440 @@
+"""GPU parity: the HIP path through the C ABI against the CPU oracle on the
+same seeded inputs.
+
+Bars: dequantization is bit-exact with quant.rs; matmul and LoRA outputs
+agree with realm-compute-cpu's CandleCpuBackend semantics (dequantize, then
+f32 x . W^T) within 1e-3 relative L2 error (REL_TOL, the tolerance of the
+workload definition).  Full-size configurations are compared on the full
+output where the oracle finishes in seconds, otherwise on a seeded subset of
+rows.
+"""
+import numpy as np
+import pytest
+
+from realm_amd import synth
+from realm_amd.backend import BackendError, InvalidShape, RealmError
+from realm_amd.formats import GGML_Q4_K, GGML_Q6_K, GGML_Q8_0, NAMES, Q4K_DTYPE, Q6K_DTYPE
+from realm_amd.formats import Q80_DTYPE
+
+from conftest import rel_l2
+
+pytestmark = pytest.mark.gpu
+
+REL_TOL = 1e-3
+FORMATS = [GGML_Q4_K, GGML_Q6_K, GGML_Q8_0]
+
+
+def bits_equal(a, b):
+    a = np.asarray(a, np.float32)
+    b = np.asarray(b, np.float32)
+    nan = np.isnan(b)
+    return np.array_equal(np.isnan(a), nan) and np.array_equal(a[~nan].view(np.uint32),
+                                                               b[~nan].view(np.uint32))
+
+
+def special_scales(g, blocks, field):
+    """Overwrite some f16 scales with edge values: subnormals, -0, max, inf, nan."""
+    v = blocks[field]
+    n = v.size
+    pick = g.choice(n, size=min(n, 64), replace=False)
+    specials = np.array([0x0001, 0x03FF, 0x0200, 0x8000, 0x8001, 0x7BFF, 0xFBFF, 0x7C00,
+                         0xFC00, 0x7E00, 0x3C00, 0x0000], np.uint16)
+    v[pick] = specials[np.arange(pick.size) % specials.size]
+
+
+# ---------------------------------------------------------------- basics
+
+def test_init_and_name(backend):
+    assert "gfx950" in backend.name()
+
+
+@pytest.mark.parametrize("t", FORMATS)
+def test_dequant_bit_exact(backend, oracle, t):
+    g = synth.rng(100 + t)
+    blocks = synth.blocks(g, t, 64, 4096)
+    special_scales(g, blocks, "scale" if t == GGML_Q8_0 else "d")
+    if t == GGML_Q4_K:
+        special_scales(g, blocks, "dmin")
+    n_el = blocks.size * (32 if t == GGML_Q8_0 else 256)
+    got = backend.dequantize(t, blocks, n_el)
+    ref = oracle.dequantize(t, blocks)
+    assert bits_equal(got, ref)
+
+
+def test_dequant_kats_and_positions(backend, kat):
+    for key, t in (("q4k", GGML_Q4_K), ("q6k", GGML_Q6_K), ("q8", GGML_Q8_0)):
+        blk = kat[f"{key}_kat_block"]
+        exp = kat[f"{key}_kat_expected"]
+        assert bits_equal(backend.dequantize(t, blk, exp.size), exp), key
+    for key, t, hot, cold in (("q4k", GGML_Q4_K, 15.0, 0.0), ("q6k", GGML_Q6_K, 31.0, -32.0)):
+        blocks = kat[f"{key}_pos_blocks"]
+        idx = kat[f"{key}_pos_index"]
+        y = backend.dequantize(t, blocks, idx.size * 256).reshape(-1, 256)
+        exp = np.full_like(y, cold)
+        exp[np.arange(idx.size), idx] = hot
+        assert np.array_equal(y, exp), key
+
+
+def test_dequantize_tensor_semantics(backend, oracle):
+    b4 = synth.q4k_blocks(synth.rng(5), 2, 256).view(np.uint8)
+    with pytest.raises(RealmError) as e:
+        backend.dequantize(GGML_Q4_K, b4[:-1], 512)
+    assert e.value.code == 4  # ModelParseError (Error::InvalidFormat)
+    with pytest.raises(InvalidShape):
+        backend.dequantize(GGML_Q4_K, b4, 500)
+    b6 = synth.q6k_blocks(synth.rng(6), 2, 256).view(np.uint8)
+    raw = np.concatenate([b6, b6[:50]])
+    got = backend.dequantize(GGML_Q6_K, raw, 600)
+    rc, ref = oracle.dequantize_tensor(GGML_Q6_K, raw, 600)
+    assert rc == 0 and bits_equal(got, ref)
+    with pytest.raises(InvalidShape):  # the reference panics here
+        backend.dequantize(GGML_Q6_K, b6, 300)
+    with pytest.raises(BackendError):
+        backend.dequantize(2, b6, 256)
+
+
+def test_trait_validation(backend):
+    """fused.rs:2977-3000 / webgpu_dequant_tests.rs:238-333 error cases."""
+    one = np.zeros(1, Q4K_DTYPE)
+    with pytest.raises(InvalidShape):
+        backend.fused_dequant_matmul_q4k(one, np.zeros(100, np.float32), 1, 1, 100)
+    with pytest.raises(InvalidShape):
+        backend.fused_dequant_matmul_q4k(one, np.zeros(256, np.float32), 1, 2, 256)
+    with pytest.raises(InvalidShape):  # wrong input length
+        backend.fused_dequant_matmul_q4k(np.zeros(4, Q4K_DTYPE), np.zeros(255, np.float32),
+                                         1, 4, 256)
+    with pytest.raises(InvalidShape):
+        backend.fused_dequant_matmul_q80(np.zeros(2, Q80_DTYPE), np.zeros(40, np.float32),
+                                         1, 1, 40)
+    with pytest.raises(BackendError):
+        backend.fused_dequant_matmul_q5k(None, None, 1, 1, 256)
+    # empty K: zero output, like the reference's empty accumulation
+    y = backend.fused_dequant_matmul_q4k(np.zeros(0, Q4K_DTYPE), np.zeros(0, np.float32), 2, 3, 0)
+    assert np.array_equal(y, np.zeros(6, np.float32))
+
+
+# ---------------------------------------------------------------- matmul
+
+def test_fused_reference_inputs(backend, oracle):
+    """The reference's own fused.rs test inputs (N=2)."""
+    from test_oracle import _ref_test_q4k_blocks, _ref_test_q6k_blocks, _ref_test_q80_blocks
+    for t, k, mk in ((GGML_Q4_K, 512, _ref_test_q4k_blocks), (GGML_Q6_K, 512, _ref_test_q6k_blocks),
+                     (GGML_Q8_0, 64, _ref_test_q80_blocks)):
+        blocks = mk()
+        x = ((np.arange(k) % 7).astype(np.float32) - 3.0) * 0.5
+        got = backend._fused(t, blocks, x, 1, 2, k)
+        rc, ref = oracle.candle_fused(t, blocks, x, 1, 2, k)
+        assert rc == 0 and rel_l2(got, ref) < REL_TOL, NAMES[t]
+
+
+@pytest.mark.parametrize("t", FORMATS)
+@pytest.mark.parametrize("m", [1, 2, 5, 16, 17, 33, 64, 100, 130])
+def test_fused_random(backend, oracle, t, m):
+    g = synth.rng(1000 * t + m)
+    n, k = 200, 1024 if t != GGML_Q8_0 else 1056
+    blocks = synth.blocks(g, t, n, k)
+    x = synth.activations(g, m, k)
+    got = backend._fused(t, blocks, x, m, n, k)
+    rc, ref = oracle.candle_fused(t, blocks, x, m, n, k)
+    assert rc == 0
+    err = rel_l2(got, ref)
+    print(f"{NAMES[t]} m={m} rel_l2={err:.3e}")
+    assert err < REL_TOL
+
+
+@pytest.mark.parametrize("t", FORMATS)
+def test_fused_odd_shapes(backend, oracle, t):
+    """Short rows (K = one block), N not a multiple of any tile."""
+    g = synth.rng(77 + t)
+    for n, k, m in ((1, 256, 1), (3, 256, 3), (17, 512, 1), (129, 768, 19)):
+        if t == GGML_Q8_0:
+            k = k // 8 * 3 if k > 256 else 96  # K % 64 != 0 exercises the padded layout
+        blocks = synth.blocks(g, t, n, k)
+        x = synth.activations(g, m, k)
+        got = backend._fused(t, blocks, x, m, n, k)
+        rc, ref = oracle.candle_fused(t, blocks, x, m, n, k)
+        assert rc == 0 and rel_l2(got, ref) < REL_TOL, (n, k, m)
+
+
+def test_config0_full(backend, oracle):
+    """Q4_K GEMV M=1, W 5632 x 2048 (the reference's CPU-runnable case)."""
+    g = synth.rng(0)
+    n, k = 5632, 2048
+    blocks = synth.q4k_blocks(g, n, k)
+    x = synth.activations(g, 1, k)
+    h = backend.register_weights(GGML_Q4_K, blocks, n, k)
+    try:
+        got = backend.weights_matmul(h, x)
+    finally:
+        backend.release_weights(h)
+    rc, ref = oracle.candle_fused(GGML_Q4_K, blocks, x, 1, n, k)
+    assert rc == 0 and rel_l2(got, ref) < REL_TOL
+
+
+LAYER_7B = [("wq", GGML_Q4_K, 4096, 4096), ("wk", GGML_Q4_K, 4096, 4096),
+            ("wv", GGML_Q4_K, 4096, 4096), ("wo", GGML_Q4_K, 4096, 4096),
+            ("w_gate", GGML_Q4_K, 11008, 4096), ("w_up", GGML_Q4_K, 11008, 4096),
+            ("w_down", GGML_Q6_K, 4096, 11008)]
+
+
+@pytest.mark.parametrize("m", [1, 4, 16])
+def test_config1_layer(backend, oracle, m):
+    """The LLaMA-7B decoder-layer matvec set at decode batch 1/4/16."""
+    g = synth.rng(1)
+    for name, t, n, k in LAYER_7B:
+        blocks = synth.blocks(g, t, n, k)
+        x = synth.activations(g, m, k)
+        h = backend.register_weights(t, blocks, n, k)
+        try:
+            got = backend.weights_matmul(h, x)
+        finally:
+            backend.release_weights(h)
+        rc, ref = oracle.candle_fused(t, blocks, x, m, n, k)
+        err = rel_l2(got, ref)
+        print(f"{name} m={m} rel_l2={err:.3e}")
+        assert rc == 0 and err < REL_TOL, name
+
+
+def _row_subset(t, blocks, n, k, rows):
+    bpr = k // (32 if t == GGML_Q8_0 else 256)
+    return blocks.reshape(n, bpr)[rows].reshape(-1)
+
+
+@pytest.mark.parametrize("t", [GGML_Q4_K, GGML_Q8_0])
+def test_config2_prefill_bf16(backend, oracle, t):
+    """Prefill M=512, K=4096 -> N=11008 with bf16 activations, checked on a
+    seeded subset of 96 output rows for all 512 tokens."""
+    g = synth.rng(2)
+    m, n, k = 512, 11008, 4096
+    blocks = synth.blocks(g, t, n, k)
+    xb = synth.activations_bf16(g, m, k)
+    h = backend.register_weights(t, blocks, n, k)
+    dx = backend.alloc(xb.nbytes).upload(xb)
+    dy = backend.alloc(m * n * 4)
+    try:
+        backend.matmul_dev(h, dx.ptr, m, dy.ptr, bf16=True)
+        backend.synchronize()
+        got = dy.download(np.float32, m * n).reshape(m, n)
+    finally:
+        backend.release_weights(h)
+        dx.close()
+        dy.close()
+    rows = np.sort(synth.rng(22).choice(n, 96, replace=False))
+    rc, ref = oracle.candle_fused(t, _row_subset(t, blocks, n, k, rows),
+                                  synth.bf16_bits_to_f32(xb), m, rows.size, k)
+    assert rc == 0
+    err = rel_l2(got[:, rows], ref.reshape(m, rows.size))
+    print(f"prefill {NAMES[t]} rel_l2={err:.3e}")
+    assert err < REL_TOL
+    assert np.isfinite(got).all()
+
+
+def test_q6k_wide_scales(backend, oracle):
+    """Q6_K sub-scales over the full int8 range use the split-scale path."""
+    g = synth.rng(66)
+    n, k = 96, 2048
+    blocks = synth.q6k_blocks(g, n, k)
+    blocks["scales"] = g.integers(-128, 128, blocks["scales"].shape, dtype=np.int8)
+    for m in (1, 8, 40):
+        x = synth.activations(g, m, k)
+        got = backend.fused_dequant_matmul_q6k(blocks, x, m, n, k)
+        rc, ref = oracle.candle_fused(GGML_Q6_K, blocks, x, m, n, k)
+        assert rc == 0 and rel_l2(got, ref) < REL_TOL, m
+
+
+@pytest.mark.parametrize("scale", [1e-30, 1e-6, 1e6, 1e30])
+def test_activation_range(backend, oracle, scale):
+    """Activations far outside f16 range stay exact through the per-token
+    power-of-two rescale of the MFMA path (and the f32 GEMV path)."""
+    g = synth.rng(55)
+    n, k = 64, 1024
+    blocks = synth.q4k_blocks(g, n, k)
+    for m in (1, 20):
+        x = synth.activations(g, m, k) * np.float32(scale)
+        x[:, 5] *= 1e3  # a large outlier per token
+        got = backend.fused_dequant_matmul_q4k(blocks, x, m, n, k)
+        rc, ref = oracle.candle_fused(GGML_Q4_K, blocks, x, m, n, k)
+        assert rc == 0 and rel_l2(got, ref) < REL_TOL, (scale, m)
+
+
+def test_nan_fallback(backend, oracle):
+    g = synth.rng(8)
+    n, k = 32, 512
+    blocks = synth.q4k_blocks(g, n, k)
+    blocks["d"][::7] = 0x7E00
+    for m in (1, 24):
+        x = synth.activations(g, m, k)
+        got = backend.fused_dequant_matmul_q4k(blocks, x, m, n, k)
+        rc, ref = oracle.candle_fused(GGML_Q4_K, blocks, x, m, n, k)
+        assert np.array_equal(np.isnan(got), np.isnan(ref))
+        backend.set_nan_fallback(True)
+        try:
+            got = backend.fused_dequant_matmul_q4k(blocks, x, m, n, k)
+        finally:
+            backend.set_nan_fallback(False)
+        rc, ref = oracle.fused(GGML_Q4_K, blocks, x, m, n, k, nan_fallback=True)
+        assert np.isfinite(got).all() and rel_l2(got, ref) < REL_TOL
+
+
+# ------------------------------------------------------------------- LoRA
+
+def _oracle_lora(oracle, t, blocks, x, ids, adapters, n, k):
+    m = x.shape[0]
+    rc, base = oracle.candle_fused(t, blocks, x, m, n, k)
+    assert rc == 0
+    ad = [(a.astype(np.float32), b.astype(np.float32), r, al) for a, b, r, al in adapters]
+    return oracle.multi_lora_delta(x, ids, ad, base.reshape(m, n).copy())
+
+
+@pytest.mark.parametrize("t", FORMATS)
+@pytest.mark.parametrize("dtype", [np.float16, np.float32])
+def test_multi_lora_small(backend, oracle, t, dtype):
+    g = synth.rng(300 + t)
+    n, k, m = 160, 512, 37
+    blocks = synth.blocks(g, t, n, k)
+    x = synth.activations(g, m, k)
+    adapters, handles = [], []
+    for r in (8, 16, 64, 3):
+        a, b = synth.lora_adapter(g, r, k, n)
+        a, b = a.astype(dtype), b.astype(dtype)
+        adapters.append((a, b, r, 16.0))
+        handles.append(backend.lora_register(a, b, r, 16.0, k, n))
+    ids = synth.adapter_ids(g, m, len(adapters))
+    ids[3] = 99  # unknown slot: base only
+    wh = backend.register_weights(t, blocks, n, k)
+    sh = backend.lora_set_create(handles)
+    try:
+        got = backend.multi_lora_matmul(wh, sh, x, ids)
+        base = backend.weights_matmul(wh, x)
+    finally:
+        backend.lora_set_release(sh)
+        for h in handles:
+            backend.lora_release(h)
+        backend.release_weights(wh)
+    ref = _oracle_lora(oracle, t, blocks, x, ids, adapters, n, k)
+    assert rel_l2(got, ref) < REL_TOL
+    none = (ids < 0) | (ids >= len(adapters))
+    assert np.array_equal(got[none], base[none]) or rel_l2(got[none], base[none]) < 1e-6
+
+
+def test_multi_lora_config3(backend, oracle):
+    """16 tenants, ranks from {8,16,64}, 64 tokens with Zipf(1.1) ids and 10%
+    no-adapter, on a shared Q4_K 4096 x 4096 projection."""
+    g = synth.rng(3)
+    n = k = 4096
+    m = 64
+    blocks = synth.q4k_blocks(g, n, k)
+    ranks = g.choice([8, 16, 64], 16)
+    adapters = []
+    for r in ranks:
+        a, b = synth.lora_adapter(g, int(r), k, n)
+        adapters.append((a, b, int(r), 16.0))
+    ids = synth.adapter_ids(g, m, 16)
+    x = synth.activations(g, m, k)
+    handles = [backend.lora_register(a, b, r, al, k, n) for a, b, r, al in adapters]
+    wh = backend.register_weights(GGML_Q4_K, blocks, n, k)
+    sh = backend.lora_set_create(handles)
+    try:
+        got = backend.multi_lora_matmul(wh, sh, x, ids)
+    finally:
+        backend.lora_set_release(sh)
+        for h in handles:
+            backend.lora_release(h)
+        backend.release_weights(wh)
+    ref = _oracle_lora(oracle, GGML_Q4_K, blocks, x, ids, adapters, n, k)
+    err = rel_l2(got, ref)
+    # the LoRA delta itself, not just the sum, must match
+    rc, base = oracle.candle_fused(GGML_Q4_K, blocks, x, m, n, k)
+    derr = rel_l2(got - base.reshape(m, n), ref - base.reshape(m, n))
+    print(f"config3 rel_l2={err:.3e} delta rel_l2={derr:.3e}")
+    assert err < REL_TOL and derr < 1e-2
+
+
+def test_lora_validation(backend):
+    a = np.zeros((4, 256), np.float16)
+    b = np.zeros((64, 4), np.float16)
+    with pytest.raises(InvalidShape):
+        backend.lora_register(a, b, 0, 1.0, 256, 64)
+    h = backend.lora_register(a, b, 4, 8.0, 256, 64)
+    sh = backend.lora_set_create([h])
+    with pytest.raises(InvalidShape):  # in use by a set
+        backend.lora_release(h)
+    wh = backend.register_weights(GGML_Q4_K, synth.q4k_blocks(synth.rng(1), 32, 256), 32, 256)
+    with pytest.raises(InvalidShape):  # dims differ from the weight
+        backend.multi_lora_matmul(wh, sh, np.zeros((1, 256), np.float32), np.zeros(1, np.int32))
+    backend.release_weights(wh)
+    backend.lora_set_release(sh)
+    backend.lora_release(h)
+
+
+# ------------------------------------------------------------------ dense
+
+def test_dense_kats(backend, kat):
+    assert np.array_equal(backend.matmul(kat["dense_a1"], kat["dense_b1"], 2, 3, 2),
+                          kat["dense_e1"])
+    assert np.array_equal(backend.matmul(kat["dense_a3"], kat["dense_b3"], 2, 2, 2),
+                          kat["dense_e3"])
+    with pytest.raises(RealmError):
+        backend.matmul(kat["dense_a1"], kat["dense_b1"], 2, 2, 2)
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 1, 1), (3, 5, 7), (64, 64, 64), (65, 130, 33),
+                                   (200, 300, 100)])
+def test_dense_random(backend, m, k, n):
+    g = synth.rng(m * 7 + k)
+    a = g.standard_normal((m, k), dtype=np.float32)
+    b = g.standard_normal((k, n), dtype=np.float32)
+    got = backend.matmul(a, b, m, k, n).reshape(m, n)
+    ref = a.astype(np.float64) @ b.astype(np.float64)
+    assert rel_l2(got, ref) < 1e-5
+
+
+def test_candle_matmul_host_function(backend, kat):
+    """env.candle_matmul over a linear memory (memory64_host.rs:853-1086)."""
+    mem = np.zeros(4096, np.uint8)
+    a, b = kat["dense_a2"], kat["dense_bt2"]
+    mem[100:116] = a.view(np.uint8)  # unaligned offsets are allowed
+    mem[203:219] = b.view(np.uint8)
+    rc = backend.candle_matmul(mem, 100, 203, 301, 2, 2, 2, transposed=True)
+    assert rc == 4
+    assert np.array_equal(mem[301:317].copy().view(np.float32), kat["dense_e2"])
+    mem[203:219] = np.array([1, 2, 3, 4], np.float32).view(np.uint8)
+    rc = backend.candle_matmul(mem, 100, 203, 301, 2, 2, 2)
+    assert rc == 4 and np.array_equal(mem[301:317].copy().view(np.float32),
+                                      np.array([7, 10, 15, 22], np.float32))
+    assert backend.candle_matmul(mem, 4090, 0, 0, 2, 2, 2) == -3
+    assert backend.candle_matmul(mem, 0, 4090, 0, 2, 2, 2) == -4
+    assert backend.candle_matmul(mem, 0, 0, 4090, 2, 2, 2) == -6
+
+
+# ------------------------------------------------------- device-pointer path
+
+def test_resident_dev_path_and_events(backend, oracle):
+    g = synth.rng(12)
+    n, k, m = 512, 2048, 8
+    blocks = synth.q4k_blocks(g, n, k)
+    x = synth.activations(g, m, k)
+    h = backend.register_weights(GGML_Q4_K, blocks, n, k)
+    assert backend.weights_info(h)[:3] == (GGML_Q4_K, n, k)
+    dx = backend.alloc(x.nbytes).upload(x)
+    dy = backend.alloc(m * n * 4)
+    s = backend.stream()
+    e0, e1 = backend.event(), backend.event()
+    try:
+        backend.record(e0, s)
+        backend.matmul_dev(h, dx.ptr, m, dy.ptr, stream=s)
+        backend.record(e1, s)
+        assert backend.elapsed_ms(e0, e1) >= 0.0
+        got = dy.download(np.float32, m * n)
+        # repeated calls give identical results
+        backend.matmul_dev(h, dx.ptr, m, dy.ptr, stream=s)
+        backend.synchronize()
+        assert np.array_equal(dy.download(np.float32, m * n), got)
+    finally:
+        backend.release_weights(h)
+        dx.close()
+        dy.close()
+    rc, ref = oracle.candle_fused(GGML_Q4_K, blocks, x, m, n, k)
+    assert rel_l2(got, ref) < REL_TOL
+    with pytest.raises(InvalidShape):
+        backend.weights_matmul(h, x)  # released handle
