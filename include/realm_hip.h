@@ -163,6 +163,15 @@ int realm_hip_weights_matmul(uint64_t handle, const float *input, size_t batch,
 int realm_hip_weights_matmul_dev(uint64_t handle, const float *d_input, size_t batch,
                                  float *d_out, void *stream);
 
+/* Grouped form for 1..4 resident weights of one format and K that share the
+ * input, e.g. the q/k/v projections (or gate/up) that realm_forward_layer
+ * issues back to back on the same normed hidden state
+ * (crates/realm-runtime/src/memory64_host.rs:2078-2308, 2384-2443):
+ * d_outs[i] = x . W_i^T.  Batch 1 runs all of them in one launch. */
+int realm_hip_weights_matmul_group_dev(const uint64_t *handles, size_t count,
+                                       const float *d_input, size_t batch,
+                                       float *const *d_outs, void *stream);
+
 /* Prefill form with bf16 activations (raw bf16 bits, [batch,k]). */
 int realm_hip_weights_matmul_bf16_dev(uint64_t handle, const uint16_t *d_input,
                                       size_t batch, float *d_out, void *stream);

@@ -269,6 +269,12 @@ class HipGpuBackend:
               else self.lib.realm_hip_weights_matmul_dev)
         self._check(fn(handle, c_void_p(d_x), batch, c_void_p(d_y), c_void_p(stream or 0)))
 
+    def matmul_group_dev(self, handles, d_x: int, batch: int, d_ys, stream=None) -> None:
+        hs = (c_uint64 * len(handles))(*handles)
+        ys = (c_void_p * len(d_ys))(*d_ys)
+        self._check(self.lib.realm_hip_weights_matmul_group_dev(
+            hs, len(handles), c_void_p(d_x), batch, ys, c_void_p(stream or 0)))
+
     def graph_begin(self, stream: int) -> None:
         self._check(self.lib.realm_hip_graph_begin(c_void_p(stream)))
 

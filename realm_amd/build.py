@@ -40,28 +40,28 @@ def _run(cmd: list[str]) -> None:
         print(out, file=sys.stderr)
 
 
-def build_hsaco() -> str:
-    os.makedirs(LIB_DIR, exist_ok=True)
-    tmp = HSACO + ".tmp"
-    _run([os.path.join(ROCM, "bin", "hipcc"), *HIP_FLAGS, "-I", KDIR,
-          os.path.join(KDIR, "realm_kernels.hip"), "-o", tmp])
-    os.replace(tmp, HSACO)
-    return HSACO
+def build_hsaco(out: str = HSACO, defines: tuple = ()) -> str:
+    os.makedirs(os.path.dirname(out), exist_ok=True)
+    tmp = out + ".tmp"
+    _run([os.path.join(ROCM, "bin", "hipcc"), *HIP_FLAGS, *[f"-D{d}" for d in defines],
+          "-I", KDIR, os.path.join(KDIR, "realm_kernels.hip"), "-o", tmp])
+    os.replace(tmp, out)
+    return out
 
 
-def build_host() -> str:
-    os.makedirs(LIB_DIR, exist_ok=True)
-    tmp = LIBSO + ".tmp"
+def build_host(out: str = LIBSO, hsaco: str = HSACO) -> str:
+    os.makedirs(os.path.dirname(out), exist_ok=True)
+    tmp = out + ".tmp"
     _run(["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-fvisibility=hidden",
           "-Wall", "-Wextra", "-Wno-unused-parameter",
-          "-D__HIP_PLATFORM_AMD__", f"-DREALM_HSACO_FILE={HSACO}",
+          "-D__HIP_PLATFORM_AMD__", f"-DREALM_HSACO_FILE={hsaco}",
           "-I", os.path.join(ROCM, "include"), "-I", os.path.join(REPO, "include"),
           "-I", KDIR,
           os.path.join(HDIR, "realm_hip.cpp"), "-o", tmp,
           "-L", os.path.join(ROCM, "lib"), "-Wl,-rpath," + os.path.join(ROCM, "lib"),
           "-lamdhip64", "-lpthread"])
-    os.replace(tmp, LIBSO)
-    return LIBSO
+    os.replace(tmp, out)
+    return out
 
 
 def build() -> str:

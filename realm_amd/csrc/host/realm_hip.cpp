@@ -14,6 +14,7 @@
 #include <atomic>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 #include <mutex>
@@ -302,12 +303,14 @@ int upload_repack(int type, const void *blocks, size_t n, size_t k, void *dst, W
     long long nb = (long long)nblocks;
     if (type == GGML_Q4_K) {
         void *hdr = (void *)w->w0, *qs = (void *)w->w1;
-        void *args[] = {&raw, &hdr, &qs, &nb};
+        int bpr = (int)(k / 256);
+        void *args[] = {&raw, &hdr, &qs, &nb, &bpr};
         CHECK(launch("realm_repack_q4k", dim3((unsigned)((nblocks * 9 + 255) / 256)), dim3(256),
                      0, s, args));
     } else if (type == GGML_Q6_K) {
         void *dq = (void *)w->w0, *scq = (void *)w->w1, *qq = (void *)w->w2;
-        void *args[] = {&raw, &dq, &scq, &qq, &nb};
+        int bpr = (int)(k / 256);
+        void *args[] = {&raw, &dq, &scq, &qq, &nb, &bpr};
         CHECK(launch("realm_repack_q6k", dim3((unsigned)((nblocks * 64 + 255) / 256)),
                      dim3(256), 0, s, args));
     } else {
@@ -346,47 +349,59 @@ struct LoraCall {
 
 // --------------------------------------------------------------- dispatch
 
-// M = 1, f32 activations: the VALU GEMV.  Returns BACKEND_UNSUPPORTED when
-// the row is too long for its register budget (the caller then uses MFMA).
-int run_gemv(const Weight &w, const float *d_x, float *d_y, hipStream_t s)
+// M = 1, f32 activations: the integer-dot GEMV over 1..4 matrices of one
+// format that share x (rows concatenated).  Returns BACKEND_UNSUPPORTED when
+// the row is too long for the kernel's register budget or LDS (the caller
+// then uses the MFMA path).
+int run_gemv(const Weight *const *ws, int count, const float *d_x, float *const *d_y,
+             hipStream_t s)
 {
+    const Weight &w = *ws[0];
     int U = (int)(w.kx / 64);
     int lpr = U <= 16 ? 16 : (U <= 32 ? 32 : 64);
     int upl = (U + lpr - 1) / lpr;
-    if (upl > 8 || w.kx * 4 > g_dev.max_lds)
+    size_t lds = (size_t)U * 16 * 10; // 8 x records + up to 2 meta float4 per unit
+    if (upl > 8 || lds > g_dev.max_lds || count < 1 || count > REALM_GEMV_MAX_MATS)
         return REALM_BACKEND_UNSUPPORTED;
-    // rows per pass: as many as keep >= 4 waves per CU busy
-    int rpw = 64 / lpr;
-    int maxr = upl == 1 ? 4 : (upl <= 3 ? 2 : 1);
-    if (lpr < 64 && upl > 1)
-        maxr = std::min(maxr, 2);
-    int r = maxr;
-    while (r > 1 && (long)((w.n + rpw * r - 1) / (rpw * r)) < 4L * g_dev.cu_count)
-        r >>= 1;
-    long npass = (long)((w.n + rpw * r - 1) / (rpw * r));
-    long wgs = (npass + 3) / 4;
-    // waves per CU the kernel can hold: LDS-bound (x is staged per workgroup)
-    long per_cu = std::max<long>(1, (long)(160 * 1024 / std::max<size_t>(w.kx * 4, 1)));
-    wgs = std::min<long>(wgs, std::max<long>(1, per_cu) * g_dev.cu_count * 2);
+    realm::GemvArgs a;
+    std::memset(&a, 0, sizeof a);
+    int rows = 0;
+    for (int i = 0; i < count; ++i) {
+        a.w0[i] = ws[i]->w0;
+        a.w1[i] = ws[i]->w1;
+        a.w2[i] = ws[i]->w2;
+        a.y[i] = d_y[i];
+        a.row_start[i] = rows;
+        rows += (int)ws[i]->n;
+    }
+    for (int i = count; i <= REALM_GEMV_MAX_MATS; ++i)
+        a.row_start[i] = rows;
+    a.nmat = count;
+    a.x = d_x;
+    a.K = (int)w.k;
+    a.KX = (int)w.kx;
+    a.nan_fb = g_nan_fb.load();
+    // one workgroup per CU (1024 threads while a lane owns one unit, as the
+    // kernels' launch bounds say); two rows per pass when every wave still
+    // gets at least two passes
+    const int threads = upl <= 1 ? 1024 : (upl <= 3 ? 512 : 256);
+    const int rpw = 64 / lpr;
+    const long waves = (long)(threads / 64) * g_dev.cu_count;
+    int r = 1;
+    if (upl == 1 && (long)rows / (2 * rpw) >= 2 * waves)
+        r = 2;
+    if (const char *env = getenv("REALM_GEMV_R")) { // tuning override
+        int v = atoi(env);
+        if (v == 1 || (v == 2 && upl == 1))
+            r = v;
+    }
+    long npass = ((long)rows + rpw * r - 1) / (rpw * r);
+    long wgs = std::min<long>(g_dev.cu_count, (npass + threads / 64 - 1) / (threads / 64));
     std::string name = std::string("realm_gemv_") + fmt_name(w.type) + "_l" +
                        std::to_string(lpr) + "_u" + std::to_string(upl) + "_r" +
                        std::to_string(r);
-    int N = (int)w.n, K = (int)w.k, nan_fb = g_nan_fb.load();
-    size_t lds = w.kx * 4;
-    if (w.type == GGML_Q4_K) {
-        const void *hdr = w.w0, *qs = w.w1;
-        void *args[] = {&hdr, &qs, &d_x, &d_y, &N, &K, &nan_fb};
-        return launch(name, dim3((unsigned)wgs), dim3(256), lds, s, args);
-    }
-    if (w.type == GGML_Q6_K) {
-        const void *dq = w.w0, *scq = w.w1, *qq = w.w2;
-        void *args[] = {&dq, &scq, &qq, &d_x, &d_y, &N, &K, &nan_fb};
-        return launch(name, dim3((unsigned)wgs), dim3(256), lds, s, args);
-    }
-    const void *dq = w.w0, *qq = w.w1;
-    int KP = (int)w.kx;
-    void *args[] = {&dq, &qq, &d_x, &d_y, &N, &K, &KP};
-    return launch(name, dim3((unsigned)wgs), dim3(256), lds, s, args);
+    void *args[] = {&a};
+    return launch(name, dim3((unsigned)std::max<long>(wgs, 1)), dim3(threads), lds, s, args);
 }
 
 // Any M: activation prep, optional LoRA shrink, then the MFMA kernel.
@@ -485,7 +500,9 @@ int run_matmul(const Weight &w, const void *d_x, bool bf16, size_t M, float *d_y
                hipStream_t s, const LoraCall *lora)
 {
     if (M == 1 && !bf16 && !lora) {
-        int rc = run_gemv(w, (const float *)d_x, d_y, s);
+        const Weight *ws[1] = {&w};
+        float *ys[1] = {d_y};
+        int rc = run_gemv(ws, 1, (const float *)d_x, ys, s);
         if (rc != REALM_BACKEND_UNSUPPORTED)
             return rc;
     }
@@ -841,6 +858,35 @@ REALM_API int realm_hip_weights_matmul_dev(uint64_t handle, const float *d_input
     hipStream_t s;
     CHECK(pick_stream(stream, &s));
     return run_matmul(w, d_input, false, batch, d_out, s, nullptr);
+}
+
+REALM_API int realm_hip_weights_matmul_group_dev(const uint64_t *handles, size_t count,
+                                                 const float *d_input, size_t batch,
+                                                 float *const *d_outs, void *stream)
+{
+    if (!handles || !d_outs || count == 0 || count > REALM_GEMV_MAX_MATS)
+        return fail(REALM_INVALID_ARGUMENT, "group needs 1..4 weight handles");
+    Weight w[REALM_GEMV_MAX_MATS];
+    const Weight *wp[REALM_GEMV_MAX_MATS];
+    for (size_t i = 0; i < count; ++i) {
+        CHECK(get_weight(handles[i], &w[i]));
+        if (w[i].type != w[0].type || w[i].k != w[0].k)
+            return fail(REALM_INVALID_ARGUMENT, "grouped weights must share format and K");
+        wp[i] = &w[i];
+    }
+    CHECK(ensure_init());
+    if (batch > (size_t)INT32_MAX)
+        return fail(REALM_INVALID_ARGUMENT, "batch exceeds 2^31-1");
+    hipStream_t s;
+    CHECK(pick_stream(stream, &s));
+    if (batch == 1) {
+        int rc = run_gemv(wp, (int)count, d_input, d_outs, s);
+        if (rc != REALM_BACKEND_UNSUPPORTED)
+            return rc;
+    }
+    for (size_t i = 0; i < count; ++i)
+        CHECK(run_gemm(w[i], d_input, false, batch, d_outs[i], s, nullptr));
+    return REALM_OK;
 }
 
 REALM_API int realm_hip_weights_matmul_bf16_dev(uint64_t handle, const uint16_t *d_input,

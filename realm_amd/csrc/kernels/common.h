@@ -2,24 +2,28 @@
 //
 // Device layout of a resident [N, K] matrix ("split streams", one region per
 // field, each region 256-byte aligned; built by the repack kernels from the
-// reference's packed blocks):
+// reference's packed blocks).  A row's quant bytes are cut into U = K/64
+// "units" of 64 weights and stored plane-major: plane p of a row holds the
+// p-th 16 bytes of every unit (row bytes [p*U*16 + u*16, +16)), so the 64
+// lanes of a wave that own consecutive units read 1 KB contiguous per load.
 //
 //   Q4_K  hdr[N][K/256][16]  bytes 0..15 of each 144-byte block (d, dmin, scales)
-//         qs [N][K/2]        the 128 quant bytes of each block, in order.
-//         Unit u of a row = qs[32u .. 32u+31] and holds k in [64u, 64u+64):
-//         byte j low nibble -> k = 64u + j, high nibble -> k = 64u + 32 + j
-//         (crates/realm-core/src/quant.rs:155-184).
+//         qs [N][2][U][16]   unit u = qs group g = u%4 of block u/4 (32 bytes,
+//                            halves in planes 0/1): byte j low nibble -> k =
+//                            64u + j, high nibble -> k = 64u + 32 + j
+//                            (crates/realm-core/src/quant.rs:155-184).
 //   Q6_K  d  [N][K/256]      f16 super-block scale
 //         sc [N][K/256][16]  int8 sub-block scales regrouped per unit: unit v
 //                            (v = 2h + is) holds sc[8h+is+2t], t = 0..3
-//         q  [N][K/256][4][48] per unit v: ql[64h+16is .. +16], ql[64h+32+16is
-//                            .. +16], qh[32h+16is .. +16]; element (t, j) of the
-//                            unit is k = 256b + 128h + 16is + 32t + j
-//                            (quant.rs:393-451 regrouped so a unit is 48
-//                            contiguous bytes).
+//         q  [N][3][U][16]   unit u = (block u/4, v = u%4 = 2h + is): planes
+//                            ql[64h+16is ..+16], ql[64h+32+16is ..+16],
+//                            qh[32h+16is ..+16]; element (t, j) of the unit is
+//                            k = 256b + 128h + 16is + 32t + j
+//                            (quant.rs:393-451 regrouped).
 //   Q8_0  d  [N][Kp/32]      f16 block scales
-//         q  [N][Kp]         int8 quants; Kp = K rounded up to 64, the padding
-//                            is zero quants with zero scale.
+//         q  [N][4][U][16]   unit u = blocks 2u, 2u+1 (64 int8 quants, 16 per
+//                            plane); Kp = K rounded up to 64, the padding is
+//                            zero quants with zero scale.
 #pragma once
 
 #include <hip/hip_runtime.h>

@@ -6,14 +6,16 @@
 using namespace realm;
 
 // The reference never contracts `d1 * x - m1` into an FMA
-// (crates/realm-core/src/quant.rs:175,182); neither may we.
-#pragma clang fp contract(off)
+// (crates/realm-core/src/quant.rs:175,182); neither may we.  The pragma is
+// scoped to each dequant kernel body: every other kernel of the code object
+// (one translation unit) keeps FMA contraction.
 
 // quant.rs:127-187.  One thread per qs byte: 128 threads per block, two
 // outputs each (low nibble -> k = 64g + j, high nibble -> k = 64g + 32 + j).
 extern "C" __global__ __launch_bounds__(256) void realm_dequant_q4k(
     const uint8_t *__restrict__ raw, float *__restrict__ out, long long nblocks)
 {
+#pragma clang fp contract(off)
     long long gid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     long long b = gid >> 7;
     if (b >= nblocks)
@@ -44,6 +46,7 @@ extern "C" __global__ __launch_bounds__(256) void realm_dequant_q4k(
 extern "C" __global__ __launch_bounds__(256) void realm_dequant_q6k(
     const uint8_t *__restrict__ raw, float *__restrict__ out, long long nblocks)
 {
+#pragma clang fp contract(off)
     long long gid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     long long b = gid >> 6;
     if (b >= nblocks)
@@ -71,6 +74,7 @@ extern "C" __global__ __launch_bounds__(256) void realm_dequant_q6k(
 extern "C" __global__ __launch_bounds__(256) void realm_dequant_q80(
     const uint8_t *__restrict__ raw, float *__restrict__ out, long long nblocks)
 {
+#pragma clang fp contract(off)
     long long gid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     long long b = gid >> 5;
     if (b >= nblocks)
@@ -84,10 +88,11 @@ extern "C" __global__ __launch_bounds__(256) void realm_dequant_q80(
 // ------------------------------------------------------------------ repack
 
 // Q4_K: a 144-byte block is nine 16-byte pieces (the raw buffer is 256-byte
-// aligned and 144 = 9*16): piece 0 -> hdr, pieces 1..8 -> qs.
+// aligned and 144 = 9*16): piece 0 -> hdr, piece 1 + 2g + h -> plane h of
+// unit 4*kb + g of the block's row.
 extern "C" __global__ __launch_bounds__(256) void realm_repack_q4k(
     const uint8_t *__restrict__ raw, uint8_t *__restrict__ hdr, uint8_t *__restrict__ qs,
-    long long nblocks)
+    long long nblocks, int blocks_per_row)
 {
     long long gid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     long long b = gid / 9;
@@ -95,18 +100,23 @@ extern "C" __global__ __launch_bounds__(256) void realm_repack_q4k(
         return;
     int piece = (int)(gid - b * 9);
     uint4 v = ldg16(raw + b * Q4K_BLOCK_BYTES + 16 * piece);
-    if (piece == 0)
+    if (piece == 0) {
         *reinterpret_cast<uint4 *>(hdr + b * 16) = v;
-    else
-        *reinterpret_cast<uint4 *>(qs + b * 128 + 16 * (piece - 1)) = v;
+        return;
+    }
+    long long row = b / blocks_per_row;
+    int kb = (int)(b - row * blocks_per_row);
+    int g = (piece - 1) >> 1, h = (piece - 1) & 1;
+    long long U = 4LL * blocks_per_row;
+    *reinterpret_cast<uint4 *>(qs + row * (U * 32) + h * (U * 16) + (4 * kb + g) * 16) = v;
 }
 
 // Q6_K: 64 threads per block.  Thread t writes quant bytes t, t+64, t+128 of
-// the block's 192 regrouped bytes, threads 0..15 the regrouped scales and
-// thread 0 the f16 scale.
+// the block's four 48-byte units (unit v: ql_a, ql_b, qh -> planes 0, 1, 2),
+// threads 0..15 the regrouped scales and thread 0 the f16 scale.
 extern "C" __global__ __launch_bounds__(256) void realm_repack_q6k(
     const uint8_t *__restrict__ raw, uint8_t *__restrict__ dq, int8_t *__restrict__ scq,
-    uint8_t *__restrict__ qq, long long nblocks)
+    uint8_t *__restrict__ qq, long long nblocks, int blocks_per_row)
 {
     long long gid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     long long b = gid >> 6;
@@ -114,17 +124,21 @@ extern "C" __global__ __launch_bounds__(256) void realm_repack_q6k(
         return;
     int t = (int)(gid & 63);
     const uint8_t *blk = raw + b * Q6K_BLOCK_BYTES;
+    long long row = b / blocks_per_row;
+    int kb = (int)(b - row * blocks_per_row);
+    long long U = 4LL * blocks_per_row;
     for (int o = t; o < 192; o += 64) {
-        int v = o / 48, r = o - 48 * v;       // unit v, byte r of its 48
+        int v = o / 48, r = o - 48 * v; // unit v, byte r of its 48
         int h = v >> 1, is = v & 1;
+        int plane = r >> 4, j = r & 15;
         uint8_t val;
-        if (r < 16)
-            val = blk[64 * h + 16 * is + r];          // ql_a
-        else if (r < 32)
-            val = blk[64 * h + 32 + 16 * is + (r - 16)]; // ql_b
+        if (plane == 0)
+            val = blk[64 * h + 16 * is + j]; // ql_a
+        else if (plane == 1)
+            val = blk[64 * h + 32 + 16 * is + j]; // ql_b
         else
-            val = blk[128 + 32 * h + 16 * is + (r - 32)]; // qh
-        qq[b * 192 + o] = val;
+            val = blk[128 + 32 * h + 16 * is + j]; // qh
+        qq[row * (U * 48) + plane * (U * 16) + (4 * kb + v) * 16 + j] = val;
     }
     if (t < 16) {
         int v = t >> 2, tt = t & 3;
@@ -137,8 +151,9 @@ extern "C" __global__ __launch_bounds__(256) void realm_repack_q6k(
     }
 }
 
-// Q8_0: one thread per quant byte.  Block (row n, kb) goes to row n of the
-// padded [N][Kp] layout; the destination is zeroed beforehand so the padding
+// Q8_0: one thread per quant byte.  Block (row n, kb) is half kb&1 of unit
+// kb/2 of row n of the padded [N][Kp] layout; byte i sits in plane
+// (32*(kb&1) + i) / 16.  The destination is zeroed beforehand so the padding
 // holds zero quants and zero scales.
 extern "C" __global__ __launch_bounds__(256) void realm_repack_q80(
     const uint8_t *__restrict__ raw, uint8_t *__restrict__ dq, int8_t *__restrict__ qq,
@@ -152,7 +167,9 @@ extern "C" __global__ __launch_bounds__(256) void realm_repack_q80(
     long long n = b / kb_per_row;
     int kb = (int)(b - n * kb_per_row);
     const uint8_t *blk = raw + b * Q80_BLOCK_BYTES;
-    qq[n * kp + 32 * kb + i] = (int8_t)blk[2 + i];
+    int ub = 32 * (kb & 1) + i; // byte of the 64-byte unit
+    long long U = kp / 64;
+    qq[n * kp + (ub >> 4) * (U * 16) + (kb >> 1) * 16 + (ub & 15)] = (int8_t)blk[2 + i];
     if (i < 2)
         dq[(n * (kp / 32) + kb) * 2 + i] = blk[i];
 }

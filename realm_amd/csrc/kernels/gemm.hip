@@ -219,9 +219,10 @@ REALM_DEV void gemm_body(const GemmArgs &g)
                 int row = n0 + 16 * a + r16;
                 uint4 q0 = make_uint4(0, 0, 0, 0), q1 = q0, hd = q0;
                 if (row < N) {
-                    const uint8_t *qp = qs + (size_t)row * (K >> 1) + 128 * b + 32 * c;
-                    q0 = ldg16(qp);
-                    q1 = ldg16(qp + 16);
+                    const size_t U = (size_t)(K >> 6);
+                    const uint8_t *qp = qs + (size_t)row * (U * 32) + (4 * b + c) * 16;
+                    q0 = ldg16(qp);          // plane 0
+                    q1 = ldg16(qp + U * 16); // plane 1
                     hd = ldg16(hdr + ((size_t)row * B + b) * 16);
                 }
                 w[a][0] = q0.x; w[a][1] = q0.y; w[a][2] = q0.z; w[a][3] = q0.w;
@@ -314,11 +315,11 @@ REALM_DEV void gemm_body(const GemmArgs &g)
                 uint4 A = make_uint4(0, 0, 0, 0), Bq = A, H = A;
                 uint32_t scw = 0, dbits = 0;
                 if (row < N) {
-                    size_t blk = (size_t)row * B + b;
-                    const uint8_t *qp = qq + (blk * 4 + c) * 48;
+                    size_t blk = (size_t)row * B + b, U = 4 * (size_t)B;
+                    const uint8_t *qp = qq + (size_t)row * (U * 48) + (4 * b + c) * 16;
                     A = ldg16(qp);
-                    Bq = ldg16(qp + 16);
-                    H = ldg16(qp + 32);
+                    Bq = ldg16(qp + U * 16);
+                    H = ldg16(qp + U * 32);
                     scw = ldg4(scq + blk * 16 + 4 * c);
                     dbits = *reinterpret_cast<const uint16_t *>(dq + blk * 2);
                 }
@@ -415,7 +416,11 @@ REALM_DEV void gemm_body(const GemmArgs &g)
                 uint2 q = make_uint2(0, 0);
                 uint32_t dbits = 0;
                 if (row < N) {
-                    q = ldg8(qq + (size_t)row * KX + 32 * kb + 8 * c);
+                    // bytes 32kb + 8c .. +7 of the row: unit kb/2, byte 32(kb&1)
+                    // + 8c -> plane 2(kb&1) + c/2, offset 8(c&1)
+                    const size_t U = (size_t)(KX >> 6);
+                    q = ldg8(qq + (size_t)row * KX + (2 * (kb & 1) + (c >> 1)) * (U * 16) +
+                             (kb >> 1) * 16 + 8 * (c & 1));
                     dbits = *reinterpret_cast<const uint16_t *>(dq + ((size_t)row * B32 + kb) * 2);
                 }
                 float d = f16_bits_to_f32(dbits);

@@ -1,54 +1,165 @@
 // Decode GEMV, one token: y[n] = sum_k W[n,k] x[k] for resident Q4_K / Q6_K /
-// Q8_0 weights in the device layout of common.h.
+// Q8_0 weights in the device layout of common.h, up to 4 matrices that share
+// x per launch (rows concatenated: e.g. Q/K/V, or gate/up).
+//
+// Arithmetic: integer dot products.  Each workgroup first quantizes x per
+// 32-element block b into two int8 planes, scale s_b = amax_b / 127:
+//   xh = round(x / s_b),  xl = round((x - s_b*xh) * 254 / s_b)
+//   x ~= s_b * (xh + xl/254),  |error| <= amax_b / (127*508) = 1.55e-5 * amax_b.
+// Weights stay exact small integers (Q4_K 0..15, Q6_K 0..63 before the -32
+// offset, Q8_0 -127..127), so v_dot4_i32_i8 accumulates 4 exact products per
+// instruction in int32.  Per 32 (Q6_K: 16) weights the two int32 sums become
+// s_b*(Ph + Pl/254) in f32 and take the block scales; the Q4_K min term and
+// the Q6_K -32 offset use the exact integer sums of the quantized x.
 //
 // Work decomposition: a row is cut into U "units" of 64 weights (Q4_K: one
 // 32-byte qs group + the block header; Q6_K: one 48-byte ql/qh group + 4
 // sub-scales + d; Q8_0: two 34-byte blocks).  LPR lanes share a row; lane l
-// owns units l, l+LPR, ... (UPL of them) of every row it visits, and the wave
-// handles 64/LPR row slots with R rows each per pass, grid-striding over
-// passes.  x (f32) is staged once per workgroup in LDS and each lane keeps the
-// per-unit sums of x it needs (Sx), so the Q4_K min term and the Q6_K / Q8_0
-// offsets (-32, +128 bias) cost nothing per weight.  All R rows of a pass are
-// loaded before any is consumed (memory-level parallelism), and each x value
-// read from LDS is applied to R rows.
+// owns units l, l+LPR, ... (UPL of them) of every row it visits, and a wave
+// handles 64/LPR row slots of R rows per pass.  The grid is persistent: each
+// wave strides over passes and keeps two in flight (the next pass's weights
+// load while the current one computes).  Quantized x lives in LDS as one
+// 16-byte record per (unit, dword position), laid out [position][unit], so
+// lanes of a wave read consecutive records (no bank conflicts).
 #include "common.h"
+#include "kernel_args.h"
 
 using namespace realm;
+using realm::GemvArgs;
+
+#define FMT_Q4K 0
+#define FMT_Q6K 1
+#define FMT_Q80 2
 
 namespace {
-
-template <int LPR>
-struct Lanes {
-    static constexpr int RPW = 64 / LPR; // row slots per wave
-};
-
-// Stage x[0..K) into LDS xs[0..KX), zero padding past K.
-REALM_DEV void stage_x(float *xs, const float *__restrict__ x, int K, int KX)
-{
-    const float4 *x4 = reinterpret_cast<const float4 *>(x);
-    float4 *xs4 = reinterpret_cast<float4 *>(xs);
-    for (int i = threadIdx.x; i < KX / 4; i += blockDim.x)
-        xs4[i] = (4 * i < K) ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-    __syncthreads();
-}
-
-REALM_DEV float dot4(uint32_t w, float4 x, float acc)
-{
-    acc += ubyte0(w) * x.x;
-    acc += ubyte1(w) * x.y;
-    acc += ubyte2(w) * x.z;
-    acc += ubyte3(w) * x.w;
-    return acc;
-}
 
 REALM_DEV uint32_t word(const uint4 &v, int i)
 {
     return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
 }
 
-REALM_DEV float4 lds4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
+REALM_DEV int dot4(uint32_t a, uint32_t b, int c)
+{
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
 
-// ------------------------------------------------------------------- Q4_K
+template <int CTRL, int ROW_MASK>
+REALM_DEV float dpp_f(float x)
+{
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, ROW_MASK, 0xF,
+                                           false));
+}
+
+// Sum over the LPR lanes of a lane group with DPP (quad swaps, row
+// rotations, row broadcasts); the total lands in the group's last lane.
+template <int LPR>
+REALM_DEV float group_total(float v)
+{
+    v += dpp_f<0xB1, 0xF>(v);  // quad_perm [1,0,3,2]
+    v += dpp_f<0x4E, 0xF>(v);  // quad_perm [2,3,0,1]
+    v += dpp_f<0x124, 0xF>(v); // row_ror:4
+    v += dpp_f<0x128, 0xF>(v); // row_ror:8  -> every lane holds its row's sum
+    if (LPR >= 32)
+        v += dpp_f<0x142, 0xA>(v); // row_bcast:15 into rows 1 and 3
+    if (LPR >= 64)
+        v += dpp_f<0x143, 0xC>(v); // row_bcast:31 into rows 2 and 3
+    return v;
+}
+
+// Max over aligned groups of 8 lanes (one x block of 32 = 8 x float4) and sum
+// over aligned groups of 4 (one 16-element half block).
+REALM_DEV float max8(float v)
+{
+    v = fmaxf(v, __shfl_xor(v, 1, 64));
+    v = fmaxf(v, __shfl_xor(v, 2, 64));
+    return fmaxf(v, __shfl_xor(v, 4, 64));
+}
+REALM_DEV int sum4i(int v)
+{
+    v += __shfl_xor(v, 1, 64);
+    return v + __shfl_xor(v, 2, 64);
+}
+
+REALM_DEV uint32_t pack4(int a, int b, int c, int d)
+{
+    return (uint32_t)(a & 0xFF) | ((uint32_t)(b & 0xFF) << 8) | ((uint32_t)(c & 0xFF) << 16) |
+           ((uint32_t)(d & 0xFF) << 24);
+}
+
+// Quantize x into LDS.  rec[pos * U + u] (int4) holds, for unit u and dword
+// position pos, the xh and xl dwords its dot products need:
+//   Q4_K / Q8_0 (unit = x blocks 2u, 2u+1; pos = i in 0..7):
+//     (xh, xl of block 2u elements 4i..4i+3, xh, xl of block 2u+1 elements 4i..)
+//   Q6_K (unit = 16-runs t = 0..3 of one 64-weight group; pos = 2i + (t>>1)):
+//     (xh, xl of run t = 2(pos&1) elements 4i.., xh, xl of run t+1 ...)
+// meta[u] (float4; Q6_K: two float4 per unit) holds the x-block scales and
+// the sums s*(sum xh + sum xl/254) of the elements the unit covers.
+//
+// Round rd covers 4-element chunks gid = rd*blockDim + tid, i.e. x block
+// gid/8, chunk gid%8.  x_round() loads one round; quant_round() quantizes it.
+REALM_DEV float4 x_round(const float *__restrict__ x, int K, int U, int rd)
+{
+    const int gid = rd * blockDim.x + threadIdx.x;
+    const int blk = gid >> 3, c8 = gid & 7;
+    const int e0 = 32 * blk + 4 * c8;
+    return (blk < 2 * U && e0 < K) ? reinterpret_cast<const float4 *>(x)[e0 >> 2]
+                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+}
+
+template <int FMT>
+REALM_DEV void quant_round(int4 *rec, float4 *meta, float4 v, int U, int rd)
+{
+    const int gid = rd * blockDim.x + threadIdx.x;
+    const int blk = gid >> 3, c8 = gid & 7;
+    const bool live = blk < 2 * U;
+    float amax = max8(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    const float s = amax * (1.f / 127.f);
+    const float inv = amax > 0.f ? 127.f / amax : 0.f;
+    const float inv2 = amax > 0.f ? 254.f * 127.f / amax : 0.f;
+    const float xs[4] = {v.x, v.y, v.z, v.w};
+    int h[4], lo[4], sh = 0, sl = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        h[e] = (int)rintf(xs[e] * inv);
+        lo[e] = max(-127, min(127, (int)rintf((xs[e] - s * (float)h[e]) * inv2)));
+        sh += h[e];
+        sl += lo[e];
+    }
+    sh = sum4i(sh);
+    sl = sum4i(sl);
+    const float part = s * ((float)sh + (float)sl * (1.f / 254.f)); // 16 elements
+    const float other = __shfl_xor(part, 4, 64);                      // the other half
+    if (!live)
+        return;
+    const uint32_t dh = pack4(h[0], h[1], h[2], h[3]);
+    const uint32_t dl = pack4(lo[0], lo[1], lo[2], lo[3]);
+    if (FMT == FMT_Q6K) {
+        // x block blk of the 256-block B: h6 = (blk%8)/4, run t = blk%4; the
+        // chunk lies in 16-run is = c8/4 at dword position i = c8%4
+        const int B = blk >> 3, h6 = (blk >> 2) & 1, t = blk & 3;
+        const int is = c8 >> 2, i = c8 & 3;
+        const int u = 4 * B + 2 * h6 + is;
+        int *r = reinterpret_cast<int *>(&rec[(2 * i + (t >> 1)) * U + u]);
+        r[2 * (t & 1)] = (int)dh;
+        r[2 * (t & 1) + 1] = (int)dl;
+        if (i == 0) {
+            float *m = reinterpret_cast<float *>(&meta[2 * u]);
+            m[t] = s;        // scale of run t
+            m[4 + t] = part; // sum over the run's 16 elements
+        }
+    } else {
+        const int u = blk >> 1, half = blk & 1, i = c8;
+        int *r = reinterpret_cast<int *>(&rec[i * U + u]);
+        r[2 * half] = (int)dh;
+        r[2 * half + 1] = (int)dl;
+        if (c8 == 0) {
+            float *m = reinterpret_cast<float *>(&meta[u]);
+            m[half] = s;
+            m[2 + half] = part + other; // whole block of 32
+        }
+    }
+}
 
 // Scale/min pair for sub-blocks 2g and 2g+1 from header dwords s0,s1,s2
 // (crates/realm-core/src/quant.rs:110-122) with g known only at run time.
@@ -75,363 +186,318 @@ REALM_DEV void q4k_pair_rt(uint32_t s0, uint32_t s1, uint32_t s2, int g, float &
     m_hi = (float)mh;
 }
 
-template <int LPR, int UPL, int R>
-REALM_DEV void gemv_q4k(const uint8_t *__restrict__ hdr, const uint8_t *__restrict__ qs,
-                        const float *__restrict__ x, float *__restrict__ y, int N, int K,
-                        int nan_fb)
-{
-    extern __shared__ float xs[];
-    const int U = K >> 6, B = K >> 8;
-    stage_x(xs, x, K, K);
-    const int lane = threadIdx.x & 63;
-    const int slot = lane / LPR, l = lane % LPR;
-    const int wpb = blockDim.x >> 6;
-    const int gw = blockIdx.x * wpb + (threadIdx.x >> 6);
-    const int nw = gridDim.x * wpb;
+// Per-format weight registers of one (row, unit) and their loader.
+template <int FMT>
+struct Unit;
 
-    float sxl[UPL], sxh[UPL];
-#pragma unroll
-    for (int j = 0; j < UPL; ++j) {
-        int u = l + j * LPR;
-        float a = 0.f, b = 0.f;
-        if (u < U) {
-            const float *xu = xs + 64 * u;
-#pragma unroll
-            for (int i = 0; i < 32; i += 4) {
-                float4 v = lds4(xu + i), w = lds4(xu + 32 + i);
-                a += (v.x + v.y) + (v.z + v.w);
-                b += (w.x + w.y) + (w.z + w.w);
-            }
-        }
-        sxl[j] = a;
-        sxh[j] = b;
+template <>
+struct Unit<FMT_Q4K> {
+    uint4 q0, q1, hd;
+    __device__ __forceinline__ void load(const uint8_t *w0, const uint8_t *w1, const uint8_t *,
+                                         size_t row, int u, int K)
+    {
+        const size_t U = (size_t)(K >> 6);
+        const uint8_t *qp = w1 + row * (U * 32) + 16 * u;
+        q0 = ldg16(qp);          // plane 0
+        q1 = ldg16(qp + U * 16); // plane 1
+        hd = ldg16(w0 + (row * (size_t)(K >> 8) + (u >> 2)) * 16);
     }
+    __device__ __forceinline__ void zero() { q0 = q1 = hd = make_uint4(0, 0, 0, 0); }
+};
 
-    constexpr int RPP = Lanes<LPR>::RPW * R; // rows per pass per wave
-    const int npass = (N + RPP - 1) / RPP;
-    for (int p = gw; p < npass; p += nw) {
-        const int r0 = p * RPP + slot * R;
-        uint4 q0[R][UPL], q1[R][UPL], hd[R][UPL];
+template <>
+struct Unit<FMT_Q6K> {
+    uint4 qa, qb, qh;
+    uint32_t sc, d;
+    __device__ __forceinline__ void load(const uint8_t *w0, const uint8_t *w1, const uint8_t *w2,
+                                         size_t row, int u, int K)
+    {
+        size_t B = (size_t)(K >> 8), U = 4 * B;
+        const uint8_t *qp = w2 + row * (U * 48) + 16 * u;
+        qa = ldg16(qp);
+        qb = ldg16(qp + U * 16);
+        qh = ldg16(qp + U * 32);
+        size_t blk = row * B + (u >> 2);
+        sc = ldg4(w1 + blk * 16 + 4 * (u & 3));
+        d = *reinterpret_cast<const uint16_t *>(w0 + blk * 2);
+    }
+    __device__ __forceinline__ void zero()
+    {
+        qa = qb = qh = make_uint4(0, 0, 0, 0);
+        sc = d = 0;
+    }
+};
+
+template <>
+struct Unit<FMT_Q80> {
+    uint4 q[4];
+    uint32_t d;
+    // K here is the padded row length Kp
+    __device__ __forceinline__ void load(const uint8_t *w0, const uint8_t *w1, const uint8_t *,
+                                         size_t row, int u, int KP)
+    {
+        const size_t U = (size_t)(KP >> 6);
+        const uint8_t *qp = w1 + row * (size_t)KP + 16 * u;
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            q[c] = ldg16(qp + c * (U * 16));
+        d = ldg4(w0 + (row * (size_t)(KP >> 5) + 2 * u) * 2);
+    }
+    __device__ __forceinline__ void zero()
+    {
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            q[c] = make_uint4(0, 0, 0, 0);
+        d = 0;
+    }
+};
+
+REALM_DEV float combine(int ph, int pl, float s)
+{
+    return s * ((float)ph + (float)pl * (1.f / 254.f));
+}
+
+// Partial dot products of R rows with one unit of x.
+template <int FMT, int R>
+REALM_DEV void unit_dot(const Unit<FMT> (&w)[R], const int4 *rec, const float4 *meta, int U,
+                        int u, int nan_fb, float (&acc)[R])
+{
+    if constexpr (FMT == FMT_Q4K) {
+        int hl[R], ll[R], hh[R], lh[R];
 #pragma unroll
         for (int r = 0; r < R; ++r)
+            hl[r] = ll[r] = hh[r] = lh[r] = 0;
 #pragma unroll
-            for (int j = 0; j < UPL; ++j) {
-                int row = r0 + r, u = l + j * LPR;
-                if (row < N && u < U) {
-                    const uint8_t *qp = qs + (size_t)row * (K >> 1) + 32 * u;
-                    q0[r][j] = ldg16(qp);
-                    q1[r][j] = ldg16(qp + 16);
-                    hd[r][j] = ldg16(hdr + ((size_t)row * B + (u >> 2)) * 16);
-                } else {
-                    q0[r][j] = q1[r][j] = hd[r][j] = make_uint4(0, 0, 0, 0);
-                }
-            }
-        float acc[R];
+        for (int i = 0; i < 8; ++i) {
+            const int4 xq = rec[i * U + u];
 #pragma unroll
-        for (int r = 0; r < R; ++r)
-            acc[r] = 0.f;
-#pragma unroll
-        for (int j = 0; j < UPL; ++j) {
-            int u = l + j * LPR;
-            if (u < U) {
-                const float *xu = xs + 64 * u;
-                float dl[R], dh[R];
-#pragma unroll
-                for (int r = 0; r < R; ++r)
-                    dl[r] = dh[r] = 0.f;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    float4 xl = lds4(xu + 4 * i), xh = lds4(xu + 32 + 4 * i);
-#pragma unroll
-                    for (int r = 0; r < R; ++r) {
-                        uint32_t w = word(i < 4 ? q0[r][j] : q1[r][j], i & 3);
-                        dl[r] = dot4(w & 0x0F0F0F0Fu, xl, dl[r]);
-                        dh[r] = dot4((w >> 4) & 0x0F0F0F0Fu, xh, dh[r]);
-                    }
-                }
-                int g = u & 3;
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    float d = fix_scale(f16_bits_to_f32(hd[r][j].x), 0.00000006f, nan_fb);
-                    float dm = fix_scale(f16_bits_to_f32(hd[r][j].x >> 16), 0.00000024f, nan_fb);
-                    float sl, ml, sh, mh;
-                    q4k_pair_rt(hd[r][j].y, hd[r][j].z, hd[r][j].w, g, sl, ml, sh, mh);
-                    acc[r] += (d * sl) * dl[r] + (d * sh) * dh[r] -
-                              ((dm * ml) * sxl[j] + (dm * mh) * sxh[j]);
-                }
+            for (int r = 0; r < R; ++r) {
+                uint32_t q = word(i < 4 ? w[r].q0 : w[r].q1, i & 3);
+                uint32_t lo = q & 0x0F0F0F0Fu, hi = (q >> 4) & 0x0F0F0F0Fu;
+                hl[r] = dot4(lo, (uint32_t)xq.x, hl[r]);
+                ll[r] = dot4(lo, (uint32_t)xq.y, ll[r]);
+                hh[r] = dot4(hi, (uint32_t)xq.z, hh[r]);
+                lh[r] = dot4(hi, (uint32_t)xq.w, lh[r]);
             }
         }
+        const float4 m = meta[u]; // (s_lo, s_hi, sum_lo, sum_hi)
+        const int g = u & 3;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            float v = group_sum<LPR>(acc[r]);
-            int row = r0 + r;
-            if (l == 0 && row < N)
-                y[row] = v;
+            float d = fix_scale(f16_bits_to_f32(w[r].hd.x), 0.00000006f, nan_fb);
+            float dm = fix_scale(f16_bits_to_f32(w[r].hd.x >> 16), 0.00000024f, nan_fb);
+            float sl, ml, sh, mh;
+            q4k_pair_rt(w[r].hd.y, w[r].hd.z, w[r].hd.w, g, sl, ml, sh, mh);
+            acc[r] += d * (sl * combine(hl[r], ll[r], m.x) + sh * combine(hh[r], lh[r], m.y)) -
+                      dm * (ml * m.z + mh * m.w);
+        }
+    } else if constexpr (FMT == FMT_Q6K) {
+        int ph[R][4], pl[R][4];
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                ph[r][t] = pl[r][t] = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int4 x01 = rec[(2 * i) * U + u], x23 = rec[(2 * i + 1) * U + u];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                uint32_t a = word(w[r].qa, i), b = word(w[r].qb, i), h = word(w[r].qh, i);
+                uint32_t v0 = (a & 0x0F0F0F0Fu) | ((h << 4) & 0x30303030u);
+                uint32_t v1 = (b & 0x0F0F0F0Fu) | ((h << 2) & 0x30303030u);
+                uint32_t v2 = ((a >> 4) & 0x0F0F0F0Fu) | (h & 0x30303030u);
+                uint32_t v3 = ((b >> 4) & 0x0F0F0F0Fu) | ((h >> 2) & 0x30303030u);
+                ph[r][0] = dot4(v0, (uint32_t)x01.x, ph[r][0]);
+                pl[r][0] = dot4(v0, (uint32_t)x01.y, pl[r][0]);
+                ph[r][1] = dot4(v1, (uint32_t)x01.z, ph[r][1]);
+                pl[r][1] = dot4(v1, (uint32_t)x01.w, pl[r][1]);
+                ph[r][2] = dot4(v2, (uint32_t)x23.x, ph[r][2]);
+                pl[r][2] = dot4(v2, (uint32_t)x23.y, pl[r][2]);
+                ph[r][3] = dot4(v3, (uint32_t)x23.z, ph[r][3]);
+                pl[r][3] = dot4(v3, (uint32_t)x23.w, pl[r][3]);
+            }
+        }
+        const float4 ms = meta[2 * u], mx = meta[2 * u + 1]; // run scales, run sums
+        const float s[4] = {ms.x, ms.y, ms.z, ms.w}, sx[4] = {mx.x, mx.y, mx.z, mx.w};
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            float d = fix_scale(f16_bits_to_f32(w[r].d), 0.00000006f, nan_fb);
+            float part = 0.f;
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                part += (float)(int8_t)(w[r].sc >> (8 * t)) *
+                        (combine(ph[r][t], pl[r][t], s[t]) - 32.f * sx[t]);
+            acc[r] += d * part;
+        }
+    } else {
+        int ha[R], la[R], hb[R], lb[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            ha[r] = la[r] = hb[r] = lb[r] = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int4 xq = rec[i * U + u];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                uint32_t qa = word(w[r].q[i >> 2], i & 3);
+                uint32_t qb = word(w[r].q[2 + (i >> 2)], i & 3);
+                ha[r] = dot4(qa, (uint32_t)xq.x, ha[r]);
+                la[r] = dot4(qa, (uint32_t)xq.y, la[r]);
+                hb[r] = dot4(qb, (uint32_t)xq.z, hb[r]);
+                lb[r] = dot4(qb, (uint32_t)xq.w, lb[r]);
+            }
+        }
+        const float4 m = meta[u];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            float da = f16_bits_to_f32(w[r].d), db = f16_bits_to_f32(w[r].d >> 16);
+            acc[r] += da * combine(ha[r], la[r], m.x) + db * combine(hb[r], lb[r], m.y);
         }
     }
 }
 
-// ------------------------------------------------------------------- Q6_K
-
-template <int LPR, int UPL, int R>
-REALM_DEV void gemv_q6k(const uint8_t *__restrict__ dq, const int8_t *__restrict__ scq,
-                        const uint8_t *__restrict__ qq, const float *__restrict__ x,
-                        float *__restrict__ y, int N, int K, int nan_fb)
+template <int FMT, int LPR, int UPL, int R, int XR>
+REALM_DEV void gemv(const GemvArgs &a)
 {
-    extern __shared__ float xs[];
-    const int U = K >> 6, B = K >> 8;
-    stage_x(xs, x, K, K);
+    extern __shared__ int4 lds[];
+    const int K = a.K, KX = a.KX;
+    const int U = KX >> 6;
+    int4 *rec = lds;
+    float4 *meta = reinterpret_cast<float4 *>(lds + 8 * U);
     const int lane = threadIdx.x & 63;
     const int slot = lane / LPR, l = lane % LPR;
     const int wpb = blockDim.x >> 6;
-    const int gw = blockIdx.x * wpb + (threadIdx.x >> 6);
+    // wave-uniform: keeps pass/row/matrix bookkeeping (and the kernarg
+    // pointer tables) in scalar registers, out of the vector memory queue
+    const int gw = __builtin_amdgcn_readfirstlane(blockIdx.x * wpb + (threadIdx.x >> 6));
     const int nw = gridDim.x * wpb;
+    constexpr int RPP = (64 / LPR) * R; // rows per pass per wave
+    const int rs1 = a.row_start[1], rs2 = a.row_start[2], rs3 = a.row_start[3];
+    const int rows = a.row_start[REALM_GEMV_MAX_MATS];
+    const int npass = (rows + RPP - 1) / RPP;
+    const int wk = FMT == FMT_Q80 ? KX : K; // row length of the quant stream
 
-    // unit u: block u>>2, v = u&3, h = v>>1, is = v&1; element (t, j) at
-    // x[256b + 128h + 16is + 32t + j].
-    float sx[UPL][4];
-#pragma unroll
-    for (int j = 0; j < UPL; ++j) {
-        int u = l + j * LPR;
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-            sx[j][t] = 0.f;
-        if (u < U) {
-            int v = u & 3;
-            const float *xu = xs + 256 * (u >> 2) + 128 * (v >> 1) + 16 * (v & 1);
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                float s = 0.f;
-#pragma unroll
-                for (int i = 0; i < 16; i += 4) {
-                    float4 a = lds4(xu + 32 * t + i);
-                    s += (a.x + a.y) + (a.z + a.w);
-                }
-                sx[j][t] = s;
-            }
-        }
-    }
-
-    constexpr int RPP = Lanes<LPR>::RPW * R;
-    const int npass = (N + RPP - 1) / RPP;
-    for (int p = gw; p < npass; p += nw) {
+    // matrix of a global row; pointer choice by selects, never by indexing
+    // the kernarg arrays with a per-lane value
+    auto mat_of = [&](int row) {
+        return (row >= rs1 ? 1 : 0) + (row >= rs2 ? 1 : 0) + (row >= rs3 ? 1 : 0);
+    };
+    auto pick = [](int m, auto v0, auto v1, auto v2, auto v3) {
+        return m == 0 ? v0 : (m == 1 ? v1 : (m == 2 ? v2 : v3));
+    };
+    // No branch writes the registers of an in-flight load (a branch makes the
+    // compiler wait for every outstanding load): a row past the end is
+    // clamped to the last row and a unit past the end to the last unit; the
+    // results of both are masked in finish.
+    auto load_pass = [&](Unit<FMT>(&w)[UPL][R], int p) {
         const int r0 = p * RPP + slot * R;
-        uint4 qa[R][UPL], qb[R][UPL], qh[R][UPL];
-        uint32_t scw[R][UPL], dw[R][UPL];
 #pragma unroll
-        for (int r = 0; r < R; ++r)
+        for (int r = 0; r < R; ++r) {
+            const int row = min(r0 + r, rows - 1);
+            const int m = mat_of(row);
+            const size_t lr = (size_t)(row - pick(m, 0, rs1, rs2, rs3));
+            const uint8_t *p0 = (const uint8_t *)pick(m, a.w0[0], a.w0[1], a.w0[2], a.w0[3]);
+            const uint8_t *p1 = (const uint8_t *)pick(m, a.w1[0], a.w1[1], a.w1[2], a.w1[3]);
+            const uint8_t *p2 = (const uint8_t *)pick(m, a.w2[0], a.w2[1], a.w2[2], a.w2[3]);
 #pragma unroll
-            for (int j = 0; j < UPL; ++j) {
-                int row = r0 + r, u = l + j * LPR;
-                if (row < N && u < U) {
-                    const uint8_t *qp = qq + ((size_t)row * B * 4 + u) * 48;
-                    qa[r][j] = ldg16(qp);
-                    qb[r][j] = ldg16(qp + 16);
-                    qh[r][j] = ldg16(qp + 32);
-                    size_t blk = (size_t)row * B + (u >> 2);
-                    scw[r][j] = ldg4(scq + blk * 16 + 4 * (u & 3));
-                    dw[r][j] = *reinterpret_cast<const uint16_t *>(dq + blk * 2);
-                } else {
-                    qa[r][j] = qb[r][j] = qh[r][j] = make_uint4(0, 0, 0, 0);
-                    scw[r][j] = dw[r][j] = 0;
-                }
-            }
+            for (int j = 0; j < UPL; ++j)
+                w[j][r].load(p0, p1, p2, lr, min(l + j * LPR, U - 1), wk);
+        }
+    };
+    auto finish = [&](Unit<FMT>(&w)[UPL][R], int pp) {
         float acc[R];
 #pragma unroll
         for (int r = 0; r < R; ++r)
             acc[r] = 0.f;
 #pragma unroll
         for (int j = 0; j < UPL; ++j) {
-            int u = l + j * LPR;
-            if (u < U) {
-                int v = u & 3;
-                const float *xu = xs + 256 * (u >> 2) + 128 * (v >> 1) + 16 * (v & 1);
-                float pt[R][4];
+            const int u = l + j * LPR;
+            float part[R];
 #pragma unroll
-                for (int r = 0; r < R; ++r)
+            for (int r = 0; r < R; ++r)
+                part[r] = 0.f;
+            unit_dot<FMT, R>(w[j], rec, meta, U, min(u, U - 1), a.nan_fb, part);
 #pragma unroll
-                    for (int t = 0; t < 4; ++t)
-                        pt[r][t] = 0.f;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    float4 x0 = lds4(xu + 4 * i), x1 = lds4(xu + 32 + 4 * i);
-                    float4 x2 = lds4(xu + 64 + 4 * i), x3 = lds4(xu + 96 + 4 * i);
-#pragma unroll
-                    for (int r = 0; r < R; ++r) {
-                        uint32_t a = word(qa[r][j], i), b = word(qb[r][j], i);
-                        uint32_t h = word(qh[r][j], i);
-                        uint32_t v0 = (a & 0x0F0F0F0Fu) | ((h << 4) & 0x30303030u);
-                        uint32_t v1 = (b & 0x0F0F0F0Fu) | ((h << 2) & 0x30303030u);
-                        uint32_t v2 = ((a >> 4) & 0x0F0F0F0Fu) | (h & 0x30303030u);
-                        uint32_t v3 = ((b >> 4) & 0x0F0F0F0Fu) | ((h >> 2) & 0x30303030u);
-                        pt[r][0] = dot4(v0, x0, pt[r][0]);
-                        pt[r][1] = dot4(v1, x1, pt[r][1]);
-                        pt[r][2] = dot4(v2, x2, pt[r][2]);
-                        pt[r][3] = dot4(v3, x3, pt[r][3]);
-                    }
-                }
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    float d = fix_scale(f16_bits_to_f32(dw[r][j]), 0.00000006f, nan_fb);
-                    uint32_t s = scw[r][j];
-                    float part = 0.f;
-#pragma unroll
-                    for (int t = 0; t < 4; ++t) {
-                        float sc = (float)(int8_t)(s >> (8 * t));
-                        part += sc * (pt[r][t] - 32.f * sx[j][t]);
-                    }
-                    acc[r] += d * part;
-                }
-            }
+            for (int r = 0; r < R; ++r)
+                acc[r] += u < U ? part[r] : 0.f;
         }
+        const int r0 = pp * RPP + slot * R;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            float v = group_sum<LPR>(acc[r]);
-            int row = r0 + r;
-            if (l == 0 && row < N)
-                y[row] = v;
-        }
-    }
-}
-
-// ------------------------------------------------------------------- Q8_0
-
-template <int LPR, int UPL, int R>
-REALM_DEV void gemv_q80(const uint8_t *__restrict__ dq, const int8_t *__restrict__ qq,
-                        const float *__restrict__ x, float *__restrict__ y, int N, int K,
-                        int KP)
-{
-    extern __shared__ float xs[];
-    const int U = KP >> 6;
-    stage_x(xs, x, K, KP);
-    const int lane = threadIdx.x & 63;
-    const int slot = lane / LPR, l = lane % LPR;
-    const int wpb = blockDim.x >> 6;
-    const int gw = blockIdx.x * wpb + (threadIdx.x >> 6);
-    const int nw = gridDim.x * wpb;
-
-    float s0[UPL], s1[UPL];
-#pragma unroll
-    for (int j = 0; j < UPL; ++j) {
-        int u = l + j * LPR;
-        float a = 0.f, b = 0.f;
-        if (u < U) {
-            const float *xu = xs + 64 * u;
-#pragma unroll
-            for (int i = 0; i < 32; i += 4) {
-                float4 v = lds4(xu + i), w = lds4(xu + 32 + i);
-                a += (v.x + v.y) + (v.z + v.w);
-                b += (w.x + w.y) + (w.z + w.w);
+            float v = group_total<LPR>(acc[r]);
+            const int row = r0 + r;
+            if (l == LPR - 1 && row < rows) {
+                const int m = mat_of(row);
+                float *y = pick(m, a.y[0], a.y[1], a.y[2], a.y[3]);
+                y[row - pick(m, 0, rs1, rs2, rs3)] = v;
             }
         }
-        s0[j] = a;
-        s1[j] = b;
-    }
+    };
 
-    constexpr int RPP = Lanes<LPR>::RPW * R;
-    const int npass = (N + RPP - 1) / RPP;
-    for (int p = gw; p < npass; p += nw) {
-        const int r0 = p * RPP + slot * R;
-        uint4 q[R][UPL][4];
-        uint32_t dw[R][UPL];
+    // Prologue: x loads first (so waiting for x does not wait for weights),
+    // then the weights of the wave's first two passes, then x is quantized
+    // into LDS while those loads are in flight.
+    const int rounds = (16 * U + blockDim.x - 1) / blockDim.x;
+    float4 xv[XR];
 #pragma unroll
-        for (int r = 0; r < R; ++r)
+    for (int rd = 0; rd < XR; ++rd)
+        xv[rd] = rd < rounds ? x_round(a.x, K, U, rd) : make_float4(0.f, 0.f, 0.f, 0.f);
+    Unit<FMT> A[UPL][R], B[UPL][R];
+    int p = gw;
+    load_pass(A, p);
+    load_pass(B, p + nw);
 #pragma unroll
-            for (int j = 0; j < UPL; ++j) {
-                int row = r0 + r, u = l + j * LPR;
-                if (row < N && u < U) {
-                    const int8_t *qp = qq + (size_t)row * KP + 64 * u;
-#pragma unroll
-                    for (int c = 0; c < 4; ++c)
-                        q[r][j][c] = ldg16(qp + 16 * c);
-                    dw[r][j] = ldg4(dq + ((size_t)row * (KP >> 5) + 2 * u) * 2);
-                } else {
-#pragma unroll
-                    for (int c = 0; c < 4; ++c)
-                        q[r][j][c] = make_uint4(0, 0, 0, 0);
-                    dw[r][j] = 0;
-                }
-            }
-        float acc[R];
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-            acc[r] = 0.f;
-#pragma unroll
-        for (int j = 0; j < UPL; ++j) {
-            int u = l + j * LPR;
-            if (u < U) {
-                const float *xu = xs + 64 * u;
-                float pa[R], pb[R];
-#pragma unroll
-                for (int r = 0; r < R; ++r)
-                    pa[r] = pb[r] = 0.f;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    float4 xa = lds4(xu + 4 * i), xb = lds4(xu + 32 + 4 * i);
-#pragma unroll
-                    for (int r = 0; r < R; ++r) {
-                        // bytes biased to unsigned: (q + 128)
-                        uint32_t wa = word(q[r][j][i >> 2], i & 3) ^ 0x80808080u;
-                        uint32_t wb = word(q[r][j][2 + (i >> 2)], i & 3) ^ 0x80808080u;
-                        pa[r] = dot4(wa, xa, pa[r]);
-                        pb[r] = dot4(wb, xb, pb[r]);
-                    }
-                }
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    float da = f16_bits_to_f32(dw[r][j]);
-                    float db = f16_bits_to_f32(dw[r][j] >> 16);
-                    acc[r] += da * (pa[r] - 128.f * s0[j]) + db * (pb[r] - 128.f * s1[j]);
-                }
-            }
-        }
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            float v = group_sum<LPR>(acc[r]);
-            int row = r0 + r;
-            if (l == 0 && row < N)
-                y[row] = v;
-        }
+    for (int rd = 0; rd < XR; ++rd)
+        if (rd < rounds)
+            quant_round<FMT>(rec, meta, xv[rd], U, rd);
+    for (int rd = XR; rd < rounds; ++rd)
+        quant_round<FMT>(rec, meta, x_round(a.x, K, U, rd), U, rd);
+    __syncthreads();
+
+    // Two passes in flight per wave: each computes while the other loads.
+    for (;;) {
+        if (p >= npass)
+            break;
+        finish(A, p);
+        load_pass(A, p + 2 * nw);
+        p += nw;
+        if (p >= npass)
+            break;
+        finish(B, p);
+        load_pass(B, p + 2 * nw);
+        p += nw;
     }
 }
 
 } // namespace
 
-#define DEF_GEMV(LPR, UPL, R)                                                               \
-    extern "C" __global__ __launch_bounds__(256) void realm_gemv_q4k_l##LPR##_u##UPL##_r##R( \
-        const uint8_t *hdr, const uint8_t *qs, const float *x, float *y, int N, int K,        \
-        int nan_fb)                                                                            \
-    {                                                                                          \
-        gemv_q4k<LPR, UPL, R>(hdr, qs, x, y, N, K, nan_fb);                                    \
-    }                                                                                          \
-    extern "C" __global__ __launch_bounds__(256) void realm_gemv_q6k_l##LPR##_u##UPL##_r##R( \
-        const uint8_t *dq, const int8_t *scq, const uint8_t *qq, const float *x, float *y,    \
-        int N, int K, int nan_fb)                                                              \
-    {                                                                                          \
-        gemv_q6k<LPR, UPL, R>(dq, scq, qq, x, y, N, K, nan_fb);                                \
-    }                                                                                          \
-    extern "C" __global__ __launch_bounds__(256) void realm_gemv_q80_l##LPR##_u##UPL##_r##R( \
-        const uint8_t *dq, const int8_t *qq, const float *x, float *y, int N, int K, int KP)  \
-    {                                                                                          \
-        gemv_q80<LPR, UPL, R>(dq, qq, x, y, N, K, KP);                                         \
+// Workgroup size by units per lane: 1024 threads (<= 128 VGPRs) while a
+// lane owns one unit, fewer threads and more registers beyond.
+#define GEMV_THREADS(UPL) ((UPL) <= 1 ? 1024 : ((UPL) <= 3 ? 512 : 256))
+// x rounds held in registers across the prologue (more are loaded in a loop)
+#define GEMV_XR(UPL) ((UPL) <= 1 ? 2 : 8)
+
+#define DEF_GEMV1(NAME, FMT, LPR, UPL, R)                                                     \
+    extern "C" __global__ __launch_bounds__(GEMV_THREADS(UPL)) void                           \
+        realm_gemv_##NAME##_l##LPR##_u##UPL##_r##R(GemvArgs a)                              \
+    {                                                                                        \
+        gemv<FMT, LPR, UPL, R, GEMV_XR(UPL)>(a);                                             \
     }
+#define DEF_GEMV(LPR, UPL, R)                \
+    DEF_GEMV1(q4k, FMT_Q4K, LPR, UPL, R)     \
+    DEF_GEMV1(q6k, FMT_Q6K, LPR, UPL, R)     \
+    DEF_GEMV1(q80, FMT_Q80, LPR, UPL, R)
 
 // (lanes per row, units per lane, rows per pass) variants the host chooses from.
 DEF_GEMV(16, 1, 1)
 DEF_GEMV(16, 1, 2)
-DEF_GEMV(16, 1, 4)
 DEF_GEMV(32, 1, 1)
 DEF_GEMV(32, 1, 2)
-DEF_GEMV(32, 1, 4)
-DEF_GEMV(32, 2, 1)
-DEF_GEMV(32, 2, 2)
 DEF_GEMV(64, 1, 1)
 DEF_GEMV(64, 1, 2)
-DEF_GEMV(64, 1, 4)
 DEF_GEMV(64, 2, 1)
-DEF_GEMV(64, 2, 2)
 DEF_GEMV(64, 3, 1)
-DEF_GEMV(64, 3, 2)
 DEF_GEMV(64, 4, 1)
 DEF_GEMV(64, 5, 1)
 DEF_GEMV(64, 6, 1)

@@ -39,6 +39,22 @@ struct GemmArgs {
     int32_t pad;
 };
 
+// Arguments of the realm_gemv_* kernels: up to 4 matrices of one format
+// that share the input x (a grouped launch, e.g. Q/K/V), rows concatenated.
+#define REALM_GEMV_MAX_MATS 4
+struct GemvArgs {
+    const void *w0[REALM_GEMV_MAX_MATS];
+    const void *w1[REALM_GEMV_MAX_MATS];
+    const void *w2[REALM_GEMV_MAX_MATS];
+    float *y[REALM_GEMV_MAX_MATS];
+    int32_t row_start[REALM_GEMV_MAX_MATS + 1]; // prefix sums of row counts
+    int32_t nmat;
+    const float *x;
+    int32_t K, KX;
+    int32_t nan_fb;
+    int32_t pad;
+};
+
 #ifdef __cplusplus
 } // namespace realm
 #endif
