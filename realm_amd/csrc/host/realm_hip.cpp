@@ -381,25 +381,45 @@ int run_gemv(const Weight *const *ws, int count, const float *d_x, float *const 
     a.K = (int)w.k;
     a.KX = (int)w.kx;
     a.nan_fb = g_nan_fb.load();
-    // one workgroup per CU (1024 threads while a lane owns one unit, as the
-    // kernels' launch bounds say); two rows per pass when every wave still
-    // gets at least two passes
-    const int threads = upl <= 1 ? 1024 : (upl <= 3 ? 512 : 256);
+    // Each wave keeps two passes in flight and should get at least two (a
+    // wave with one issues its second load for nothing).  Two rows per pass
+    // when the largest workgroups still give every wave two such passes;
+    // then the largest workgroup (at most one per CU: each one stages x in
+    // its LDS) with two passes per wave, and fewer workgroups for matrices
+    // too small for that.
     const int rpw = 64 / lpr;
-    const long waves = (long)(threads / 64) * g_dev.cu_count;
+    const int tmax = upl <= 1 ? 1024 : (upl <= 3 ? 512 : 256);
+    const long cu = g_dev.cu_count;
     int r = 1;
-    if (upl == 1 && (long)rows / (2 * rpw) >= 2 * waves)
+    if (upl == 1 && ((long)rows + 2 * rpw - 1) / (2 * rpw) >= 2 * cu * (tmax / 64))
         r = 2;
     if (const char *env = getenv("REALM_GEMV_R")) { // tuning override
         int v = atoi(env);
         if (v == 1 || (v == 2 && upl == 1))
             r = v;
     }
-    long npass = ((long)rows + rpw * r - 1) / (rpw * r);
-    long wgs = std::min<long>(g_dev.cu_count, (npass + threads / 64 - 1) / (threads / 64));
+    const long npass = ((long)rows + rpw * r - 1) / (rpw * r);
+    int threads = 256;
+    for (int t = tmax; t >= 256; t /= 2)
+        if (npass >= 2 * cu * (t / 64)) {
+            threads = t;
+            break;
+        }
+    if (const char *env = getenv("REALM_GEMV_TH")) { // tuning override
+        int v = atoi(env);
+        if ((v == 256 || v == 512 || v == 1024) && v <= tmax)
+            threads = v;
+    }
+    const int wpb = threads / 64;
+    long wgs = std::min<long>(cu, std::max<long>(1, npass / (2 * wpb)));
+    if (const char *env = getenv("REALM_GEMV_WGS")) { // tuning override
+        long v = atol(env);
+        if (v >= 1 && v <= 16 * cu)
+            wgs = v;
+    }
     std::string name = std::string("realm_gemv_") + fmt_name(w.type) + "_l" +
                        std::to_string(lpr) + "_u" + std::to_string(upl) + "_r" +
-                       std::to_string(r);
+                       std::to_string(r) + "_t" + std::to_string(threads);
     void *args[] = {&a};
     return launch(name, dim3((unsigned)std::max<long>(wgs, 1)), dim3(threads), lds, s, args);
 }

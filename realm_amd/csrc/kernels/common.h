@@ -38,6 +38,16 @@ constexpr int Q4K_BLOCK_BYTES = 144;
 constexpr int Q6K_BLOCK_BYTES = 210;
 constexpr int Q80_BLOCK_BYTES = 34;
 
+// Workgroup barrier that orders LDS accesses only.  __syncthreads() also
+// makes the wave wait for every global load it has in flight, which would
+// stall the weight loads a kernel issues ahead of its first barrier.
+REALM_DEV void lds_barrier()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 REALM_DEV float f16_bits_to_f32(uint32_t h)
 {
     // v_cvt_f32_f16: exact, f16 subnormals preserved (f16 denormal mode is on).

@@ -96,21 +96,26 @@ REALM_DEV uint32_t pack4(int a, int b, int c, int d)
 // meta[u] (float4; Q6_K: two float4 per unit) holds the x-block scales and
 // the sums s*(sum xh + sum xl/254) of the elements the unit covers.
 //
-// Round rd covers 4-element chunks gid = rd*blockDim + tid, i.e. x block
-// gid/8, chunk gid%8.  x_round() loads one round; quant_round() quantizes it.
+// Round rd covers 4-element chunks gid = rd*TH + tid (TH threads per
+// workgroup), i.e. x block gid/8, chunk gid%8.  x_round() loads one round;
+// quant_round() quantizes it.  The load is unconditional (clamped address,
+// value selected) so that no branch separates it from the weight loads that
+// follow: the workgroup size is a compile-time constant for the same reason
+// (blockDim is a memory load).
+template <int TH>
 REALM_DEV float4 x_round(const float *__restrict__ x, int K, int U, int rd)
 {
-    const int gid = rd * blockDim.x + threadIdx.x;
+    const int gid = rd * TH + threadIdx.x;
     const int blk = gid >> 3, c8 = gid & 7;
     const int e0 = 32 * blk + 4 * c8;
-    return (blk < 2 * U && e0 < K) ? reinterpret_cast<const float4 *>(x)[e0 >> 2]
-                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+    const float4 v = reinterpret_cast<const float4 *>(x)[min(e0, K - 4) >> 2];
+    return (blk < 2 * U && e0 < K) ? v : make_float4(0.f, 0.f, 0.f, 0.f);
 }
 
-template <int FMT>
+template <int FMT, int TH>
 REALM_DEV void quant_round(int4 *rec, float4 *meta, float4 v, int U, int rd)
 {
-    const int gid = rd * blockDim.x + threadIdx.x;
+    const int gid = rd * TH + threadIdx.x;
     const int blk = gid >> 3, c8 = gid & 7;
     const bool live = blk < 2 * U;
     float amax = max8(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
@@ -357,7 +362,8 @@ REALM_DEV void unit_dot(const Unit<FMT> (&w)[R], const int4 *rec, const float4 *
     }
 }
 
-template <int FMT, int LPR, int UPL, int R, int XR>
+
+template <int FMT, int LPR, int UPL, int R, int XR, int TH>
 REALM_DEV void gemv(const GemvArgs &a)
 {
     extern __shared__ int4 lds[];
@@ -367,7 +373,7 @@ REALM_DEV void gemv(const GemvArgs &a)
     float4 *meta = reinterpret_cast<float4 *>(lds + 8 * U);
     const int lane = threadIdx.x & 63;
     const int slot = lane / LPR, l = lane % LPR;
-    const int wpb = blockDim.x >> 6;
+    constexpr int wpb = TH / 64;
     // wave-uniform: keeps pass/row/matrix bookkeeping (and the kernarg
     // pointer tables) in scalar registers, out of the vector memory queue
     const int gw = __builtin_amdgcn_readfirstlane(blockIdx.x * wpb + (threadIdx.x >> 6));
@@ -375,6 +381,22 @@ REALM_DEV void gemv(const GemvArgs &a)
     constexpr int RPP = (64 / LPR) * R; // rows per pass per wave
     const int rs1 = a.row_start[1], rs2 = a.row_start[2], rs3 = a.row_start[3];
     const int rows = a.row_start[REALM_GEMV_MAX_MATS];
+    const void *const w0[4] = {a.w0[0], a.w0[1], a.w0[2], a.w0[3]};
+    const void *const w1[4] = {a.w1[0], a.w1[1], a.w1[2], a.w1[3]};
+    const void *const w2[4] = {a.w2[0], a.w2[1], a.w2[2], a.w2[3]};
+    float *const yv[4] = {a.y[0], a.y[1], a.y[2], a.y[3]};
+    const float *const xp = a.x;
+    const int nan_fb = a.nan_fb;
+    // Every kernel argument is read here, in one batch of scalar loads ahead
+    // of the first vector load.  Left alone, the compiler sinks some of these
+    // loads next to their uses, behind the x loads, and each such batch is a
+    // round trip to the argument buffer on the kernel's critical path.
+    // (one statement, so that all of them are live at once)
+    asm volatile("" ::"s"(K), "s"(KX), "s"(nw), "s"(rs1), "s"(rs2), "s"(rs3), "s"(rows),
+                 "s"(xp), "s"(nan_fb), "s"(w0[0]), "s"(w0[1]), "s"(w0[2]), "s"(w0[3]),
+                 "s"(w1[0]), "s"(w1[1]), "s"(w1[2]), "s"(w1[3]), "s"(w2[0]), "s"(w2[1]),
+                 "s"(w2[2]), "s"(w2[3]), "s"(yv[0]), "s"(yv[1]), "s"(yv[2]), "s"(yv[3]),
+                 "s"(a.pad));
     const int npass = (rows + RPP - 1) / RPP;
     const int wk = FMT == FMT_Q80 ? KX : K; // row length of the quant stream
 
@@ -397,9 +419,9 @@ REALM_DEV void gemv(const GemvArgs &a)
             const int row = min(r0 + r, rows - 1);
             const int m = mat_of(row);
             const size_t lr = (size_t)(row - pick(m, 0, rs1, rs2, rs3));
-            const uint8_t *p0 = (const uint8_t *)pick(m, a.w0[0], a.w0[1], a.w0[2], a.w0[3]);
-            const uint8_t *p1 = (const uint8_t *)pick(m, a.w1[0], a.w1[1], a.w1[2], a.w1[3]);
-            const uint8_t *p2 = (const uint8_t *)pick(m, a.w2[0], a.w2[1], a.w2[2], a.w2[3]);
+            const uint8_t *p0 = (const uint8_t *)pick(m, w0[0], w0[1], w0[2], w0[3]);
+            const uint8_t *p1 = (const uint8_t *)pick(m, w1[0], w1[1], w1[2], w1[3]);
+            const uint8_t *p2 = (const uint8_t *)pick(m, w2[0], w2[1], w2[2], w2[3]);
 #pragma unroll
             for (int j = 0; j < UPL; ++j)
                 w[j][r].load(p0, p1, p2, lr, min(l + j * LPR, U - 1), wk);
@@ -417,7 +439,7 @@ REALM_DEV void gemv(const GemvArgs &a)
 #pragma unroll
             for (int r = 0; r < R; ++r)
                 part[r] = 0.f;
-            unit_dot<FMT, R>(w[j], rec, meta, U, min(u, U - 1), a.nan_fb, part);
+            unit_dot<FMT, R>(w[j], rec, meta, U, min(u, U - 1), nan_fb, part);
 #pragma unroll
             for (int r = 0; r < R; ++r)
                 acc[r] += u < U ? part[r] : 0.f;
@@ -429,7 +451,7 @@ REALM_DEV void gemv(const GemvArgs &a)
             const int row = r0 + r;
             if (l == LPR - 1 && row < rows) {
                 const int m = mat_of(row);
-                float *y = pick(m, a.y[0], a.y[1], a.y[2], a.y[3]);
+                float *y = pick(m, yv[0], yv[1], yv[2], yv[3]);
                 y[row - pick(m, 0, rs1, rs2, rs3)] = v;
             }
         }
@@ -438,11 +460,11 @@ REALM_DEV void gemv(const GemvArgs &a)
     // Prologue: x loads first (so waiting for x does not wait for weights),
     // then the weights of the wave's first two passes, then x is quantized
     // into LDS while those loads are in flight.
-    const int rounds = (16 * U + blockDim.x - 1) / blockDim.x;
+    const int rounds = (16 * U + TH - 1) / TH;
     float4 xv[XR];
 #pragma unroll
     for (int rd = 0; rd < XR; ++rd)
-        xv[rd] = rd < rounds ? x_round(a.x, K, U, rd) : make_float4(0.f, 0.f, 0.f, 0.f);
+        xv[rd] = x_round<TH>(xp, K, U, rd);
     Unit<FMT> A[UPL][R], B[UPL][R];
     int p = gw;
     load_pass(A, p);
@@ -450,56 +472,76 @@ REALM_DEV void gemv(const GemvArgs &a)
 #pragma unroll
     for (int rd = 0; rd < XR; ++rd)
         if (rd < rounds)
-            quant_round<FMT>(rec, meta, xv[rd], U, rd);
+            quant_round<FMT, TH>(rec, meta, xv[rd], U, rd);
     for (int rd = XR; rd < rounds; ++rd)
-        quant_round<FMT>(rec, meta, x_round(a.x, K, U, rd), U, rd);
-    __syncthreads();
+        quant_round<FMT, TH>(rec, meta, x_round<TH>(xp, K, U, rd), U, rd);
+    lds_barrier();
 
     // Two passes in flight per wave: each computes while the other loads.
+    // The wave's passes are p = gw + i*nw, i < T.  Every load below is
+    // unconditional on the path that reaches it and every path into a join
+    // carries the same loads in flight (A then B), so each wait the compiler
+    // places covers exactly the pass about to be used.  No load is issued
+    // past the wave's last pass, except the prologue's B when T < 2 (the host
+    // sizes the grid so that T >= 2 wherever the matrix allows it).
+    int left = p < npass ? (npass - p + nw - 1) / nw : 0;
     for (;;) {
-        if (p >= npass)
+        if (left <= 2)
             break;
         finish(A, p);
         load_pass(A, p + 2 * nw);
-        p += nw;
-        if (p >= npass)
-            break;
-        finish(B, p);
-        load_pass(B, p + 2 * nw);
-        p += nw;
+        if (left == 3) {
+            finish(B, p + nw);
+            finish(A, p + 2 * nw);
+            return;
+        }
+        finish(B, p + nw);
+        load_pass(B, p + 3 * nw);
+        p += 2 * nw;
+        left -= 2;
     }
+    if (left >= 1)
+        finish(A, p);
+    if (left >= 2)
+        finish(B, p + nw);
 }
 
 } // namespace
 
-// Workgroup size by units per lane: 1024 threads (<= 128 VGPRs) while a
-// lane owns one unit, fewer threads and more registers beyond.
-#define GEMV_THREADS(UPL) ((UPL) <= 1 ? 1024 : ((UPL) <= 3 ? 512 : 256))
-// x rounds held in registers across the prologue (more are loaded in a loop)
-#define GEMV_XR(UPL) ((UPL) <= 1 ? 2 : 8)
+// x rounds held in registers across the prologue: all of them for the
+// longest row a variant serves (64 * UPL units, 16 float4 each)
+#define GEMV_XR(UPL, TH) ((1024 * (UPL) + (TH) - 1) / (TH))
 
-#define DEF_GEMV1(NAME, FMT, LPR, UPL, R)                                                     \
-    extern "C" __global__ __launch_bounds__(GEMV_THREADS(UPL)) void                           \
-        realm_gemv_##NAME##_l##LPR##_u##UPL##_r##R(GemvArgs a)                              \
+// Variant (lanes per row, units per lane, rows per pass, threads per
+// workgroup).  The workgroup size is a compile-time constant: at most 1024
+// threads (<= 128 VGPRs) while a lane owns one unit, fewer beyond.
+#define DEF_GEMV1(NAME, FMT, LPR, UPL, R, TH)                                                 \
+    extern "C" __global__ __launch_bounds__(TH) void                                         \
+        realm_gemv_##NAME##_l##LPR##_u##UPL##_r##R##_t##TH(GemvArgs a)                       \
     {                                                                                        \
-        gemv<FMT, LPR, UPL, R, GEMV_XR(UPL)>(a);                                             \
+        gemv<FMT, LPR, UPL, R, GEMV_XR(UPL, TH), TH>(a);                                     \
     }
-#define DEF_GEMV(LPR, UPL, R)                \
-    DEF_GEMV1(q4k, FMT_Q4K, LPR, UPL, R)     \
-    DEF_GEMV1(q6k, FMT_Q6K, LPR, UPL, R)     \
-    DEF_GEMV1(q80, FMT_Q80, LPR, UPL, R)
+#define DEF_GEMV_T(LPR, UPL, R, TH)              \
+    DEF_GEMV1(q4k, FMT_Q4K, LPR, UPL, R, TH)     \
+    DEF_GEMV1(q6k, FMT_Q6K, LPR, UPL, R, TH)     \
+    DEF_GEMV1(q80, FMT_Q80, LPR, UPL, R, TH)
+#define DEF_GEMV(LPR, UPL, R)                                             \
+    DEF_GEMV_T(LPR, UPL, R, 256)                                          \
+    DEF_GEMV_T(LPR, UPL, R, 512)                                          \
+    DEF_GEMV_T(LPR, UPL, R, 1024)
+#define DEF_GEMV_MID(UPL) DEF_GEMV_T(64, UPL, 1, 256) DEF_GEMV_T(64, UPL, 1, 512)
 
-// (lanes per row, units per lane, rows per pass) variants the host chooses from.
+// The variants the host chooses from.
 DEF_GEMV(16, 1, 1)
 DEF_GEMV(16, 1, 2)
 DEF_GEMV(32, 1, 1)
 DEF_GEMV(32, 1, 2)
 DEF_GEMV(64, 1, 1)
 DEF_GEMV(64, 1, 2)
-DEF_GEMV(64, 2, 1)
-DEF_GEMV(64, 3, 1)
-DEF_GEMV(64, 4, 1)
-DEF_GEMV(64, 5, 1)
-DEF_GEMV(64, 6, 1)
-DEF_GEMV(64, 7, 1)
-DEF_GEMV(64, 8, 1)
+DEF_GEMV_MID(2)
+DEF_GEMV_MID(3)
+DEF_GEMV_T(64, 4, 1, 256)
+DEF_GEMV_T(64, 5, 1, 256)
+DEF_GEMV_T(64, 6, 1, 256)
+DEF_GEMV_T(64, 7, 1, 256)
+DEF_GEMV_T(64, 8, 1, 256)

@@ -55,6 +55,6 @@ def test_code_object_is_embedded_for_gfx950():
     assert blob[:4] == b"\x7fELF" and b"gfx950" in blob
     lib = open(_lib.LIB_PATH, "rb").read()
     assert blob[:4096] in lib  # embedded verbatim
-    for k in (b"realm_gemv_q4k_l64_u1_r1", b"realm_gemm_q4k_p4_bf16", b"realm_dequant_q6k",
+    for k in (b"realm_gemv_q4k_l64_u1_r1_t512", b"realm_gemm_q4k_p4_bf16", b"realm_dequant_q6k",
               b"realm_lora_shrink_q4k_f32", b"realm_dense_f32"):
         assert k in blob
