@@ -3,18 +3,23 @@
 
 Headline (the timed region): LLaMA-7B decode, batch 1 -- one step is the
 decoder-layer matvec set (Wq, Wk, Wv, Wo, W_gate, W_up in Q4_K, W_down in
-Q6_K) of all 32 layers, 224 launches captured in one HIP graph.  Every layer
-has its own copy of the weights in HBM (4.0 GB per step, far beyond the
-256 MB Infinity Cache), activations are resident before timing starts.
-``value`` is algorithmic GB/s = (packed weight bytes + activations read +
-outputs written) / step time; tok/s = batch / step time.
+Q6_K) of all 32 layers, captured in one HIP graph.  Launches follow the
+layer's data dependencies: Q/K/V share their input and go in one grouped
+launch, so do gate/up; Wo and W_down each wait for the work before them
+(attention and SwiGLU in a full model), so each is a launch of its own: four
+launches per layer, 128 per step.  Every layer has its own copy of the
+weights in HBM (4.0 GB per step, far beyond the 256 MB Infinity Cache);
+activations are resident before timing starts.  ``value`` is algorithmic
+GB/s = (packed weight bytes + activations read + outputs written) / step
+time; tok/s = batch / step time.
 
-After the timed region, bench.py reports (in "extra"): the same step at
-batch 4 and 16, the roofline of the dominant kernel (the Q4_K GEMV, timed per
-launch with HIP events on its stream), 16-tenant multi-LoRA overhead
-(config 3), prefill TFLOP/s (config 2, Q4_K and Q8_0 with bf16 activations)
-and the CPU baseline (the oracle's restatement of realm-compute-cpu, timed on
-this host).  All inputs are synthetic and seeded (realm_amd/synth.py).
+After the timed region, bench.py reports the roofline of the dominant Q4_K
+kernel (the grouped gate/up GEMV: its launches replayed from a graph of their
+own, HIP events on its stream) and, in "extra": the same step at batch 4 and
+16, 16-tenant multi-LoRA overhead (config 3), prefill TFLOP/s (config 2,
+Q4_K and Q8_0 with bf16 activations) and the CPU baseline (the oracle's
+restatement of realm-compute-cpu, timed on this host).  All inputs are
+synthetic and seeded (realm_amd/synth.py).
 """
 from __future__ import annotations
 
@@ -65,16 +70,36 @@ class Model7B:
                   for k in (4096, 11008)}
         self.y = {name: be.alloc(max_m * n * 4) for name, _, n, _ in LAYER}
 
-    def step(self, m: int, stream: int, only_q4k: bool = False) -> None:
-        for layer in self.layers:
-            for name, t, n, k, h in layer:
-                if only_q4k and t != GGML_Q4_K:
-                    continue
-                self.be.matmul_dev(h, self.x[k].ptr, m, self.y[name].ptr, stream=stream)
+    # launch groups of a layer (indices into LAYER): matrices in one group
+    # share their input
+    GROUPS = ((0, 1, 2), (3,), (4, 5), (6,))
 
-    def bytes_per_step(self, m: int, only_q4k: bool = False) -> int:
-        return len(self.layers) * sum(alg_bytes(t, n, k, m) for _, t, n, k in LAYER
-                                      if not only_q4k or t == GGML_Q4_K)
+    def launch_group(self, layer, gi: int, m: int, stream: int) -> None:
+        idx = self.GROUPS[gi]
+        k = LAYER[idx[0]][3]
+        hs = [layer[i][4] for i in idx]
+        ys = [self.y[LAYER[i][0]].ptr for i in idx]
+        if len(hs) == 1:
+            self.be.matmul_dev(hs[0], self.x[k].ptr, m, ys[0], stream=stream)
+        else:
+            self.be.matmul_group_dev(hs, self.x[k].ptr, m, ys, stream=stream)
+
+    def step(self, m: int, stream: int) -> None:
+        for layer in self.layers:
+            for gi in range(len(self.GROUPS)):
+                self.launch_group(layer, gi, m, stream)
+
+    @classmethod
+    def group_bytes(cls, gi: int, m: int) -> int:
+        """Algorithmic bytes of one launch group: its packed weights, its
+        shared input read once, its outputs."""
+        idx = cls.GROUPS[gi]
+        k = LAYER[idx[0]][3]
+        return sum(weight_bytes(LAYER[i][1], LAYER[i][2], k) + 4 * m * LAYER[i][2]
+                   for i in idx) + 4 * m * k
+
+    def bytes_per_step(self, m: int) -> int:
+        return len(self.layers) * sum(self.group_bytes(gi, m) for gi in range(len(self.GROUPS)))
 
     def close(self):
         for layer in self.layers:
@@ -102,37 +127,38 @@ def time_graph(be, graph: int, stream: int, reps: int) -> float:
     return be.elapsed_ms(e0, e1) / reps
 
 
-def per_launch_ms(be, stream: int, launches) -> list[float]:
-    """Duration of each launch, HIP events recorded right around it."""
-    evs = [(be.event(), be.event()) for _ in launches]
-    for (a, b), fn in zip(evs, launches):
-        be.record(a, stream)
-        fn()
-        be.record(b, stream)
-    be.synchronize()
-    return [be.elapsed_ms(a, b) for a, b in evs]
+ROOF_GROUP = 2  # the grouped gate/up launch: the largest Q4_K kernel of the step
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "gemv_q4k_gateup_7b_traffic.json")
 
 
-def decode_roofline(be, model: Model7B, stream: int) -> dict:
-    """Q4_K GEMV (batch 1) over the 6 Q4_K matrices of all 32 layers."""
-    launches, nbytes = [], []
-    for layer in model.layers:
-        for name, t, n, k, h in layer:
-            if t != GGML_Q4_K:
-                continue
-            launches.append(lambda h=h, k=k, name=name: be.matmul_dev(
-                h, model.x[k].ptr, 1, model.y[name].ptr, stream=stream))
-            nbytes.append(alg_bytes(t, n, k, 1))
-    per_launch_ms(be, stream, launches)  # warm
-    ms = per_launch_ms(be, stream, launches)
-    avg_ms = float(np.mean(ms))
-    avg_bytes = float(np.mean(nbytes))
-    achieved = avg_bytes / (avg_ms * 1e-3) / 1e9
+def decode_roofline(be, model: Model7B, stream: int, reps: int) -> dict:
+    """The dominant Q4_K kernel of the decode step: the grouped gate/up GEMV
+    (2 x 11008x4096, batch 1).  Its 32 per-layer launches (distinct weights)
+    are replayed from a graph of their own; HIP events on the launch stream
+    bracket `reps` replays, so the average includes nothing but those
+    kernels back to back.  Algorithmic bytes per launch: both packed
+    matrices, x once, both outputs."""
+    def launches():
+        for layer in model.layers:
+            model.launch_group(layer, ROOF_GROUP, 1, stream)
+    gr = capture(be, stream, launches)
+    kernel = be.last_kernel()
+    time_graph(be, gr, stream, 3)
+    ms = time_graph(be, gr, stream, reps) / len(model.layers)
+    be.graph_release(gr)
+    nbytes = Model7B.group_bytes(ROOF_GROUP, 1)
+    achieved = nbytes / (ms * 1e-3) / 1e9
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            rec = json.load(f)
+        if rec.get("kernel") == kernel:
+            traffic = rec.get("hbm_bytes_per_launch")
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-            "kernel": "realm_gemv_q4k_l64_u1_r4", "launches": len(ms),
-            "avg_launch_us": round(avg_ms * 1e3, 3), "avg_alg_bytes_per_launch": int(avg_bytes),
-            "shape_mix": "4 x (4096x4096) + 2 x (11008x4096) per layer, 32 layers"}
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+            "kernel": kernel, "launches": len(model.layers) * reps,
+            "avg_launch_us": round(ms * 1e3, 3), "alg_bytes_per_launch": nbytes,
+            "shape": "grouped W_gate + W_up, 2 x (11008 x 4096) Q4_K, batch 1"}
 
 
 def lora_overhead(be, stream: int, reps: int) -> dict:
@@ -262,6 +288,9 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=8.0)
     ap.add_argument("--skip-extra", action="store_true",
                     help="only the timed decode step and the roofline")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="no timing: one 256 MiB device copy (the counter reference) then "
+                         "one gate/up GEMV launch per layer, for rocprofv3 --pmc runs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
@@ -273,6 +302,19 @@ def main() -> int:
     stream = be.stream()
     log(f"registering {args.layers} LLaMA-7B layers")
     model = Model7B(be, args.layers, 16)
+    if args.traffic_probe:
+        nb = 256 << 20
+        src, dst = be.alloc(nb), be.alloc(nb)
+        be.memcpy_dtod(dst, src, nb)
+        for layer in model.layers:
+            model.launch_group(layer, ROOF_GROUP, 1, stream)
+        be.synchronize()
+        log(f"traffic probe: copy of {nb} bytes, then {len(model.layers)} x {be.last_kernel()} "
+            f"({Model7B.group_bytes(ROOF_GROUP, 1)} algorithmic bytes each)")
+        src.close()
+        dst.close()
+        model.close()
+        return 0
 
     # ---- timed region: batch-1 decode steps replayed from one HIP graph
     m = 1
@@ -297,7 +339,7 @@ def main() -> int:
     extra = {"decode": {"b1": {"ms_per_step": round(wall * 1e3, 4),
                                "tok_per_s": round(m / wall, 1),
                                "gb_per_s": round(value, 1)}}}
-    roof = decode_roofline(be, model, stream)
+    roof = decode_roofline(be, model, stream, max(5, args.steps))
     log(f"roofline: {roof['achieved']} GB/s ({roof['frac'] * 100:.1f}% of peak)")
     if not args.skip_extra:
         for mb in (4, 16):
@@ -324,10 +366,11 @@ def main() -> int:
     line = {
         "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall * 1e3, 4),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "i8dot+f32",
         "data": "synthetic (seeded, realm_amd/synth.py)",
         "config": {"workload": "config1: LLaMA-7B decoder-layer matvec set (Q4_K Wq/Wk/Wv/Wo/"
-                               "W_gate/W_up, Q6_K W_down) x 32 layers, decode batch 1",
+                               "W_gate/W_up, Q6_K W_down) x 32 layers, decode batch 1; "
+                               "launches per layer: QKV grouped, Wo, gate/up grouped, W_down",
                    "layers": args.layers, "batch": m, "alg_bytes_per_step": step_bytes,
                    "tok_per_s": round(m / wall, 1), "hbm_frac": round(value / HBM_PEAK_GBS, 4)},
         "roofline": roof,

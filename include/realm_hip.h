@@ -69,6 +69,12 @@ int realm_hip_init(int device);
  * crates/realm-runtime/src/lib.rs:137-150 (set_last_error/take_last_error). */
 const char *realm_hip_last_error(void);
 
+/* Name of the last kernel this thread launched through the library ("" if
+ * none): a diagnostic for profilers and benchmarks, so that a timing can be
+ * matched to the kernel variant the dispatcher chose.  No counterpart in the
+ * reference (its backends have no kernel variants). */
+const char *realm_hip_last_kernel(void);
+
 /* GpuBackendTrait::name (crates/realm-compute-gpu/src/gpu_backend_trait.rs:142). */
 const char *realm_hip_backend_name(void);
 

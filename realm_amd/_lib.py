@@ -15,6 +15,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libr
 SIGNATURES = {
     "realm_hip_init": (c_int, [c_int]),
     "realm_hip_last_error": (c_char_p, []),
+    "realm_hip_last_kernel": (c_char_p, []),
     "realm_hip_backend_name": (c_char_p, []),
     "realm_hip_set_nan_fallback": (c_int, [c_int]),
     "realm_hip_matmul": (c_int, [c_void_p, c_size_t, c_void_p, c_size_t, c_uint32, c_uint32,

@@ -103,6 +103,10 @@ class HipGpuBackend:
     def name(self) -> str:
         return self.lib.realm_hip_backend_name().decode()
 
+    def last_kernel(self) -> str:
+        """Name of the last kernel this thread launched (diagnostic)."""
+        return self.lib.realm_hip_last_kernel().decode()
+
     def matmul(self, a, b, m: int, k: int, n: int) -> np.ndarray:
         a = np.ascontiguousarray(a, np.float32)
         b = np.ascontiguousarray(b, np.float32)
@@ -240,6 +244,11 @@ class HipGpuBackend:
     # --------------------------------------------------------- plumbing
     def alloc(self, nbytes: int) -> DeviceBuffer:
         return DeviceBuffer(self, nbytes)
+
+    def memcpy_dtod(self, dst: DeviceBuffer, src: DeviceBuffer, nbytes: int) -> None:
+        if nbytes > min(dst.nbytes, src.nbytes):
+            raise InvalidShape(f"copy of {nbytes} bytes exceeds a buffer")
+        self._check(self.lib.realm_hip_memcpy_dtod(c_void_p(dst.ptr), c_void_p(src.ptr), nbytes))
 
     def stream(self) -> int:
         s = c_void_p()

@@ -157,6 +157,8 @@ int get_fn(const std::string &name, hipFunction_t *out)
     return REALM_OK;
 }
 
+thread_local std::string t_last_kernel;
+
 int launch(const std::string &name, dim3 grid, dim3 block, size_t lds, hipStream_t s,
            void **args)
 {
@@ -164,6 +166,7 @@ int launch(const std::string &name, dim3 grid, dim3 block, size_t lds, hipStream
         return REALM_OK;
     hipFunction_t f;
     CHECK(get_fn(name, &f));
+    t_last_kernel = name;
     HIP_TRY(hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z,
                                   (unsigned)lds, s, args, nullptr));
     return REALM_OK;
@@ -664,6 +667,8 @@ REALM_API int realm_hip_init(int device)
 }
 
 REALM_API const char *realm_hip_last_error(void) { return t_last_error.c_str(); }
+
+REALM_API const char *realm_hip_last_kernel(void) { return t_last_kernel.c_str(); }
 
 REALM_API const char *realm_hip_backend_name(void) { return "HIP (gfx950)"; }
 
