@@ -19,6 +19,12 @@ KDIR = os.path.join(PKG, "csrc", "kernels")
 HDIR = os.path.join(PKG, "csrc", "host")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
+# code objects: the non-GEMV kernels, then the GEMV variants per format
+# (compiled in parallel; the host library embeds all of them)
+HSACO_UNITS = [("realm_kernels", "realm_kernels.hip", ()),
+               ("realm_gemv_q4k", "gemv_fmt.hip", ("REALM_GEMV_FMT=0",)),
+               ("realm_gemv_q6k", "gemv_fmt.hip", ("REALM_GEMV_FMT=1",)),
+               ("realm_gemv_q80", "gemv_fmt.hip", ("REALM_GEMV_FMT=2",))]
 HSACO = os.path.join(LIB_DIR, "realm_kernels.hsaco")
 LIBSO = os.path.join(LIB_DIR, "librealm_hip.so")
 
@@ -40,21 +46,33 @@ def _run(cmd: list[str]) -> None:
         print(out, file=sys.stderr)
 
 
-def build_hsaco(out: str = HSACO, defines: tuple = ()) -> str:
+def build_hsaco(out: str = HSACO, defines: tuple = (), src: str = "realm_kernels.hip") -> str:
     os.makedirs(os.path.dirname(out), exist_ok=True)
     tmp = out + ".tmp"
     _run([os.path.join(ROCM, "bin", "hipcc"), *HIP_FLAGS, *[f"-D{d}" for d in defines],
-          "-I", KDIR, os.path.join(KDIR, "realm_kernels.hip"), "-o", tmp])
+          "-I", KDIR, os.path.join(KDIR, src), "-o", tmp])
     os.replace(tmp, out)
     return out
 
 
-def build_host(out: str = LIBSO, hsaco: str = HSACO) -> str:
+def build_all_hsaco(out_dir: str = LIB_DIR, defines: tuple = ()) -> list:
+    """Every code object of HSACO_UNITS, compiled in parallel; returns paths."""
+    import concurrent.futures as cf
+    jobs = [(os.path.join(out_dir, name + ".hsaco"), tuple(defs) + tuple(defines), src)
+            for name, src, defs in HSACO_UNITS]
+    with cf.ThreadPoolExecutor(len(jobs)) as ex:
+        return list(ex.map(lambda j: build_hsaco(*j), jobs))
+
+
+def build_host(out: str = LIBSO, hsacos: list | None = None) -> str:
+    if hsacos is None:
+        hsacos = [os.path.join(LIB_DIR, name + ".hsaco") for name, _, _ in HSACO_UNITS]
     os.makedirs(os.path.dirname(out), exist_ok=True)
     tmp = out + ".tmp"
+    embeds = [f"-DREALM_HSACO_FILE{i}={p}" for i, p in enumerate(hsacos)]
     _run(["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-fvisibility=hidden",
           "-Wall", "-Wextra", "-Wno-unused-parameter",
-          "-D__HIP_PLATFORM_AMD__", f"-DREALM_HSACO_FILE={hsaco}",
+          "-D__HIP_PLATFORM_AMD__", f"-DREALM_HSACO_COUNT={len(hsacos)}", *embeds,
           "-I", os.path.join(ROCM, "include"), "-I", os.path.join(REPO, "include"),
           "-I", KDIR,
           os.path.join(HDIR, "realm_hip.cpp"), "-o", tmp,
@@ -65,8 +83,7 @@ def build_host(out: str = LIBSO, hsaco: str = HSACO) -> str:
 
 
 def build() -> str:
-    build_hsaco()
-    return build_host()
+    return build_host(hsacos=build_all_hsaco())
 
 
 if __name__ == "__main__":

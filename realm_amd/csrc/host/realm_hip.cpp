@@ -28,20 +28,25 @@
 #define REALM_STR2(x) #x
 #define REALM_STR(x) REALM_STR2(x)
 
-// The code object, embedded at link time.
-__asm__(".pushsection .rodata.realm_hsaco,\"a\",@progbits\n"
-        ".balign 4096\n"
-        ".globl realm_hsaco_begin\n"
-        ".hidden realm_hsaco_begin\n"
-        "realm_hsaco_begin:\n"
-        ".incbin \"" REALM_STR(REALM_HSACO_FILE) "\"\n"
-        ".globl realm_hsaco_end\n"
-        ".hidden realm_hsaco_end\n"
-        "realm_hsaco_end:\n"
-        ".byte 0\n"
-        ".popsection\n");
-extern "C" const unsigned char realm_hsaco_begin[];
-extern "C" const unsigned char realm_hsaco_end[];
+// The code objects (REALM_HSACO_COUNT of them: the non-GEMV kernels and the
+// GEMV variants of each weight format), embedded at link time.
+#define REALM_EMBED(I, FILE)                                                                   \
+    __asm__(".pushsection .rodata.realm_hsaco" #I ",\"a\",@progbits\n"                        \
+            ".balign 4096\n"                                                                  \
+            ".globl realm_hsaco" #I "\n"                                                      \
+            ".hidden realm_hsaco" #I "\n"                                                     \
+            "realm_hsaco" #I ":\n"                                                            \
+            ".incbin \"" REALM_STR(FILE) "\"\n"                                                \
+            ".byte 0\n"                                                                       \
+            ".popsection\n");                                                                 \
+    extern "C" const unsigned char realm_hsaco##I[];
+REALM_EMBED(0, REALM_HSACO_FILE0)
+REALM_EMBED(1, REALM_HSACO_FILE1)
+REALM_EMBED(2, REALM_HSACO_FILE2)
+REALM_EMBED(3, REALM_HSACO_FILE3)
+static_assert(REALM_HSACO_COUNT == 4, "the build embeds four code objects");
+static const unsigned char *const realm_hsacos[REALM_HSACO_COUNT] = {realm_hsaco0, realm_hsaco1,
+                                                                      realm_hsaco2, realm_hsaco3};
 
 #define REALM_API extern "C" __attribute__((visibility("default")))
 
@@ -95,7 +100,7 @@ struct Device {
     int id = 0;
     int cu_count = 256;
     size_t max_lds = 65536;
-    hipModule_t module = nullptr;
+    hipModule_t modules[REALM_HSACO_COUNT] = {};
     std::unordered_map<std::string, hipFunction_t> fns;
 };
 
@@ -124,7 +129,8 @@ int init_locked(int device)
                     std::string("code object is built for gfx950, device is ") + prop.gcnArchName);
     g_dev.cu_count = prop.multiProcessorCount;
     g_dev.max_lds = prop.sharedMemPerBlock;
-    HIP_TRY(hipModuleLoadData(&g_dev.module, realm_hsaco_begin));
+    for (int i = 0; i < REALM_HSACO_COUNT; ++i)
+        HIP_TRY(hipModuleLoadData(&g_dev.modules[i], realm_hsacos[i]));
     g_dev.id = device;
     g_dev.ready = true;
     return REALM_OK;
@@ -148,10 +154,13 @@ int get_fn(const std::string &name, hipFunction_t *out)
         *out = it->second;
         return REALM_OK;
     }
-    hipFunction_t f;
-    hipError_t e = hipModuleGetFunction(&f, g_dev.module, name.c_str());
-    if (e != hipSuccess)
-        return fail(REALM_GENERIC_FAILURE, "kernel " + name + " not found: " + hipGetErrorString(e));
+    hipFunction_t f = nullptr;
+    for (int i = 0; i < REALM_HSACO_COUNT && !f; ++i)
+        if (hipModuleGetFunction(&f, g_dev.modules[i], name.c_str()) != hipSuccess)
+            f = nullptr;
+    (void)hipGetLastError(); // lookups in the other code objects set it
+    if (!f)
+        return fail(REALM_GENERIC_FAILURE, "kernel " + name + " not found in the code objects");
     g_dev.fns[name] = f;
     *out = f;
     return REALM_OK;
@@ -244,29 +253,33 @@ std::unordered_map<uint64_t, Weight> g_weights;
 uint64_t g_next_handle = 1;
 
 // Byte offsets of the streams of the device layout (see kernels/common.h).
+// Device layout of an [n, k] matrix (offsets of its streams in one
+// allocation).  Every stream has 4 zeroed rows of padding past row n-1: a
+// GEMV pass covers up to 4 rows and reads them without per-row clamping.
 size_t layout(int type, size_t n, size_t k, size_t off[3], size_t *kx)
 {
     size_t B = k / 256;
+    size_t np = n + 4;
     if (type == GGML_Q4_K) {
         off[0] = 0;
-        off[1] = align256(n * B * 16);
+        off[1] = align256(np * B * 16);
         off[2] = 0;
         *kx = k;
-        return off[1] + n * (k / 2);
+        return off[1] + np * (k / 2);
     }
     if (type == GGML_Q6_K) {
         off[0] = 0;
-        off[1] = align256(n * B * 2);
-        off[2] = off[1] + align256(n * B * 16);
+        off[1] = align256(np * B * 2);
+        off[2] = off[1] + align256(np * B * 16);
         *kx = k;
-        return off[2] + n * B * 192;
+        return off[2] + np * B * 192;
     }
     size_t kp = round_up(k, 64);
     off[0] = 0;
-    off[1] = align256(n * (kp / 32) * 2);
+    off[1] = align256(np * (kp / 32) * 2);
     off[2] = 0;
     *kx = kp;
-    return off[1] + n * kp;
+    return off[1] + np * kp;
 }
 
 bool q6k_wide(const uint8_t *blocks, size_t nblocks)
@@ -298,6 +311,8 @@ int upload_repack(int type, const void *blocks, size_t n, size_t k, void *dst, W
     w->w1 = base + off[1];
     w->w2 = type == GGML_Q6_K ? base + off[2] : nullptr;
     w->wide = type == GGML_Q6_K && q6k_wide((const uint8_t *)blocks, nblocks);
+    // zeroes the row padding (and the Q8_0 K padding) of every stream
+    HIP_TRY(hipMemsetAsync(dst, 0, total, s));
     if (nblocks == 0)
         return REALM_OK;
     void *raw;
@@ -317,7 +332,6 @@ int upload_repack(int type, const void *blocks, size_t n, size_t k, void *dst, W
         CHECK(launch("realm_repack_q6k", dim3((unsigned)((nblocks * 64 + 255) / 256)),
                      dim3(256), 0, s, args));
     } else {
-        HIP_TRY(hipMemsetAsync(dst, 0, total, s));
         void *dq = (void *)w->w0, *qq = (void *)w->w1;
         int kbr = (int)(k / 32), kp = (int)kx;
         void *args[] = {&raw, &dq, &qq, &nb, &kbr, &kp};
@@ -363,9 +377,18 @@ int run_gemv(const Weight *const *ws, int count, const float *d_x, float *const 
     int U = (int)(w.kx / 64);
     int lpr = U <= 16 ? 16 : (U <= 32 ? 32 : 64);
     int upl = (U + lpr - 1) / lpr;
+    const int rpp = 64 / lpr;
     size_t lds = (size_t)U * 16 * 10; // 8 x records + up to 2 meta float4 per unit
     if (upl > 8 || lds > g_dev.max_lds || count < 1 || count > REALM_GEMV_MAX_MATS)
         return REALM_BACKEND_UNSUPPORTED;
+    // A grouped launch needs every matrix to start on a pass boundary;
+    // otherwise the matrices go one launch each.
+    for (int i = 0; count > 1 && i < count; ++i)
+        if (ws[i]->n % rpp) {
+            for (int j = 0; j < count; ++j)
+                CHECK(run_gemv(ws + j, 1, d_x, d_y + j, s));
+            return REALM_OK;
+        }
     realm::GemvArgs a;
     std::memset(&a, 0, sizeof a);
     int rows = 0;
@@ -384,45 +407,44 @@ int run_gemv(const Weight *const *ws, int count, const float *d_x, float *const 
     a.K = (int)w.k;
     a.KX = (int)w.kx;
     a.nan_fb = g_nan_fb.load();
-    // Each wave keeps two passes in flight and should get at least two (a
-    // wave with one issues its second load for nothing).  Two rows per pass
-    // when the largest workgroups still give every wave two such passes;
-    // then the largest workgroup (at most one per CU: each one stages x in
-    // its LDS) with two passes per wave, and fewer workgroups for matrices
-    // too small for that.
-    const int rpw = 64 / lpr;
-    const int tmax = upl <= 1 ? 1024 : (upl <= 3 ? 512 : 256);
+    // At most one workgroup per CU (each stages x in its LDS); each wave
+    // keeps a ring of D passes in flight, D the smallest variant that holds
+    // all of the wave's passes (so the whole weight stream is requested
+    // before the first pass is computed).  The workgroup size follows the
+    // variant's register budget (GEMV_TH in gemv.hip).
+    static const int d_u1[] = {1, 2, 3, 4, 6, 8, 12}, d_u2[] = {1, 2, 3, 4},
+                     d_u3[] = {1, 2, 3, 4, 6}, d_u45[] = {1, 2}, d_big[] = {1};
+    const int *ds = upl == 1 ? d_u1 : upl == 2 ? d_u2 : upl == 3 ? d_u3 : upl <= 5 ? d_u45 : d_big;
+    const int nd = upl == 1 ? 7 : upl == 2 ? 4 : upl == 3 ? 5 : upl <= 5 ? 2 : 1;
+    auto threads_of = [&](int d) {
+        return upl == 1 ? (d <= 4 ? 1024 : 512) : (upl == 2 || (upl == 3 && d <= 2) ? 512 : 256);
+    };
     const long cu = g_dev.cu_count;
-    int r = 1;
-    if (upl == 1 && ((long)rows + 2 * rpw - 1) / (2 * rpw) >= 2 * cu * (tmax / 64))
-        r = 2;
-    if (const char *env = getenv("REALM_GEMV_R")) { // tuning override
+    const long npass = ((long)rows + rpp - 1) / rpp;
+    // Occupancy first (measured: deeper rings cost registers and lose): one
+    // pass in flight per wave, except that a wave with one unit per lane and
+    // several passes keeps two, so its next pass loads while it computes.
+    const long nw1 = cu * (threads_of(1) / 64);
+    int d = (upl == 1 && npass > nw1) ? 2 : 1;
+    if (w.type == GGML_Q8_0 && d > 8) // its 12-deep ring does not fit the registers
+        d = 8;
+    if (const char *env = getenv("REALM_GEMV_D")) { // tuning override
         int v = atoi(env);
-        if (v == 1 || (v == 2 && upl == 1))
-            r = v;
+        for (int i = 0; i < nd; ++i)
+            if (ds[i] == v)
+                d = v;
     }
-    const long npass = ((long)rows + rpw * r - 1) / (rpw * r);
-    int threads = 256;
-    for (int t = tmax; t >= 256; t /= 2)
-        if (npass >= 2 * cu * (t / 64)) {
-            threads = t;
-            break;
-        }
-    if (const char *env = getenv("REALM_GEMV_TH")) { // tuning override
-        int v = atoi(env);
-        if ((v == 256 || v == 512 || v == 1024) && v <= tmax)
-            threads = v;
-    }
+    const int threads = threads_of(d);
     const int wpb = threads / 64;
-    long wgs = std::min<long>(cu, std::max<long>(1, npass / (2 * wpb)));
+    long wgs = std::min<long>(cu, (npass + wpb - 1) / wpb);
     if (const char *env = getenv("REALM_GEMV_WGS")) { // tuning override
         long v = atol(env);
         if (v >= 1 && v <= 16 * cu)
             wgs = v;
     }
     std::string name = std::string("realm_gemv_") + fmt_name(w.type) + "_l" +
-                       std::to_string(lpr) + "_u" + std::to_string(upl) + "_r" +
-                       std::to_string(r) + "_t" + std::to_string(threads);
+                       std::to_string(lpr) + "_u" + std::to_string(upl) + "_d" +
+                       std::to_string(d) + "_m" + (count == 1 ? "1" : "4");
     void *args[] = {&a};
     return launch(name, dim3((unsigned)std::max<long>(wgs, 1)), dim3(threads), lds, s, args);
 }

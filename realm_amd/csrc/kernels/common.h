@@ -7,11 +7,19 @@
 // p-th 16 bytes of every unit (row bytes [p*U*16 + u*16, +16)), so the 64
 // lanes of a wave that own consecutive units read 1 KB contiguous per load.
 //
-//   Q4_K  hdr[N][K/256][16]  bytes 0..15 of each 144-byte block (d, dmin, scales)
+//   Q4_K  hdr[N][K/256][16]  dword 0: d | dmin << 16 (as in the block);
+//                            dwords 1..3: the 8 six-bit (scale, min) pairs of
+//                            the block's 12 packed bytes (quant.rs:110-122),
+//                            re-packed so that group g's four fields are the
+//                            24 bits at bit 24g of the 96-bit field
+//                            (sc[2g] | m[2g] << 6 | sc[2g+1] << 12 |
+//                            m[2g+1] << 18): one funnel shift per lane.
 //         qs [N][2][U][16]   unit u = qs group g = u%4 of block u/4 (32 bytes,
 //                            halves in planes 0/1): byte j low nibble -> k =
 //                            64u + j, high nibble -> k = 64u + 32 + j
-//                            (crates/realm-core/src/quant.rs:155-184).
+//                            (crates/realm-core/src/quant.rs:155-184), the
+//                            high nibble stored XOR 8: masked with 0xF0 it
+//                            reads as the int8 16 * (q - 8).
 //   Q6_K  d  [N][K/256]      f16 super-block scale
 //         sc [N][K/256][16]  int8 sub-block scales regrouped per unit: unit v
 //                            (v = 2h + is) holds sc[8h+is+2t], t = 0..3
@@ -77,6 +85,16 @@ REALM_DEV void q4k_scale_min_pair(uint32_t s0, uint32_t s1, uint32_t s2, int g,
     };
     get(2 * g, sc_lo, m_lo);
     get(2 * g + 1, sc_hi, m_hi);
+}
+
+// The 24-bit (scale, min) field of Q4_K group g (0..3) from device header
+// dwords h1..h3 (see the layout above).
+REALM_DEV uint32_t q4k_dev_pair(uint32_t h1, uint32_t h2, uint32_t h3, int g)
+{
+    const uint32_t lo = g < 2 ? h1 : (g == 2 ? h2 : h3);
+    const uint32_t hi = g < 2 ? h2 : h3;
+    const uint32_t sh = (uint32_t)(24 * g) & 31u;
+    return (uint32_t)((((uint64_t)hi << 32) | lo) >> sh);
 }
 
 // fused.rs NaN/Inf scale replacement (crates/realm-compute-cpu/src/

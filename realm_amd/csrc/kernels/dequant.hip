@@ -88,8 +88,9 @@ extern "C" __global__ __launch_bounds__(256) void realm_dequant_q80(
 // ------------------------------------------------------------------ repack
 
 // Q4_K: a 144-byte block is nine 16-byte pieces (the raw buffer is 256-byte
-// aligned and 144 = 9*16): piece 0 -> hdr, piece 1 + 2g + h -> plane h of
-// unit 4*kb + g of the block's row.
+// aligned and 144 = 9*16): piece 0 -> hdr (scale/min pairs re-packed per
+// group, see common.h), piece 1 + 2g + h -> plane h of unit 4*kb + g of the
+// block's row, high nibbles XOR 8.
 extern "C" __global__ __launch_bounds__(256) void realm_repack_q4k(
     const uint8_t *__restrict__ raw, uint8_t *__restrict__ hdr, uint8_t *__restrict__ qs,
     long long nblocks, int blocks_per_row)
@@ -101,6 +102,21 @@ extern "C" __global__ __launch_bounds__(256) void realm_repack_q4k(
     int piece = (int)(gid - b * 9);
     uint4 v = ldg16(raw + b * Q4K_BLOCK_BYTES + 16 * piece);
     if (piece == 0) {
+        uint64_t f0 = 0, f1 = 0; // 96-bit field, low and high parts
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            uint32_t sl, ml, sh, mh;
+            q4k_scale_min_pair(v.y, v.z, v.w, g, sl, ml, sh, mh);
+            const uint64_t pair = sl | (ml << 6) | (sh << 12) | (mh << 18);
+            const int at = 24 * g; // 0, 24, 48, 72
+            if (at < 64)
+                f0 |= pair << at;
+            if (at + 24 > 64)
+                f1 |= at < 64 ? pair >> (64 - at) : pair << (at - 64);
+        }
+        v.y = (uint32_t)f0;
+        v.z = (uint32_t)(f0 >> 32);
+        v.w = (uint32_t)f1;
         *reinterpret_cast<uint4 *>(hdr + b * 16) = v;
         return;
     }
@@ -108,6 +124,10 @@ extern "C" __global__ __launch_bounds__(256) void realm_repack_q4k(
     int kb = (int)(b - row * blocks_per_row);
     int g = (piece - 1) >> 1, h = (piece - 1) & 1;
     long long U = 4LL * blocks_per_row;
+    v.x ^= 0x80808080u;
+    v.y ^= 0x80808080u;
+    v.z ^= 0x80808080u;
+    v.w ^= 0x80808080u;
     *reinterpret_cast<uint4 *>(qs + row * (U * 32) + h * (U * 16) + (4 * kb + g) * 16) = v;
 }
 

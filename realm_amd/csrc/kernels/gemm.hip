@@ -225,23 +225,17 @@ REALM_DEV void gemm_body(const GemmArgs &g)
                     q1 = ldg16(qp + U * 16); // plane 1
                     hd = ldg16(hdr + ((size_t)row * B + b) * 16);
                 }
-                w[a][0] = q0.x; w[a][1] = q0.y; w[a][2] = q0.z; w[a][3] = q0.w;
-                w[a][4] = q1.x; w[a][5] = q1.y; w[a][6] = q1.z; w[a][7] = q1.w;
+                // the device layout stores high nibbles XOR 8: undo it here
+                w[a][0] = q0.x ^ 0x80808080u; w[a][1] = q0.y ^ 0x80808080u;
+                w[a][2] = q0.z ^ 0x80808080u; w[a][3] = q0.w ^ 0x80808080u;
+                w[a][4] = q1.x ^ 0x80808080u; w[a][5] = q1.y ^ 0x80808080u;
+                w[a][6] = q1.z ^ 0x80808080u; w[a][7] = q1.w ^ 0x80808080u;
                 d[a] = fix_scale(f16_bits_to_f32(hd.x), 0.00000006f, g.nan_fb);
                 dm[a] = fix_scale(f16_bits_to_f32(hd.x >> 16), 0.00000024f, g.nan_fb);
                 // scale/min pair of sub-blocks 2c (low nibbles) and 2c+1 (high)
-                int sh = 16 * (c & 1);
-                uint32_t a0 = hd.y >> sh, a1 = hd.z >> sh, a2 = hd.w >> sh;
-                uint32_t sl, ml, shh, mh;
-                if (c < 2) {
-                    sl = a0 & 63u; ml = a1 & 63u;
-                    shh = (a0 >> 8) & 63u; mh = (a1 >> 8) & 63u;
-                } else {
-                    sl = (a2 & 0xFu) | (((a0 >> 6) & 3u) << 4);
-                    ml = ((a2 >> 4) & 0xFu) | (((a1 >> 6) & 3u) << 4);
-                    shh = ((a2 >> 8) & 0xFu) | (((a0 >> 14) & 3u) << 4);
-                    mh = ((a2 >> 12) & 0xFu) | (((a1 >> 14) & 3u) << 4);
-                }
+                const uint32_t pr = q4k_dev_pair(hd.y, hd.z, hd.w, c);
+                const uint32_t sl = pr & 63u, ml = (pr >> 6) & 63u;
+                const uint32_t shh = (pr >> 12) & 63u, mh = (pr >> 18) & 63u;
                 sc2[a][0] = splat2((float)sl);
                 cc2[a][0] = splat2(-1024.f * (float)sl);
                 sc2[a][1] = splat2((float)shh);

@@ -16,11 +16,13 @@
 // 32-byte qs group + the block header; Q6_K: one 48-byte ql/qh group + 4
 // sub-scales + d; Q8_0: two 34-byte blocks).  LPR lanes share a row; lane l
 // owns units l, l+LPR, ... (UPL of them) of every row it visits, and a wave
-// handles 64/LPR row slots of R rows per pass.  The grid is persistent: each
-// wave strides over passes and keeps two in flight (the next pass's weights
-// load while the current one computes).  Quantized x lives in LDS as one
-// 16-byte record per (unit, dword position), laid out [position][unit], so
-// lanes of a wave read consecutive records (no bank conflicts).
+// covers 64/LPR rows per pass.  The grid has at most one workgroup per CU;
+// each wave strides over passes and keeps a ring of D passes in flight, all
+// issued before its first pass is computed (the host picks D so that a
+// wave's passes usually all fit: the whole weight stream is requested up
+// front).  Quantized x lives in LDS as one 16-byte record per (unit, dword
+// position), laid out [position][unit], so lanes of a wave read consecutive
+// records (no bank conflicts).
 #include "common.h"
 #include "kernel_args.h"
 
@@ -93,8 +95,9 @@ REALM_DEV uint32_t pack4(int a, int b, int c, int d)
 //     (xh, xl of block 2u elements 4i..4i+3, xh, xl of block 2u+1 elements 4i..)
 //   Q6_K (unit = 16-runs t = 0..3 of one 64-weight group; pos = 2i + (t>>1)):
 //     (xh, xl of run t = 2(pos&1) elements 4i.., xh, xl of run t+1 ...)
-// meta[u] (float4; Q6_K: two float4 per unit) holds the x-block scales and
-// the sums s*(sum xh + sum xl/254) of the elements the unit covers.
+// meta[u] (float4; Q4_K and Q6_K: two float4 per unit, meta[2u], meta[2u+1])
+// holds the x-block scales and the sums s*(sum xh + sum xl/254) of the
+// elements the unit covers, in the form each format's dot product uses.
 //
 // Round rd covers 4-element chunks gid = rd*TH + tid (TH threads per
 // workgroup), i.e. x block gid/8, chunk gid%8.  x_round() loads one round;
@@ -159,101 +162,108 @@ REALM_DEV void quant_round(int4 *rec, float4 *meta, float4 v, int U, int rd)
         r[2 * half] = (int)dh;
         r[2 * half + 1] = (int)dl;
         if (c8 == 0) {
-            float *m = reinterpret_cast<float *>(&meta[u]);
-            m[half] = s;
-            m[2 + half] = part + other; // whole block of 32
+            const float sum = part + other; // whole block of 32
+            if (FMT == FMT_Q4K) {
+                // (s_a/254, s_b/(254*16), Sx_a, Sx_b), (8 Sx_b, ...): the
+                // high-nibble dot products carry a factor 16 and a -8 offset
+                float *m = reinterpret_cast<float *>(&meta[2 * u]);
+                m[half] = s * (half ? 1.f / (254.f * 16.f) : 1.f / 254.f);
+                m[2 + half] = sum;
+                if (half)
+                    m[4] = 8.f * sum;
+            } else {
+                float *m = reinterpret_cast<float *>(&meta[u]);
+                m[half] = s;
+                m[2 + half] = sum;
+            }
         }
     }
 }
 
-// Scale/min pair for sub-blocks 2g and 2g+1 from header dwords s0,s1,s2
-// (crates/realm-core/src/quant.rs:110-122) with g known only at run time.
-REALM_DEV void q4k_pair_rt(uint32_t s0, uint32_t s1, uint32_t s2, int g, float &sc_lo,
-                           float &m_lo, float &sc_hi, float &m_hi)
-{
-    int sh = 16 * (g & 1); // byte 2g&3 of a dword
-    uint32_t a0 = s0 >> sh, a1 = s1 >> sh, a2 = s2 >> sh;
-    uint32_t sl, ml, shh, mh;
-    if (g < 2) {
-        sl = a0 & 63u;
-        ml = a1 & 63u;
-        shh = (a0 >> 8) & 63u;
-        mh = (a1 >> 8) & 63u;
-    } else {
-        sl = (a2 & 0xFu) | (((a0 >> 6) & 3u) << 4);
-        ml = ((a2 >> 4) & 0xFu) | (((a1 >> 6) & 3u) << 4);
-        shh = ((a2 >> 8) & 0xFu) | (((a0 >> 14) & 3u) << 4);
-        mh = ((a2 >> 12) & 0xFu) | (((a1 >> 14) & 3u) << 4);
-    }
-    sc_lo = (float)sl;
-    m_lo = (float)ml;
-    sc_hi = (float)shh;
-    m_hi = (float)mh;
-}
+// Per-format weight registers of one (row, unit) and their loader.  A pass
+// reads each stream at a wave-uniform row base (scalar registers) plus a
+// per-lane byte offset fixed for the whole kernel (the lane's row slot and
+// unit), so the loads take the SGPR-base + 32-bit VGPR-offset form and no
+// per-pass vector address arithmetic is needed.
+struct Bases {
+    const uint8_t *b0, *b1, *b2;
+};
 
-// Per-format weight registers of one (row, unit) and their loader.
 template <int FMT>
 struct Unit;
 
+// Q4_K: two 16-byte qs planes of the unit + the 16-byte block header.
 template <>
 struct Unit<FMT_Q4K> {
     uint4 q0, q1, hd;
-    __device__ __forceinline__ void load(const uint8_t *w0, const uint8_t *w1, const uint8_t *,
-                                         size_t row, int u, int K)
+    struct Off {
+        uint32_t q, h;
+    };
+    // row strides (bytes) of the hdr and qs streams
+    static __device__ __forceinline__ Off offsets(int slot, int u, int U)
     {
-        const size_t U = (size_t)(K >> 6);
-        const uint8_t *qp = w1 + row * (U * 32) + 16 * u;
-        q0 = ldg16(qp);          // plane 0
-        q1 = ldg16(qp + U * 16); // plane 1
-        hd = ldg16(w0 + (row * (size_t)(K >> 8) + (u >> 2)) * 16);
+        return {(uint32_t)(slot * U * 32 + u * 16), (uint32_t)(slot * U * 4 + (u >> 2) * 16)};
     }
-    __device__ __forceinline__ void zero() { q0 = q1 = hd = make_uint4(0, 0, 0, 0); }
+    static __device__ __forceinline__ size_t stride0(int U) { return (size_t)U * 4; }
+    static __device__ __forceinline__ size_t stride1(int U) { return (size_t)U * 32; }
+    static __device__ __forceinline__ size_t stride2(int) { return 0; }
+    __device__ __forceinline__ void load(const Bases &b, const Off &o, int U)
+    {
+        q0 = ldg16(b.b1 + o.q);
+        q1 = ldg16(b.b1 + o.q + (uint32_t)(U * 16));
+        hd = ldg16(b.b0 + o.h);
+    }
 };
 
+// Q6_K: three 16-byte quant planes, the unit's 4 sub-scales, the block's d.
 template <>
 struct Unit<FMT_Q6K> {
     uint4 qa, qb, qh;
     uint32_t sc, d;
-    __device__ __forceinline__ void load(const uint8_t *w0, const uint8_t *w1, const uint8_t *w2,
-                                         size_t row, int u, int K)
+    struct Off {
+        uint32_t q, s, d;
+    };
+    static __device__ __forceinline__ Off offsets(int slot, int u, int U)
     {
-        size_t B = (size_t)(K >> 8), U = 4 * B;
-        const uint8_t *qp = w2 + row * (U * 48) + 16 * u;
-        qa = ldg16(qp);
-        qb = ldg16(qp + U * 16);
-        qh = ldg16(qp + U * 32);
-        size_t blk = row * B + (u >> 2);
-        sc = ldg4(w1 + blk * 16 + 4 * (u & 3));
-        d = *reinterpret_cast<const uint16_t *>(w0 + blk * 2);
+        return {(uint32_t)(slot * U * 48 + u * 16),
+                (uint32_t)(slot * U * 4 + (u >> 2) * 16 + (u & 3) * 4),
+                (uint32_t)(slot * (U / 2) + (u >> 2) * 2)};
     }
-    __device__ __forceinline__ void zero()
+    static __device__ __forceinline__ size_t stride0(int U) { return (size_t)(U / 2); }
+    static __device__ __forceinline__ size_t stride1(int U) { return (size_t)U * 4; }
+    static __device__ __forceinline__ size_t stride2(int U) { return (size_t)U * 48; }
+    __device__ __forceinline__ void load(const Bases &b, const Off &o, int U)
     {
-        qa = qb = qh = make_uint4(0, 0, 0, 0);
-        sc = d = 0;
+        qa = ldg16(b.b2 + o.q);
+        qb = ldg16(b.b2 + o.q + (uint32_t)(U * 16));
+        qh = ldg16(b.b2 + o.q + (uint32_t)(U * 32));
+        sc = ldg4(b.b1 + o.s);
+        d = *reinterpret_cast<const uint16_t *>(b.b0 + o.d);
     }
 };
 
+// Q8_0 (rows padded to KP = 64 U): four 16-byte planes and the two f16
+// scales of the unit's blocks.
 template <>
 struct Unit<FMT_Q80> {
     uint4 q[4];
     uint32_t d;
-    // K here is the padded row length Kp
-    __device__ __forceinline__ void load(const uint8_t *w0, const uint8_t *w1, const uint8_t *,
-                                         size_t row, int u, int KP)
+    struct Off {
+        uint32_t q, d;
+    };
+    static __device__ __forceinline__ Off offsets(int slot, int u, int U)
     {
-        const size_t U = (size_t)(KP >> 6);
-        const uint8_t *qp = w1 + row * (size_t)KP + 16 * u;
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-            q[c] = ldg16(qp + c * (U * 16));
-        d = ldg4(w0 + (row * (size_t)(KP >> 5) + 2 * u) * 2);
+        return {(uint32_t)(slot * U * 64 + u * 16), (uint32_t)(slot * U * 4 + u * 4)};
     }
-    __device__ __forceinline__ void zero()
+    static __device__ __forceinline__ size_t stride0(int U) { return (size_t)U * 4; }
+    static __device__ __forceinline__ size_t stride1(int U) { return (size_t)U * 64; }
+    static __device__ __forceinline__ size_t stride2(int) { return 0; }
+    __device__ __forceinline__ void load(const Bases &b, const Off &o, int U)
     {
 #pragma unroll
         for (int c = 0; c < 4; ++c)
-            q[c] = make_uint4(0, 0, 0, 0);
-        d = 0;
+            q[c] = ldg16(b.b1 + o.q + (uint32_t)(c * U * 16));
+        d = ldg4(b.b0 + o.d);
     }
 };
 
@@ -268,33 +278,41 @@ REALM_DEV void unit_dot(const Unit<FMT> (&w)[R], const int4 *rec, const float4 *
                         int u, int nan_fb, float (&acc)[R])
 {
     if constexpr (FMT == FMT_Q4K) {
-        int hl[R], ll[R], hh[R], lh[R];
+        // low nibbles (sub-block 2g) read as int8 q in 0..15, high nibbles
+        // (sub-block 2g+1, stored XOR 8) masked as int8 16 * (q - 8)
+        int ha[R], la[R], hb[R], lb[R];
 #pragma unroll
         for (int r = 0; r < R; ++r)
-            hl[r] = ll[r] = hh[r] = lh[r] = 0;
+            ha[r] = la[r] = hb[r] = lb[r] = 0;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const int4 xq = rec[i * U + u];
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 uint32_t q = word(i < 4 ? w[r].q0 : w[r].q1, i & 3);
-                uint32_t lo = q & 0x0F0F0F0Fu, hi = (q >> 4) & 0x0F0F0F0Fu;
-                hl[r] = dot4(lo, (uint32_t)xq.x, hl[r]);
-                ll[r] = dot4(lo, (uint32_t)xq.y, ll[r]);
-                hh[r] = dot4(hi, (uint32_t)xq.z, hh[r]);
-                lh[r] = dot4(hi, (uint32_t)xq.w, lh[r]);
+                uint32_t lo = q & 0x0F0F0F0Fu, hi = q & 0xF0F0F0F0u;
+                ha[r] = dot4(lo, (uint32_t)xq.x, ha[r]);
+                la[r] = dot4(lo, (uint32_t)xq.y, la[r]);
+                hb[r] = dot4(hi, (uint32_t)xq.z, hb[r]);
+                lb[r] = dot4(hi, (uint32_t)xq.w, lb[r]);
             }
         }
-        const float4 m = meta[u]; // (s_lo, s_hi, sum_lo, sum_hi)
+        // (s_a/254, s_b/(254*16), Sx_a, Sx_b), (8 Sx_b, -, -, -)
+        const float4 m = meta[2 * u], m2 = meta[2 * u + 1];
         const int g = u & 3;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            float d = fix_scale(f16_bits_to_f32(w[r].hd.x), 0.00000006f, nan_fb);
-            float dm = fix_scale(f16_bits_to_f32(w[r].hd.x >> 16), 0.00000024f, nan_fb);
-            float sl, ml, sh, mh;
-            q4k_pair_rt(w[r].hd.y, w[r].hd.z, w[r].hd.w, g, sl, ml, sh, mh);
-            acc[r] += d * (sl * combine(hl[r], ll[r], m.x) + sh * combine(hh[r], lh[r], m.y)) -
-                      dm * (ml * m.z + mh * m.w);
+            const float d = fix_scale(f16_bits_to_f32(w[r].hd.x), 0.00000006f, nan_fb);
+            const float dm = fix_scale(f16_bits_to_f32(w[r].hd.x >> 16), 0.00000024f, nan_fb);
+            const uint32_t pr = q4k_dev_pair(w[r].hd.y, w[r].hd.z, w[r].hd.w, g);
+            const float sa = (float)(pr & 63u), ma = (float)((pr >> 6) & 63u);
+            const float sb = (float)((pr >> 12) & 63u), mb = (float)((pr >> 18) & 63u);
+            // exact integers: |ha*254 + la| < 2^24, |hb*254 + lb| < 2^28
+            const float fa = (float)(ha[r] * 254 + la[r]);
+            const float fb = (float)(hb[r] * 254 + lb[r]);
+            const float ta = m.x * fa;          // sum over sub-block a of q * x
+            const float tb = fmaf(m.y, fb, m2.x); // sum over b of (q - 8) x + 8 sum x
+            acc[r] += d * fmaf(sa, ta, sb * tb) - dm * fmaf(ma, m.z, mb * m.w);
         }
     } else if constexpr (FMT == FMT_Q6K) {
         int ph[R][4], pl[R][4];
@@ -363,9 +381,14 @@ REALM_DEV void unit_dot(const Unit<FMT> (&w)[R], const int4 *rec, const float4 *
 }
 
 
-template <int FMT, int LPR, int UPL, int R, int XR, int TH>
+// One launch: NM matrices (1, or up to REALM_GEMV_MAX_MATS with NM = 4)
+// that share x, rows concatenated.  LPR lanes share a row (64/LPR row slots
+// per wave and pass), lane l owns units l, l+LPR, ... (UPL of them), and
+// each wave keeps a ring of D passes in flight.
+template <int FMT, int LPR, int UPL, int D, int XR, int TH, int NM>
 REALM_DEV void gemv(const GemvArgs &a)
 {
+    using W = Unit<FMT>;
     extern __shared__ int4 lds[];
     const int K = a.K, KX = a.KX;
     const int U = KX >> 6;
@@ -374,13 +397,12 @@ REALM_DEV void gemv(const GemvArgs &a)
     const int lane = threadIdx.x & 63;
     const int slot = lane / LPR, l = lane % LPR;
     constexpr int wpb = TH / 64;
-    // wave-uniform: keeps pass/row/matrix bookkeeping (and the kernarg
-    // pointer tables) in scalar registers, out of the vector memory queue
+    constexpr int RPP = 64 / LPR; // rows per pass
+    // wave-uniform bookkeeping stays in scalar registers
     const int gw = __builtin_amdgcn_readfirstlane(blockIdx.x * wpb + (threadIdx.x >> 6));
     const int nw = gridDim.x * wpb;
-    constexpr int RPP = (64 / LPR) * R; // rows per pass per wave
     const int rs1 = a.row_start[1], rs2 = a.row_start[2], rs3 = a.row_start[3];
-    const int rows = a.row_start[REALM_GEMV_MAX_MATS];
+    const int rows = a.row_start[NM == 1 ? 1 : REALM_GEMV_MAX_MATS];
     const void *const w0[4] = {a.w0[0], a.w0[1], a.w0[2], a.w0[3]};
     const void *const w1[4] = {a.w1[0], a.w1[1], a.w1[2], a.w1[3]};
     const void *const w2[4] = {a.w2[0], a.w2[1], a.w2[2], a.w2[3]};
@@ -388,87 +410,97 @@ REALM_DEV void gemv(const GemvArgs &a)
     const float *const xp = a.x;
     const int nan_fb = a.nan_fb;
     // Every kernel argument is read here, in one batch of scalar loads ahead
-    // of the first vector load.  Left alone, the compiler sinks some of these
-    // loads next to their uses, behind the x loads, and each such batch is a
-    // round trip to the argument buffer on the kernel's critical path.
-    // (one statement, so that all of them are live at once)
-    asm volatile("" ::"s"(K), "s"(KX), "s"(nw), "s"(rs1), "s"(rs2), "s"(rs3), "s"(rows),
-                 "s"(xp), "s"(nan_fb), "s"(w0[0]), "s"(w0[1]), "s"(w0[2]), "s"(w0[3]),
-                 "s"(w1[0]), "s"(w1[1]), "s"(w1[2]), "s"(w1[3]), "s"(w2[0]), "s"(w2[1]),
-                 "s"(w2[2]), "s"(w2[3]), "s"(yv[0]), "s"(yv[1]), "s"(yv[2]), "s"(yv[3]),
-                 "s"(a.pad));
+    // of the first vector load (one statement, so all are live at once):
+    // left alone, the compiler sinks some of these loads next to their uses,
+    // and each batch is a round trip to the argument buffer on the kernel's
+    // critical path.
+    if constexpr (NM == 1)
+        asm volatile("" ::"s"(K), "s"(KX), "s"(nw), "s"(rows), "s"(xp), "s"(nan_fb),
+                     "s"(w0[0]), "s"(w1[0]), "s"(w2[0]), "s"(yv[0]), "s"(a.pad));
+    else
+        asm volatile("" ::"s"(K), "s"(KX), "s"(nw), "s"(rs1), "s"(rs2), "s"(rs3), "s"(rows),
+                     "s"(xp), "s"(nan_fb), "s"(w0[0]), "s"(w0[1]), "s"(w0[2]), "s"(w0[3]),
+                     "s"(w1[0]), "s"(w1[1]), "s"(w1[2]), "s"(w1[3]), "s"(w2[0]), "s"(w2[1]),
+                     "s"(w2[2]), "s"(w2[3]), "s"(yv[0]), "s"(yv[1]), "s"(yv[2]), "s"(yv[3]),
+                     "s"(a.pad));
     const int npass = (rows + RPP - 1) / RPP;
-    const int wk = FMT == FMT_Q80 ? KX : K; // row length of the quant stream
+    // this wave's passes: p = gw + i*nw for i < T
+    const int T = gw < npass ? (npass - gw + nw - 1) / nw : 0;
 
-    // matrix of a global row; pointer choice by selects, never by indexing
-    // the kernarg arrays with a per-lane value
-    auto mat_of = [&](int row) {
-        return (row >= rs1 ? 1 : 0) + (row >= rs2 ? 1 : 0) + (row >= rs3 ? 1 : 0);
-    };
-    auto pick = [](int m, auto v0, auto v1, auto v2, auto v3) {
-        return m == 0 ? v0 : (m == 1 ? v1 : (m == 2 ? v2 : v3));
-    };
-    // No branch writes the registers of an in-flight load (a branch makes the
-    // compiler wait for every outstanding load): a row past the end is
-    // clamped to the last row and a unit past the end to the last unit; the
-    // results of both are masked in finish.
-    auto load_pass = [&](Unit<FMT>(&w)[UPL][R], int p) {
-        const int r0 = p * RPP + slot * R;
+    // per-lane offsets, fixed for the kernel (a unit past the row end is
+    // clamped to the last unit and masked in finish)
+    typename W::Off off[UPL];
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const int row = min(r0 + r, rows - 1);
-            const int m = mat_of(row);
-            const size_t lr = (size_t)(row - pick(m, 0, rs1, rs2, rs3));
-            const uint8_t *p0 = (const uint8_t *)pick(m, w0[0], w0[1], w0[2], w0[3]);
-            const uint8_t *p1 = (const uint8_t *)pick(m, w1[0], w1[1], w1[2], w1[3]);
-            const uint8_t *p2 = (const uint8_t *)pick(m, w2[0], w2[1], w2[2], w2[3]);
-#pragma unroll
-            for (int j = 0; j < UPL; ++j)
-                w[j][r].load(p0, p1, p2, lr, min(l + j * LPR, U - 1), wk);
+    for (int j = 0; j < UPL; ++j)
+        off[j] = W::offsets(slot, min(l + j * LPR, U - 1), U);
+
+    // Row base of pass i of this wave.  Pass indices past the wave's last
+    // pass (ring slots with nothing left to do) re-read the wave's first
+    // pass: those loads hit lines already fetched instead of costing HBM
+    // traffic, and no load is ever conditional.
+    auto bases = [&](int i) {
+        const int p = i < T ? gw + i * nw : gw;
+        const int row0 = p * RPP;
+        int m = 0, lr = row0;
+        if constexpr (NM > 1) {
+            m = (row0 >= rs1 ? 1 : 0) + (row0 >= rs2 ? 1 : 0) + (row0 >= rs3 ? 1 : 0);
+            lr = row0 - (m == 0 ? 0 : (m == 1 ? rs1 : (m == 2 ? rs2 : rs3)));
         }
+        auto pick = [&](const void *const(&v)[4]) {
+            if constexpr (NM == 1)
+                return (const uint8_t *)v[0];
+            else
+                return (const uint8_t *)(m == 0 ? v[0] : (m == 1 ? v[1] : (m == 2 ? v[2] : v[3])));
+        };
+        return Bases{pick(w0) + (size_t)lr * W::stride0(U), pick(w1) + (size_t)lr * W::stride1(U),
+                     pick(w2) + (size_t)lr * W::stride2(U)};
     };
-    auto finish = [&](Unit<FMT>(&w)[UPL][R], int pp) {
-        float acc[R];
+    auto load_pass = [&](W(&w)[UPL], int i) {
+        const Bases b = bases(i);
 #pragma unroll
-        for (int r = 0; r < R; ++r)
-            acc[r] = 0.f;
+        for (int j = 0; j < UPL; ++j)
+            w[j].load(b, off[j], U);
+    };
+    auto finish = [&](W(&w)[UPL], int i) {
+        float acc = 0.f;
 #pragma unroll
         for (int j = 0; j < UPL; ++j) {
             const int u = l + j * LPR;
-            float part[R];
-#pragma unroll
-            for (int r = 0; r < R; ++r)
-                part[r] = 0.f;
-            unit_dot<FMT, R>(w[j], rec, meta, U, min(u, U - 1), nan_fb, part);
-#pragma unroll
-            for (int r = 0; r < R; ++r)
-                acc[r] += u < U ? part[r] : 0.f;
+            float part[1] = {0.f};
+            W one[1] = {w[j]};
+            unit_dot<FMT, 1>(one, rec, meta, U, min(u, U - 1), nan_fb, part);
+            acc += u < U ? part[0] : 0.f;
         }
-        const int r0 = pp * RPP + slot * R;
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            float v = group_total<LPR>(acc[r]);
-            const int row = r0 + r;
-            if (l == LPR - 1 && row < rows) {
-                const int m = mat_of(row);
-                float *y = pick(m, yv[0], yv[1], yv[2], yv[3]);
-                y[row - pick(m, 0, rs1, rs2, rs3)] = v;
+        const float v = group_total<LPR>(acc);
+        const int row = (gw + i * nw) * RPP + slot;
+        if (l == LPR - 1 && row < rows) {
+            if constexpr (NM == 1) {
+                yv[0][row] = v;
+            } else {
+                const int m = (row >= rs1 ? 1 : 0) + (row >= rs2 ? 1 : 0) + (row >= rs3 ? 1 : 0);
+                float *y = m == 0 ? yv[0] : (m == 1 ? yv[1] : (m == 2 ? yv[2] : yv[3]));
+                y[row - (m == 0 ? 0 : (m == 1 ? rs1 : (m == 2 ? rs2 : rs3)))] = v;
             }
         }
     };
 
-    // Prologue: x loads first (so waiting for x does not wait for weights),
-    // then the weights of the wave's first two passes, then x is quantized
-    // into LDS while those loads are in flight.
+    // Prologue: x loads first (waiting for x then does not wait for
+    // weights), then the first ring slot, then x is quantized into LDS while
+    // those weights are in flight.
     const int rounds = (16 * U + TH - 1) / TH;
     float4 xv[XR];
 #pragma unroll
     for (int rd = 0; rd < XR; ++rd)
         xv[rd] = x_round<TH>(xp, K, U, rd);
-    Unit<FMT> A[UPL][R], B[UPL][R];
-    int p = gw;
-    load_pass(A, p);
-    load_pass(B, p + nw);
+    // Every wave of the workgroup issues its x loads before any wave issues
+    // a weight load: the CU's vector memory path returns data in request
+    // order, so x requests queued behind other waves' weight requests would
+    // hold up the quantization (and the barrier) by a full weight fetch.
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    W w[D][UPL];
+    load_pass(w[0], 0);
 #pragma unroll
     for (int rd = 0; rd < XR; ++rd)
         if (rd < rounds)
@@ -476,72 +508,80 @@ REALM_DEV void gemv(const GemvArgs &a)
     for (int rd = XR; rd < rounds; ++rd)
         quant_round<FMT, TH>(rec, meta, x_round<TH>(xp, K, U, rd), U, rd);
     lds_barrier();
+    // The rest of the ring is issued only now: a larger burst ahead of the
+    // x staging would delay x (same memory queues) and so the first pass.
+#pragma unroll
+    for (int s = 1; s < D; ++s)
+        load_pass(w[s], s);
 
-    // Two passes in flight per wave: each computes while the other loads.
-    // The wave's passes are p = gw + i*nw, i < T.  Every load below is
-    // unconditional on the path that reaches it and every path into a join
-    // carries the same loads in flight (A then B), so each wait the compiler
-    // places covers exactly the pass about to be used.  No load is issued
-    // past the wave's last pass, except the prologue's B when T < 2 (the host
-    // sizes the grid so that T >= 2 wherever the matrix allows it).
-    int left = p < npass ? (npass - p + nw - 1) / nw : 0;
-    for (;;) {
-        if (left <= 2)
-            break;
-        finish(A, p);
-        load_pass(A, p + 2 * nw);
-        if (left == 3) {
-            finish(B, p + nw);
-            finish(A, p + 2 * nw);
-            return;
+    // Every load is unconditional on the path that reaches it and every
+    // path into a join carries the same D slots in flight, so each wait the
+    // compiler places is for exactly the slot about to be used.
+    int i = 0;
+    for (; i + D < T; i += D) {
+#pragma unroll
+        for (int s = 0; s < D; ++s) {
+            finish(w[s], i + s);
+            load_pass(w[s], i + s + D);
         }
-        finish(B, p + nw);
-        load_pass(B, p + 3 * nw);
-        p += 2 * nw;
-        left -= 2;
     }
-    if (left >= 1)
-        finish(A, p);
-    if (left >= 2)
-        finish(B, p + nw);
+#pragma unroll
+    for (int s = 0; s < D; ++s) {
+        if (i + s >= T)
+            break;
+        finish(w[s], i + s);
+    }
 }
 
 } // namespace
 
 // x rounds held in registers across the prologue: all of them for the
-// longest row a variant serves (64 * UPL units, 16 float4 each)
-#define GEMV_XR(UPL, TH) ((1024 * (UPL) + (TH) - 1) / (TH))
+// longest row a variant serves (64 * UPL units, 16 float4 each), at most 8
+// (further rounds are loaded after the weights)
+#define GEMV_XR(UPL, TH) ((1024 * (UPL) + (TH) - 1) / (TH) < 8 ? (1024 * (UPL) + (TH) - 1) / (TH) : 8)
+// Workgroup size by units per lane and ring depth: 1024 threads (<= 128
+// VGPRs) for one unit per lane and up to 4 passes in flight, fewer threads
+// and more registers beyond.
+#define GEMV_TH(UPL, D) \
+    ((UPL) == 1 ? ((D) <= 4 ? 1024 : 512) : ((UPL) == 2 || ((UPL) == 3 && (D) <= 2) ? 512 : 256))
 
-// Variant (lanes per row, units per lane, rows per pass, threads per
-// workgroup).  The workgroup size is a compile-time constant: at most 1024
-// threads (<= 128 VGPRs) while a lane owns one unit, fewer beyond.
-#define DEF_GEMV1(NAME, FMT, LPR, UPL, R, TH)                                                 \
-    extern "C" __global__ __launch_bounds__(TH) void                                         \
-        realm_gemv_##NAME##_l##LPR##_u##UPL##_r##R##_t##TH(GemvArgs a)                       \
+// Variant: lanes per row, units per lane, ring depth, matrices (1 or 4).
+#define DEF_GEMV1(NAME, FMT, LPR, UPL, D, NM)                                                 \
+    extern "C" __global__ __launch_bounds__(GEMV_TH(UPL, D)) void                            \
+        realm_gemv_##NAME##_l##LPR##_u##UPL##_d##D##_m##NM(GemvArgs a)                       \
     {                                                                                        \
-        gemv<FMT, LPR, UPL, R, GEMV_XR(UPL, TH), TH>(a);                                     \
+        gemv<FMT, LPR, UPL, D, GEMV_XR(UPL, GEMV_TH(UPL, D)), GEMV_TH(UPL, D), NM>(a);      \
     }
-#define DEF_GEMV_T(LPR, UPL, R, TH)              \
-    DEF_GEMV1(q4k, FMT_Q4K, LPR, UPL, R, TH)     \
-    DEF_GEMV1(q6k, FMT_Q6K, LPR, UPL, R, TH)     \
-    DEF_GEMV1(q80, FMT_Q80, LPR, UPL, R, TH)
-#define DEF_GEMV(LPR, UPL, R)                                             \
-    DEF_GEMV_T(LPR, UPL, R, 256)                                          \
-    DEF_GEMV_T(LPR, UPL, R, 512)                                          \
-    DEF_GEMV_T(LPR, UPL, R, 1024)
-#define DEF_GEMV_MID(UPL) DEF_GEMV_T(64, UPL, 1, 256) DEF_GEMV_T(64, UPL, 1, 512)
+#if REALM_GEMV_FMT == FMT_Q4K
+#define DEF_GEMV2(LPR, UPL, D, NM) DEF_GEMV1(q4k, FMT_Q4K, LPR, UPL, D, NM)
+#elif REALM_GEMV_FMT == FMT_Q6K
+#define DEF_GEMV2(LPR, UPL, D, NM) DEF_GEMV1(q6k, FMT_Q6K, LPR, UPL, D, NM)
+#else
+#define DEF_GEMV2(LPR, UPL, D, NM) DEF_GEMV1(q80, FMT_Q80, LPR, UPL, D, NM)
+#endif
+#define DEF_GEMV(LPR, UPL, D) DEF_GEMV2(LPR, UPL, D, 1) DEF_GEMV2(LPR, UPL, D, 4)
 
-// The variants the host chooses from.
-DEF_GEMV(16, 1, 1)
-DEF_GEMV(16, 1, 2)
-DEF_GEMV(32, 1, 1)
-DEF_GEMV(32, 1, 2)
-DEF_GEMV(64, 1, 1)
-DEF_GEMV(64, 1, 2)
-DEF_GEMV_MID(2)
-DEF_GEMV_MID(3)
-DEF_GEMV_T(64, 4, 1, 256)
-DEF_GEMV_T(64, 5, 1, 256)
-DEF_GEMV_T(64, 6, 1, 256)
-DEF_GEMV_T(64, 7, 1, 256)
-DEF_GEMV_T(64, 8, 1, 256)
+// The variants the host chooses from (ring depths per units-per-lane must
+// match the host's tables).
+#define DEF_GEMV_ONE_UNIT(LPR)                                                                \
+    DEF_GEMV(LPR, 1, 1) DEF_GEMV(LPR, 1, 2) DEF_GEMV(LPR, 1, 3) DEF_GEMV(LPR, 1, 4)           \
+        DEF_GEMV(LPR, 1, 6) DEF_GEMV(LPR, 1, 8) DEF_GEMV(LPR, 1, 12)
+DEF_GEMV_ONE_UNIT(16)
+DEF_GEMV_ONE_UNIT(32)
+DEF_GEMV_ONE_UNIT(64)
+DEF_GEMV(64, 2, 1)
+DEF_GEMV(64, 2, 2)
+DEF_GEMV(64, 2, 3)
+DEF_GEMV(64, 2, 4)
+DEF_GEMV(64, 3, 1)
+DEF_GEMV(64, 3, 2)
+DEF_GEMV(64, 3, 3)
+DEF_GEMV(64, 3, 4)
+DEF_GEMV(64, 3, 6)
+DEF_GEMV(64, 4, 1)
+DEF_GEMV(64, 4, 2)
+DEF_GEMV(64, 5, 1)
+DEF_GEMV(64, 5, 2)
+DEF_GEMV(64, 6, 1)
+DEF_GEMV(64, 7, 1)
+DEF_GEMV(64, 8, 1)

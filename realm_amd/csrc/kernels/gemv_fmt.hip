@@ -1,0 +1,6 @@
+// Translation unit of the GEMV variants of one weight format, selected with
+// -DREALM_GEMV_FMT=0 (Q4_K), 1 (Q6_K) or 2 (Q8_0).
+#ifndef REALM_GEMV_FMT
+#error "REALM_GEMV_FMT must be defined"
+#endif
+#include "gemv.hip"

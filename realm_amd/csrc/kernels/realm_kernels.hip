@@ -1,6 +1,7 @@
-// Single translation unit for the gfx950 code object (realm_kernels.hsaco)
-// that the host library embeds and loads with hipModuleLoadData.
+// Translation unit of the non-GEMV kernels (dequant/repack, MFMA GEMM,
+// dense).  The GEMV variants are compiled per weight format from
+// gemv_fmt.hip, in parallel; the host library embeds every code object and
+// loads each with hipModuleLoadData.
 #include "dequant.hip"
-#include "gemv.hip"
 #include "gemm.hip"
 #include "dense.hip"

@@ -49,12 +49,17 @@ def test_ctypes_binding_matches_header():
 
 def test_code_object_is_embedded_for_gfx950():
     from realm_amd import _lib, build
-    if not os.path.exists(build.HSACO):
-        pytest.skip("code object not built")
-    blob = open(build.HSACO, "rb").read()
-    assert blob[:4] == b"\x7fELF" and b"gfx950" in blob
+    paths = [os.path.join(build.LIB_DIR, name + ".hsaco") for name, _, _ in build.HSACO_UNITS]
+    if not all(os.path.exists(p) for p in paths):
+        pytest.skip("code objects not built")
     lib = open(_lib.LIB_PATH, "rb").read()
-    assert blob[:4096] in lib  # embedded verbatim
-    for k in (b"realm_gemv_q4k_l64_u1_r1_t512", b"realm_gemm_q4k_p4_bf16", b"realm_dequant_q6k",
+    blobs = b""
+    for p in paths:
+        blob = open(p, "rb").read()
+        assert blob[:4] == b"\x7fELF" and b"gfx950" in blob
+        assert blob[:4096] in lib  # embedded verbatim
+        blobs += blob
+    for k in (b"realm_gemv_q4k_l64_u1_d2_m1", b"realm_gemv_q6k_l64_u3_d2_m4",
+              b"realm_gemv_q80_l32_u1_d1_m1", b"realm_gemm_q4k_p4_bf16", b"realm_dequant_q6k",
               b"realm_lora_shrink_q4k_f32", b"realm_dense_f32"):
-        assert k in blob
+        assert k in blobs
