@@ -416,16 +416,22 @@ int run_gemv(const Weight *const *ws, int count, const float *d_x, float *const 
                      d_u3[] = {1, 2, 3, 4, 6}, d_u45[] = {1, 2}, d_big[] = {1};
     const int *ds = upl == 1 ? d_u1 : upl == 2 ? d_u2 : upl == 3 ? d_u3 : upl <= 5 ? d_u45 : d_big;
     const int nd = upl == 1 ? 7 : upl == 2 ? 4 : upl == 3 ? 5 : upl <= 5 ? 2 : 1;
-    auto threads_of = [&](int d) {
-        return upl == 1 ? (d <= 4 ? 1024 : 512) : (upl == 2 || (upl == 3 && d <= 2) ? 512 : 256);
+    auto threads_of = [&](int d) { // GEMV_TH in gemv.hip
+        return upl == 1 ? (d <= 4 ? 1024 : 512)
+                        : (upl <= 3 ? (d == 1 ? 1024 : (upl == 2 || d == 2 ? 512 : 256)) : 256);
     };
     const long cu = g_dev.cu_count;
     const long npass = ((long)rows + rpp - 1) / rpp;
-    // Occupancy first (measured: deeper rings cost registers and lose): one
-    // pass in flight per wave, except that a wave with one unit per lane and
-    // several passes keeps two, so its next pass loads while it computes.
-    const long nw1 = cu * (threads_of(1) / 64);
-    int d = (upl == 1 && npass > nw1) ? 2 : 1;
+    // Measured policy: one pass in flight per wave when the largest
+    // workgroups give each wave one pass; otherwise two (the next pass loads
+    // while the current one computes), which for 2-3 units per lane halves
+    // the workgroup (register budget).  Deeper rings cost more registers
+    // than they gain.
+    int d = 1;
+    if (upl == 1 && npass > cu * 16)
+        d = 2;
+    else if ((upl == 2 || upl == 3) && npass >= 2 * cu * 8)
+        d = 2;
     if (w.type == GGML_Q8_0 && d > 8) // its 12-deep ring does not fit the registers
         d = 8;
     if (const char *env = getenv("REALM_GEMV_D")) { // tuning override

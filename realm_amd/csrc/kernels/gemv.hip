@@ -69,25 +69,6 @@ REALM_DEV float group_total(float v)
     return v;
 }
 
-// Max over aligned groups of 8 lanes (one x block of 32 = 8 x float4) and sum
-// over aligned groups of 4 (one 16-element half block).
-REALM_DEV float max8(float v)
-{
-    v = fmaxf(v, __shfl_xor(v, 1, 64));
-    v = fmaxf(v, __shfl_xor(v, 2, 64));
-    return fmaxf(v, __shfl_xor(v, 4, 64));
-}
-REALM_DEV int sum4i(int v)
-{
-    v += __shfl_xor(v, 1, 64);
-    return v + __shfl_xor(v, 2, 64);
-}
-
-REALM_DEV uint32_t pack4(int a, int b, int c, int d)
-{
-    return (uint32_t)(a & 0xFF) | ((uint32_t)(b & 0xFF) << 8) | ((uint32_t)(c & 0xFF) << 16) |
-           ((uint32_t)(d & 0xFF) << 24);
-}
 
 // Quantize x into LDS.  rec[pos * U + u] (int4) holds, for unit u and dword
 // position pos, the xh and xl dwords its dot products need:
@@ -99,82 +80,112 @@ REALM_DEV uint32_t pack4(int a, int b, int c, int d)
 // holds the x-block scales and the sums s*(sum xh + sum xl/254) of the
 // elements the unit covers, in the form each format's dot product uses.
 //
-// Round rd covers 4-element chunks gid = rd*TH + tid (TH threads per
-// workgroup), i.e. x block gid/8, chunk gid%8.  x_round() loads one round;
-// quant_round() quantizes it.  The load is unconditional (clamped address,
-// value selected) so that no branch separates it from the weight loads that
-// follow: the workgroup size is a compile-time constant for the same reason
-// (blockDim is a memory load).
+// Round rd covers 8-element chunks gid = rd*TH + tid (TH threads per
+// workgroup): x block blk = gid/4 (32 elements), elements 8*(gid%4) .. +7,
+// so the four chunks of a block sit in one quad of lanes and the block's max
+// and sums reduce with two quad-permute DPP steps.  x_round() loads one
+// round (unconditionally: clamped address, value selected, so that no branch
+// separates it from the weight loads that follow; the workgroup size is a
+// compile-time constant for the same reason: blockDim is a memory load);
+// quant_round() quantizes it.
 template <int TH>
-REALM_DEV float4 x_round(const float *__restrict__ x, int K, int U, int rd)
+REALM_DEV void x_round(const float *__restrict__ x, int K, int U, int rd, float4 (&v)[2])
 {
     const int gid = rd * TH + threadIdx.x;
-    const int blk = gid >> 3, c8 = gid & 7;
-    const int e0 = 32 * blk + 4 * c8;
-    const float4 v = reinterpret_cast<const float4 *>(x)[min(e0, K - 4) >> 2];
-    return (blk < 2 * U && e0 < K) ? v : make_float4(0.f, 0.f, 0.f, 0.f);
+    const int blk = gid >> 2, e0 = 8 * gid; // e0 = 32 blk + 8 (gid % 4)
+    const bool live = blk < 2 * U && e0 < K; // K is a multiple of 32
+    const float4 *p = reinterpret_cast<const float4 *>(x) + (min(e0, K - 8) >> 2);
+    const float4 a = p[0], b = p[1], z = make_float4(0.f, 0.f, 0.f, 0.f);
+    v[0] = live ? a : z;
+    v[1] = live ? b : z;
+}
+
+REALM_DEV float quad_max(float v)
+{
+    v = fmaxf(v, dpp_f<0xB1, 0xF>(v)); // quad_perm [1,0,3,2]
+    return fmaxf(v, dpp_f<0x4E, 0xF>(v)); // quad_perm [2,3,0,1]
+}
+
+REALM_DEV uint32_t pack_u8(float b0, float b1, float b2, float b3)
+{
+    uint32_t r = __builtin_amdgcn_cvt_pk_u8_f32(b0, 0, 0u);
+    r = __builtin_amdgcn_cvt_pk_u8_f32(b1, 1, r);
+    r = __builtin_amdgcn_cvt_pk_u8_f32(b2, 2, r);
+    return __builtin_amdgcn_cvt_pk_u8_f32(b3, 3, r);
 }
 
 template <int FMT, int TH>
-REALM_DEV void quant_round(int4 *rec, float4 *meta, float4 v, int U, int rd)
+REALM_DEV void quant_round(int4 *rec, float4 *meta, const float4 (&v)[2], int U, int rd)
 {
     const int gid = rd * TH + threadIdx.x;
-    const int blk = gid >> 3, c8 = gid & 7;
+    const int blk = gid >> 2, part = gid & 3;
     const bool live = blk < 2 * U;
-    float amax = max8(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    const float xs[8] = {v[0].x, v[0].y, v[0].z, v[0].w, v[1].x, v[1].y, v[1].z, v[1].w};
+    float amax = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+        amax = fmaxf(amax, fabsf(xs[e]));
+    amax = quad_max(amax);
     const float s = amax * (1.f / 127.f);
     const float inv = amax > 0.f ? 127.f / amax : 0.f;
-    const float inv2 = amax > 0.f ? 254.f * 127.f / amax : 0.f;
-    const float xs[4] = {v.x, v.y, v.z, v.w};
-    int h[4], lo[4], sh = 0, sl = 0;
+    const float inv2 = 254.f * inv;
+    // xh = round(x/s) in [-127, 127]; xl = round((x - s xh) 254/s) in
+    // [-127, 127]; both biased by 128 into bytes, then xor 0x80 -> int8
+    // in biased form: hb = xh + 128 = rint(x inv + 128) and
+    // lb = xl + 128 = rint(x inv2 - 254 xh + 128) = rint(x inv2 + 32640 - 254 hb);
+    // |x inv - xh| <= 1/2 keeps |xl| <= 127
+    float hb[8], lb[8];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        h[e] = (int)rintf(xs[e] * inv);
-        lo[e] = max(-127, min(127, (int)rintf((xs[e] - s * (float)h[e]) * inv2)));
-        sh += h[e];
-        sl += lo[e];
+    for (int e = 0; e < 8; ++e) {
+        hb[e] = rintf(fmaf(xs[e], inv, 128.f));
+        lb[e] = rintf(fmaf(-254.f, hb[e], fmaf(xs[e], inv2, 32640.f)));
     }
-    sh = sum4i(sh);
-    sl = sum4i(sl);
-    const float part = s * ((float)sh + (float)sl * (1.f / 254.f)); // 16 elements
-    const float other = __shfl_xor(part, 4, 64);                      // the other half
+    const uint32_t dh0 = pack_u8(hb[0], hb[1], hb[2], hb[3]) ^ 0x80808080u;
+    const uint32_t dh1 = pack_u8(hb[4], hb[5], hb[6], hb[7]) ^ 0x80808080u;
+    const uint32_t dl0 = pack_u8(lb[0], lb[1], lb[2], lb[3]) ^ 0x80808080u;
+    const uint32_t dl1 = pack_u8(lb[4], lb[5], lb[6], lb[7]) ^ 0x80808080u;
+    const int sh = dot4(dh1, 0x01010101u, dot4(dh0, 0x01010101u, 0));
+    const int sl = dot4(dl1, 0x01010101u, dot4(dl0, 0x01010101u, 0));
+    float part_sum = s * ((float)sh + (float)sl * (1.f / 254.f)); // 8 elements
+    part_sum += dpp_f<0xB1, 0xF>(part_sum);                       // 16 elements
+    if (FMT != FMT_Q6K)
+        part_sum += dpp_f<0x4E, 0xF>(part_sum); // the whole block of 32
     if (!live)
         return;
-    const uint32_t dh = pack4(h[0], h[1], h[2], h[3]);
-    const uint32_t dl = pack4(lo[0], lo[1], lo[2], lo[3]);
     if (FMT == FMT_Q6K) {
         // x block blk of the 256-block B: h6 = (blk%8)/4, run t = blk%4; the
-        // chunk lies in 16-run is = c8/4 at dword position i = c8%4
+        // chunk lies in 16-run is = part/2 at dword positions 2(part%2) + k
         const int B = blk >> 3, h6 = (blk >> 2) & 1, t = blk & 3;
-        const int is = c8 >> 2, i = c8 & 3;
+        const int is = part >> 1, i0 = 2 * (part & 1);
         const int u = 4 * B + 2 * h6 + is;
-        int *r = reinterpret_cast<int *>(&rec[(2 * i + (t >> 1)) * U + u]);
-        r[2 * (t & 1)] = (int)dh;
-        r[2 * (t & 1) + 1] = (int)dl;
-        if (i == 0) {
+        int2 *r0 = reinterpret_cast<int2 *>(&rec[(2 * i0 + (t >> 1)) * U + u]) + (t & 1);
+        int2 *r1 = reinterpret_cast<int2 *>(&rec[(2 * (i0 + 1) + (t >> 1)) * U + u]) + (t & 1);
+        *r0 = make_int2((int)dh0, (int)dl0);
+        *r1 = make_int2((int)dh1, (int)dl1);
+        if ((part & 1) == 0) {
             float *m = reinterpret_cast<float *>(&meta[2 * u]);
-            m[t] = s;        // scale of run t
-            m[4 + t] = part; // sum over the run's 16 elements
+            m[t] = s;            // scale of run t
+            m[4 + t] = part_sum; // sum over the run's 16 elements
         }
     } else {
-        const int u = blk >> 1, half = blk & 1, i = c8;
-        int *r = reinterpret_cast<int *>(&rec[i * U + u]);
-        r[2 * half] = (int)dh;
-        r[2 * half + 1] = (int)dl;
-        if (c8 == 0) {
-            const float sum = part + other; // whole block of 32
+        const int u = blk >> 1, half = blk & 1;
+        int2 *r0 = reinterpret_cast<int2 *>(&rec[(2 * part) * U + u]) + half;
+        int2 *r1 = reinterpret_cast<int2 *>(&rec[(2 * part + 1) * U + u]) + half;
+        *r0 = make_int2((int)dh0, (int)dl0);
+        *r1 = make_int2((int)dh1, (int)dl1);
+        if (part == 0) {
             if (FMT == FMT_Q4K) {
                 // (s_a/254, s_b/(254*16), Sx_a, Sx_b), (8 Sx_b, ...): the
                 // high-nibble dot products carry a factor 16 and a -8 offset
                 float *m = reinterpret_cast<float *>(&meta[2 * u]);
                 m[half] = s * (half ? 1.f / (254.f * 16.f) : 1.f / 254.f);
-                m[2 + half] = sum;
+                m[2 + half] = part_sum;
                 if (half)
-                    m[4] = 8.f * sum;
+                    m[4] = 8.f * part_sum;
             } else {
                 float *m = reinterpret_cast<float *>(&meta[u]);
                 m[half] = s;
-                m[2 + half] = sum;
+                m[2 + half] = part_sum;
             }
         }
     }
@@ -462,13 +473,23 @@ REALM_DEV void gemv(const GemvArgs &a)
             w[j].load(b, off[j], U);
     };
     auto finish = [&](W(&w)[UPL], int i) {
+        // With several units per lane the x records the loop reuses are
+        // kept in registers but the per-unit scales and sums are re-read
+        // from LDS every pass (an opaque zero offset stops the compiler from
+        // hoisting them), which keeps a two-pass ring within the budget.
+        const float4 *mt = meta;
+        if constexpr (UPL >= 2) {
+            uint32_t zero = 0;
+            asm volatile("" : "+v"(zero));
+            mt = meta + zero;
+        }
         float acc = 0.f;
 #pragma unroll
         for (int j = 0; j < UPL; ++j) {
             const int u = l + j * LPR;
             float part[1] = {0.f};
             W one[1] = {w[j]};
-            unit_dot<FMT, 1>(one, rec, meta, U, min(u, U - 1), nan_fb, part);
+            unit_dot<FMT, 1>(one, rec, mt, U, min(u, U - 1), nan_fb, part);
             acc += u < U ? part[0] : 0.f;
         }
         const float v = group_total<LPR>(acc);
@@ -487,11 +508,11 @@ REALM_DEV void gemv(const GemvArgs &a)
     // Prologue: x loads first (waiting for x then does not wait for
     // weights), then the first ring slot, then x is quantized into LDS while
     // those weights are in flight.
-    const int rounds = (16 * U + TH - 1) / TH;
-    float4 xv[XR];
+    const int rounds = (8 * U + TH - 1) / TH;
+    float4 xv[XR][2];
 #pragma unroll
     for (int rd = 0; rd < XR; ++rd)
-        xv[rd] = x_round<TH>(xp, K, U, rd);
+        x_round<TH>(xp, K, U, rd, xv[rd]);
     // Every wave of the workgroup issues its x loads before any wave issues
     // a weight load: the CU's vector memory path returns data in request
     // order, so x requests queued behind other waves' weight requests would
@@ -505,8 +526,11 @@ REALM_DEV void gemv(const GemvArgs &a)
     for (int rd = 0; rd < XR; ++rd)
         if (rd < rounds)
             quant_round<FMT, TH>(rec, meta, xv[rd], U, rd);
-    for (int rd = XR; rd < rounds; ++rd)
-        quant_round<FMT, TH>(rec, meta, x_round<TH>(xp, K, U, rd), U, rd);
+    for (int rd = XR; rd < rounds; ++rd) {
+        float4 v[2];
+        x_round<TH>(xp, K, U, rd, v);
+        quant_round<FMT, TH>(rec, meta, v, U, rd);
+    }
     lds_barrier();
     // The rest of the ring is issued only now: a larger burst ahead of the
     // x staging would delay x (same memory queues) and so the first pass.
@@ -536,14 +560,15 @@ REALM_DEV void gemv(const GemvArgs &a)
 } // namespace
 
 // x rounds held in registers across the prologue: all of them for the
-// longest row a variant serves (64 * UPL units, 16 float4 each), at most 8
-// (further rounds are loaded after the weights)
-#define GEMV_XR(UPL, TH) ((1024 * (UPL) + (TH) - 1) / (TH) < 8 ? (1024 * (UPL) + (TH) - 1) / (TH) : 8)
+// longest row a variant serves (64 * UPL units, 8 chunks of 8 elements
+// each), at most 8 (further rounds are loaded after the weights)
+#define GEMV_XR(UPL, TH) ((512 * (UPL) + (TH) - 1) / (TH) < 8 ? (512 * (UPL) + (TH) - 1) / (TH) : 8)
 // Workgroup size by units per lane and ring depth: 1024 threads (<= 128
 // VGPRs) for one unit per lane and up to 4 passes in flight, fewer threads
 // and more registers beyond.
-#define GEMV_TH(UPL, D) \
-    ((UPL) == 1 ? ((D) <= 4 ? 1024 : 512) : ((UPL) == 2 || ((UPL) == 3 && (D) <= 2) ? 512 : 256))
+#define GEMV_TH(UPL, D)                                                                    \
+    ((UPL) == 1 ? ((D) <= 4 ? 1024 : 512)                                                    \
+                : ((UPL) <= 3 ? ((D) == 1 ? 1024 : ((UPL) == 2 || (D) == 2 ? 512 : 256)) : 256))
 
 // Variant: lanes per row, units per lane, ring depth, matrices (1 or 4).
 #define DEF_GEMV1(NAME, FMT, LPR, UPL, D, NM)                                                 \
