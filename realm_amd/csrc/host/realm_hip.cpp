@@ -422,16 +422,18 @@ int run_gemv(const Weight *const *ws, int count, const float *d_x, float *const 
     };
     const long cu = g_dev.cu_count;
     const long npass = ((long)rows + rpp - 1) / rpp;
-    // Measured policy: one pass in flight per wave when the largest
-    // workgroups give each wave one pass; otherwise two (the next pass loads
-    // while the current one computes), which for 2-3 units per lane halves
-    // the workgroup (register budget).  Deeper rings cost more registers
-    // than they gain.
+    // Measured policy: with one unit per lane, all of a wave's passes in
+    // flight when there are at most 3, else two (the next pass loads while
+    // the current one computes); with 2-3 units per lane two passes once
+    // the halved workgroup (register budget) leaves each wave two of them.
+    // Deeper rings cost more registers than they gain.
     int d = 1;
-    if (upl == 1 && npass > cu * 16)
+    if (upl == 1) {
+        const long t1 = (npass + cu * 16 - 1) / (cu * 16); // passes per wave
+        d = t1 <= 3 ? (int)std::max<long>(t1, 1) : 2;
+    } else if ((upl == 2 || upl == 3) && npass >= 2 * cu * 8) {
         d = 2;
-    else if ((upl == 2 || upl == 3) && npass >= 2 * cu * 8)
-        d = 2;
+    }
     if (w.type == GGML_Q8_0 && d > 8) // its 12-deep ring does not fit the registers
         d = 8;
     if (const char *env = getenv("REALM_GEMV_D")) { // tuning override

@@ -446,11 +446,14 @@ REALM_DEV void gemv(const GemvArgs &a)
         off[j] = W::offsets(slot, min(l + j * LPR, U - 1), U);
 
     // Row base of pass i of this wave.  Pass indices past the wave's last
-    // pass (ring slots with nothing left to do) re-read the wave's first
-    // pass: those loads hit lines already fetched instead of costing HBM
-    // traffic, and no load is ever conditional.
+    // pass (ring slots with nothing left to do) re-read the wave's last
+    // pass, whose lines were just fetched (no HBM traffic), so no load is
+    // ever conditional; a wave with no pass at all reads the matrix's last
+    // pass.  Every pass read is < npass, so with the 4 padding rows every
+    // address stays inside the allocation.
+    const int p_last = T > 0 ? gw + (T - 1) * nw : npass - 1;
     auto bases = [&](int i) {
-        const int p = i < T ? gw + i * nw : gw;
+        const int p = i < T ? gw + i * nw : p_last;
         const int row0 = p * RPP;
         int m = 0, lr = row0;
         if constexpr (NM > 1) {
