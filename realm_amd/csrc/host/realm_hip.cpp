@@ -457,56 +457,78 @@ int run_gemv(const Weight *const *ws, int count, const float *d_x, float *const 
     return launch(name, dim3((unsigned)std::max<long>(wgs, 1)), dim3(threads), lds, s, args);
 }
 
-// Any M: activation prep, optional LoRA shrink, then the MFMA kernel.
-int run_gemm(const Weight &w, const void *d_x, bool bf16, size_t M, float *d_y, hipStream_t s,
-             const LoraCall *lora)
+// MFMA path for any M: activation prep (once per input, shared by a group
+// of weights), optional LoRA shrink, then the MFMA kernel.
+struct GemmTile {
+    std::string name;
+    unsigned rows_per_wg, toks_per_wg, threads;
+};
+
+// small batches (16 rows x 8/16/32 tokens, K split over the workgroup's
+// 16/TM waves; f32 input packs a token's hi/lo parts into two MFMA slots),
+// decode tiles (16 rows x 64 tokens, K split over 4 waves) or the prefill
+// tile (128 rows x 64 tokens)
+GemmTile gemm_tile(size_t M, bool bf16)
 {
-    if (M == 0 || w.n == 0)
-        return REALM_OK;
-    // tile choice: decode tiles (16 rows x 16/32/64 tokens, K split over 4
-    // waves) or the prefill tile (128 rows x 64 tokens)
     size_t M16 = round_up(M, 16);
-    std::string tile;
-    unsigned rows_per_wg, toks_per_wg;
-    if (M16 >= 128) {
-        tile = "p4";
-        rows_per_wg = 128;
-        toks_per_wg = 64;
-    } else if (M16 <= 16) {
-        tile = "d1";
-        rows_per_wg = 16;
-        toks_per_wg = 16;
-    } else if (M16 <= 32 && !bf16) {
-        tile = "d2";
-        rows_per_wg = 16;
-        toks_per_wg = 32;
-    } else {
-        tile = "d4";
-        rows_per_wg = 16;
-        toks_per_wg = 64;
+    if (!bf16 && M <= 32) {
+        if (M <= 8)
+            return {"s1", 16, 8, 1024};
+        return M <= 16 ? GemmTile{"s2", 16, 16, 512} : GemmTile{"s4", 16, 32, 256};
     }
+    if (bf16 && M <= 32)
+        return M <= 16 ? GemmTile{"s1", 16, 16, 1024} : GemmTile{"s2", 16, 32, 512};
+    if (M16 >= 128)
+        return {"p4", 128, 64, 256};
+    if (M16 <= 16)
+        return {"d1", 16, 16, 256};
+    if (M16 <= 32 && !bf16)
+        return {"d2", 16, 32, 256};
+    return {"d4", 16, 64, 256};
+}
+
+struct XPrep {
+    void *xh = nullptr, *xl = nullptr, *xm = nullptr, *ts = nullptr;
+    size_t Mp = 0;
+};
+
+// xprep limit: the kernel holds 4 rounds of 1024 x 8 positions per thread
+constexpr size_t XPREP_MAX_KX = 32768;
+
+int prep_x(const Weight &w, const void *d_x, bool bf16, size_t M, const GemmTile &tile,
+           hipStream_t s, XPrep *p)
+{
+    if (w.kx > XPREP_MAX_KX)
+        return fail(REALM_INVALID_ARGUMENT,
+                    "K " + std::to_string(w.k) + " exceeds the batched path's limit of " +
+                        std::to_string(XPREP_MAX_KX));
     // every token a workgroup reads must exist in the prepared activations
-    size_t Mp = round_up(M, toks_per_wg);
+    p->Mp = round_up(M, tile.toks_per_wg);
     size_t B = w.k / 256;
-    void *xh, *xl = nullptr, *xm = nullptr, *ts;
-    CHECK(ws_get(s, WS_XH, Mp * w.kx * 2, &xh));
+    CHECK(ws_get(s, WS_XH, p->Mp * w.kx * 2, &p->xh));
     if (!bf16)
-        CHECK(ws_get(s, WS_XL, Mp * w.kx * 2, &xl));
+        CHECK(ws_get(s, WS_XL, p->Mp * w.kx * 2, &p->xl));
+    else
+        p->xl = nullptr;
     if (w.type == GGML_Q4_K)
-        CHECK(ws_get(s, WS_XM, Mp * B * 64, &xm));
-    CHECK(ws_get(s, WS_TS, Mp * 4, &ts));
-    {
-        int ibf = bf16 ? 1 : 0, iM = (int)M, iK = (int)w.k, iKX = (int)w.kx;
-        void *args[] = {(void *)&d_x, &ibf, &xh, &xl, &xm, &ts, &iM, &iK, &iKX};
-        CHECK(launch(std::string("realm_xprep_") + fmt_name(w.type), dim3((unsigned)Mp),
-                     dim3(256), 0, s, args));
-    }
+        CHECK(ws_get(s, WS_XM, p->Mp * B * 64, &p->xm));
+    CHECK(ws_get(s, WS_TS, p->Mp * 4, &p->ts));
+    int ibf = bf16 ? 1 : 0, iM = (int)M, iK = (int)w.k, iKX = (int)w.kx;
+    void *args[] = {(void *)&d_x, &ibf, &p->xh, &p->xl, &p->xm, &p->ts, &iM, &iK, &iKX};
+    return launch(std::string("realm_xprep_") + fmt_name(w.type), dim3((unsigned)p->Mp),
+                  dim3(1024), 0, s, args);
+}
+
+int gemm_launch(const Weight &w, const XPrep &p, bool bf16, size_t M, const GemmTile &tile,
+                float *d_y, hipStream_t s, const LoraCall *lora)
+{
     void *u = nullptr;
     if (lora) {
         const AdapterSet &set = *lora->set;
-        CHECK(ws_get(s, WS_U, Mp * (size_t)set.rmax * 4, &u));
+        CHECK(ws_get(s, WS_U, p.Mp * (size_t)set.rmax * 4, &u));
         const void *table = set.table;
         const int32_t *ids = lora->d_ids;
+        void *xh = p.xh, *xl = p.xl, *ts = p.ts;
         int iM = (int)M, iK = (int)w.k, iKX = (int)w.kx, rmax = set.rmax;
         void *args[] = {&xh, &xl, &ts, (void *)&ids, (void *)&table, &u, &iM, &iK, &iKX, &rmax};
         std::string name = std::string("realm_lora_shrink_") + fmt_name(w.type) +
@@ -519,17 +541,17 @@ int run_gemm(const Weight &w, const void *d_x, bool bf16, size_t M, float *d_y, 
     std::string fmt = fmt_name(w.type);
     if (w.type == GGML_Q6_K && w.wide)
         fmt = "q6kw";
-    std::string name = "realm_gemm_" + fmt + "_" + tile + (bf16 ? "_bf16" : "_f32") +
+    std::string name = "realm_gemm_" + fmt + "_" + tile.name + (bf16 ? "_bf16" : "_f32") +
                        (lora ? "_lora" : "");
     GemmArgs g;
     std::memset(&g, 0, sizeof g);
     g.w0 = w.w0;
     g.w1 = w.w1;
     g.w2 = w.w2;
-    g.xh = xh;
-    g.xl = xl;
-    g.xm = xm;
-    g.tscale = (const float *)ts;
+    g.xh = p.xh;
+    g.xl = p.xl;
+    g.xm = p.xm;
+    g.tscale = (const float *)p.ts;
     g.y = d_y;
     g.N = (int)w.n;
     g.K = (int)w.k;
@@ -544,9 +566,20 @@ int run_gemm(const Weight &w, const void *d_x, bool bf16, size_t M, float *d_y, 
         g.rmax = lora->set->rmax;
     }
     void *args[] = {&g};
-    dim3 grid((unsigned)((w.n + rows_per_wg - 1) / rows_per_wg),
-              (unsigned)((Mp + toks_per_wg - 1) / toks_per_wg));
-    return launch(name, grid, dim3(256), 0, s, args);
+    dim3 grid((unsigned)((w.n + tile.rows_per_wg - 1) / tile.rows_per_wg),
+              (unsigned)((p.Mp + tile.toks_per_wg - 1) / tile.toks_per_wg));
+    return launch(name, grid, dim3(tile.threads), 0, s, args);
+}
+
+int run_gemm(const Weight &w, const void *d_x, bool bf16, size_t M, float *d_y, hipStream_t s,
+             const LoraCall *lora)
+{
+    if (M == 0 || w.n == 0)
+        return REALM_OK;
+    const GemmTile tile = gemm_tile(M, bf16);
+    XPrep p;
+    CHECK(prep_x(w, d_x, bf16, M, tile, s, &p));
+    return gemm_launch(w, p, bf16, M, tile, d_y, s, lora);
 }
 
 int run_matmul(const Weight &w, const void *d_x, bool bf16, size_t M, float *d_y,
@@ -939,8 +972,17 @@ REALM_API int realm_hip_weights_matmul_group_dev(const uint64_t *handles, size_t
         if (rc != REALM_BACKEND_UNSUPPORTED)
             return rc;
     }
+    // batched: one activation prep for the whole group (the matrices share
+    // format and K, so the prepared layout is the same), then one MFMA launch
+    // per matrix
+    if (batch == 0)
+        return REALM_OK;
+    const GemmTile tile = gemm_tile(batch, false);
+    XPrep p;
+    CHECK(prep_x(w[0], d_input, false, batch, tile, s, &p));
     for (size_t i = 0; i < count; ++i)
-        CHECK(run_gemm(w[i], d_input, false, batch, d_outs[i], s, nullptr));
+        if (w[i].n)
+            CHECK(gemm_launch(w[i], p, false, batch, tile, d_outs[i], s, nullptr));
     return REALM_OK;
 }
 

@@ -83,30 +83,50 @@ REALM_DEV float load_x(const void *x, int bf16, size_t i)
 
 // ------------------------------------------------------------------ xprep
 //
-// One workgroup per (padded) token.  Writes, for token t:
+// One workgroup of 1024 threads per (padded) token.  Writes, for token t:
 //   xh[t][p], xl[t][p]  f16 hi/lo of x[t][k(p)] * 2^-e_t, p in [0, KX)
 //   xm[t][b][c][8]      Q4_K only: (Sxh(2c), Sxh(2c+1), Sxl(2c), Sxl(2c+1), 0...)
 //   tscale[t] = 2^e_t
-// Tokens t >= M get zeros.
+// Tokens t >= M get zeros.  Position group pg = p/8 (8 slots) is handled by
+// thread pg % 1024: it loads the 8 consecutive x of its k window once, takes
+// part in the token's max, then converts them; the Q4_K 32-element sums come
+// from the four threads of a half group (lanes 4 apart in one DPP row).
+#define XPREP_TH 1024
+#define XPREP_R 4 // position-group rounds held in registers: KX <= 32768
+
 template <int FMT>
 REALM_DEV void xprep(const void *__restrict__ x, int bf16, _Float16 *__restrict__ xh,
                      _Float16 *__restrict__ xl, _Float16 *__restrict__ xm,
                      float *__restrict__ tscale, int M, int K, int KX)
 {
-    __shared__ float red[4];
+    __shared__ float red[XPREP_TH / 64];
     const int t = blockIdx.x;
     const bool live = t < M;
     const size_t xrow = (size_t)t * K;
+    const int ngroups = KX >> 3;
+    float v[XPREP_R][8];
     float amax = 0.f;
-    if (live)
-        for (int k = threadIdx.x; k < K; k += blockDim.x)
-            amax = fmaxf(amax, fabsf(load_x(x, bf16, xrow + k)));
+#pragma unroll
+    for (int r = 0; r < XPREP_R; ++r) {
+        const int pg = r * XPREP_TH + threadIdx.x;
+        const int k0 = pg < ngroups ? kwin<FMT>(pg) : 0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int k = k0 + e;
+            v[r][e] = (live && pg < ngroups && k < K) ? load_x(x, bf16, xrow + k) : 0.f;
+            amax = fmaxf(amax, fabsf(v[r][e]));
+        }
+    }
+    // workgroup max: wave reduction (lane 63 ends with it), then LDS
     for (int off = 32; off > 0; off >>= 1)
         amax = fmaxf(amax, __shfl_xor(amax, off, 64));
     if ((threadIdx.x & 63) == 0)
         red[threadIdx.x >> 6] = amax;
     __syncthreads();
-    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    amax = 0.f;
+#pragma unroll
+    for (int w = 0; w < XPREP_TH / 64; ++w)
+        amax = fmaxf(amax, red[w]);
     int e = 0;
     if (amax > 0.f && __builtin_isfinite(amax)) {
         int ex;
@@ -118,46 +138,46 @@ REALM_DEV void xprep(const void *__restrict__ x, int bf16, _Float16 *__restrict_
         tscale[t] = ldexpf(1.f, e);
 
     const size_t orow = (size_t)t * KX;
-    for (int pg = threadIdx.x; pg < KX / 8; pg += blockDim.x) {
-        int k0 = kwin<FMT>(pg);
+    const int B = K >> 8;
+#pragma unroll
+    for (int r = 0; r < XPREP_R; ++r) {
+        const int pg = r * XPREP_TH + threadIdx.x;
         _Float16 hv[8], lv[8];
+        float sum = 0.f; // of this thread's 8 x * down (its window)
 #pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            int k = k0 + pi8(s);
-            float v = (live && k < K) ? load_x(x, bf16, xrow + k) * down : 0.f;
-            _Float16 h = (_Float16)v;
-            hv[s] = h;
-            lv[s] = (_Float16)(v - (float)h);
+        for (int s2 = 0; s2 < 8; ++s2) {
+            const float val = v[r][pi8(s2)] * down;
+            const _Float16 h = (_Float16)val;
+            hv[s2] = h;
+            lv[s2] = (_Float16)(val - (float)h);
+            sum += val;
         }
-        *reinterpret_cast<uint4 *>(xh + orow + 8 * pg) = __builtin_bit_cast(uint4, hv);
-        if (xl)
-            *reinterpret_cast<uint4 *>(xl + orow + 8 * pg) = __builtin_bit_cast(uint4, lv);
-    }
-    if (FMT == FMT_Q4K) {
-        const int B = K >> 8;
-        for (int bc = threadIdx.x; bc < B * 4; bc += blockDim.x) {
-            int b = bc >> 2, c = bc & 3;
-            float s[2] = {0.f, 0.f};
-            if (live)
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    size_t k0 = xrow + 256 * b + 64 * c + 32 * h;
-                    float acc = 0.f;
-                    for (int j = 0; j < 32; ++j)
-                        acc += load_x(x, bf16, k0 + j) * down;
-                    s[h] = acc;
-                }
-            _Float16 h0 = (_Float16)s[0], h1 = (_Float16)s[1];
-            _Float16 v[8] = {h0, h1, (_Float16)(s[0] - (float)h0), (_Float16)(s[1] - (float)h1),
-                             (_Float16)0.f, (_Float16)0.f, (_Float16)0.f, (_Float16)0.f};
-            *reinterpret_cast<uint4 *>(xm + ((size_t)t * B + b) * 32 + 8 * c) =
-                __builtin_bit_cast(uint4, v);
+        if (pg < ngroups) {
+            *reinterpret_cast<uint4 *>(xh + orow + 8 * pg) = __builtin_bit_cast(uint4, hv);
+            if (xl)
+                *reinterpret_cast<uint4 *>(xl + orow + 8 * pg) = __builtin_bit_cast(uint4, lv);
+        }
+        if (FMT == FMT_Q4K) {
+            // pg = 32b + 4i + c: the half group (b, c, h = i/4) is the four
+            // threads pg, pg+4, pg+8, pg+12 of one 16-lane DPP row
+            sum += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sum), 0x124, 0xF, 0xF, false)); // row_ror:4
+            sum += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sum), 0x128, 0xF, 0xF, false)); // row_ror:8
+            const int b = pg >> 5, i = (pg >> 2) & 7, c = pg & 3, h = i >> 2;
+            if (pg < ngroups && b < B && (i & 3) == 0) {
+                const _Float16 sh = (_Float16)sum;
+                const _Float16 sl = (_Float16)(sum - (float)sh);
+                _Float16 *dst = xm + ((size_t)t * B + b) * 32 + 8 * c;
+                dst[h] = sh;
+                dst[2 + h] = sl;
+                if (h == 0)
+                    *reinterpret_cast<uint2 *>(dst + 4) = make_uint2(0u, 0u);
+            }
         }
     }
 }
 
 #define DEF_XPREP(NAME, FMT)                                                               \
-    extern "C" __global__ __launch_bounds__(256) void realm_xprep_##NAME(                 \
+    extern "C" __global__ __launch_bounds__(XPREP_TH) void realm_xprep_##NAME(            \
         const void *x, int bf16, _Float16 *xh, _Float16 *xl, _Float16 *xm, float *tscale, \
         int M, int K, int KX)                                                              \
     {                                                                                      \
@@ -178,15 +198,23 @@ REALM_DEV float lora_elem(const void *p, int dtype, size_t i)
 
 // ------------------------------------------------------------- main kernel
 
-template <int FMT, int TN, int TM, int KSPLIT, bool LO, bool WIDE, bool LORA>
+// WAVES waves per workgroup: WAVES / KSPLIT along rows, KSPLIT along K.
+// PACK (f32 activations only): the 16 MFMA token slots hold 8 tokens as
+// (hi, lo) pairs, slot 2t + p = part p of token t, so one MFMA covers both
+// parts and the epilogue adds the pair; otherwise a slot is one token and
+// the lo part (LO) takes a second MFMA.
+template <int FMT, int TN, int TM, int KSPLIT, bool LO, bool WIDE, bool LORA, int WAVES = 4,
+          bool PACK = false>
 REALM_DEV void gemm_body(const GemmArgs &g)
 {
-    constexpr int WN = 4 / KSPLIT; // waves along rows
+    constexpr int WN = WAVES / KSPLIT; // waves along rows
+    constexpr bool SEP = LO && !PACK;  // separate MFMAs for the lo part
+    constexpr int TOK = PACK ? 8 : 16; // tokens per 16-slot tile
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int wn = wave / KSPLIT, wk = wave % KSPLIT;
     const int r16 = lane & 15, c = lane >> 4;
     const int n0 = blockIdx.x * (WN * 16 * TN) + wn * 16 * TN;
-    const int t0 = blockIdx.y * (16 * TM);
+    const int t0 = blockIdx.y * (TOK * TM);
     const int K = g.K, KX = g.KX, N = g.N;
 
     floatx4 acc[TN][TM];
@@ -196,14 +224,20 @@ REALM_DEV void gemm_body(const GemmArgs &g)
         for (int b = 0; b < TM; ++b)
             acc[a][b] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    // activation row pointers for this lane's token in each token tile
+    // activation row pointers for this lane's slot in each token tile
     const _Float16 *xrow_h[TM];
     const _Float16 *xrow_l[TM];
 #pragma unroll
     for (int b = 0; b < TM; ++b) {
-        size_t tok = (size_t)(t0 + 16 * b + r16);
-        xrow_h[b] = (const _Float16 *)g.xh + tok * KX + 8 * c;
-        xrow_l[b] = LO ? (const _Float16 *)g.xl + tok * KX + 8 * c : nullptr;
+        if (PACK) {
+            size_t tok = (size_t)(t0 + TOK * b + (r16 >> 1));
+            xrow_h[b] = (const _Float16 *)((r16 & 1) ? g.xl : g.xh) + tok * KX + 8 * c;
+            xrow_l[b] = nullptr;
+        } else {
+            size_t tok = (size_t)(t0 + 16 * b + r16);
+            xrow_h[b] = (const _Float16 *)g.xh + tok * KX + 8 * c;
+            xrow_l[b] = LO ? (const _Float16 *)g.xl + tok * KX + 8 * c : nullptr;
+        }
     }
 
     if (FMT == FMT_Q4K) {
@@ -255,7 +289,7 @@ REALM_DEV void gemm_body(const GemmArgs &g)
 #pragma unroll
                 for (int bb = 0; bb < TM; ++bb) {
                     ah[bb] = ld_h8(xrow_h[bb] + 256 * b + 32 * i);
-                    if (LO)
+                    if (SEP)
                         al[bb] = ld_h8(xrow_l[bb] + 256 * b + 32 * i);
                 }
 #pragma unroll
@@ -274,7 +308,7 @@ REALM_DEV void gemm_body(const GemmArgs &g)
 #pragma unroll
                     for (int bb = 0; bb < TM; ++bb) {
                         P[a][bb] = mfma(ah[bb], bf, P[a][bb]);
-                        if (LO)
+                        if (SEP)
                             P[a][bb] = mfma(al[bb], bf, P[a][bb]);
                     }
                 }
@@ -282,8 +316,11 @@ REALM_DEV void gemm_body(const GemmArgs &g)
             // min term: one MFMA on (Sx hi, Sx lo) x (m, m) slots
 #pragma unroll
             for (int bb = 0; bb < TM; ++bb) {
-                size_t tok = (size_t)(t0 + 16 * bb + r16);
+                // packed: the hi slot of a token carries its whole min term
+                size_t tok = PACK ? (size_t)(t0 + TOK * bb + (r16 >> 1)) : (size_t)(t0 + 16 * bb + r16);
                 half8_t am = ld_h8((const _Float16 *)g.xm + (tok * B + b) * 32 + 8 * c);
+                if (PACK && (r16 & 1))
+                    am = half8_t{};
 #pragma unroll
                 for (int a = 0; a < TN; ++a) {
                     half8_t bm = h8(mfrag[a], mfrag[a], 0u, 0u);
@@ -346,7 +383,7 @@ REALM_DEV void gemm_body(const GemmArgs &g)
 #pragma unroll
                 for (int bb = 0; bb < TM; ++bb) {
                     ah[bb] = ld_h8(xrow_h[bb] + 256 * b + 32 * i);
-                    if (LO)
+                    if (SEP)
                         al[bb] = ld_h8(xrow_l[bb] + 256 * b + 32 * i);
                 }
 #pragma unroll
@@ -373,11 +410,11 @@ REALM_DEV void gemm_body(const GemmArgs &g)
 #pragma unroll
                     for (int bb = 0; bb < TM; ++bb) {
                         P[a][bb] = mfma(ah[bb], bf, P[a][bb]);
-                        if (LO)
+                        if (SEP)
                             P[a][bb] = mfma(al[bb], bf, P[a][bb]);
                         if (WIDE) {
                             P[a][bb] = mfma(ah[bb], bh, P[a][bb]);
-                            if (LO)
+                            if (SEP)
                                 P[a][bb] = mfma(al[bb], bh, P[a][bb]);
                         }
                     }
@@ -401,7 +438,7 @@ REALM_DEV void gemm_body(const GemmArgs &g)
 #pragma unroll
             for (int bb = 0; bb < TM; ++bb) {
                 ah[bb] = ld_h8(xrow_h[bb] + 32 * kb);
-                if (LO)
+                if (SEP)
                     al[bb] = ld_h8(xrow_l[bb] + 32 * kb);
             }
 #pragma unroll
@@ -427,7 +464,7 @@ REALM_DEV void gemm_body(const GemmArgs &g)
 #pragma unroll
                 for (int bb = 0; bb < TM; ++bb) {
                     floatx4 P = mfma(ah[bb], bf, floatx4{0.f, 0.f, 0.f, 0.f});
-                    if (LO)
+                    if (SEP)
                         P = mfma(al[bb], bf, P);
 #pragma unroll
                     for (int v = 0; v < 4; ++v)
@@ -439,7 +476,7 @@ REALM_DEV void gemm_body(const GemmArgs &g)
 
     // ---- reduce the KSPLIT partial sums through LDS
     if (KSPLIT > 1) {
-        __shared__ float red[4][TN * TM * 4][64];
+        __shared__ float red[WAVES][TN * TM * 4][64];
         if (wk != 0)
 #pragma unroll
             for (int a = 0; a < TN; ++a)
@@ -466,8 +503,9 @@ REALM_DEV void gemm_body(const GemmArgs &g)
 #pragma unroll
     for (int bb = 0; bb < TM; ++bb)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            int tok = t0 + 16 * bb + 4 * c + v;
+        for (int v = 0; v < 4; v += (PACK ? 2 : 1)) {
+            // packed: D rows 4c+v, 4c+v+1 are the (hi, lo) parts of one token
+            int tok = PACK ? t0 + TOK * bb + 2 * c + (v >> 1) : t0 + 16 * bb + 4 * c + v;
             if (tok >= g.M)
                 continue;
             float ts = g.tscale[tok];
@@ -485,7 +523,8 @@ REALM_DEV void gemm_body(const GemmArgs &g)
                 int row = n0 + 16 * a + r16;
                 if (row >= N)
                     continue;
-                float out = acc[a][bb][v] * ts;
+                float sum = PACK ? acc[a][bb][v] + acc[a][bb][v + 1] : acc[a][bb][v];
+                float out = sum * ts;
                 if (LORA && aid >= 0) {
                     const float *ut = g.u + (size_t)tok * g.rmax;
                     float s = 0.f;
@@ -503,10 +542,26 @@ REALM_DEV void gemm_body(const GemmArgs &g)
     {                                                                                     \
         gemm_body<FMT, TN, TM, KS, LO, WIDE, LORA>(g);                                    \
     }
+// Small batches: one 16-row tile per workgroup with K split over all of its
+// 16/TM waves (more loads in flight per CU; the register budget of TM token
+// tiles bounds the wave count); f32 activations pack (hi, lo) slots.
+#define GEMM_KERNEL_S(NAME, FMT, TM, LO, WIDE, LORA)                                      \
+    extern "C" __global__ __launch_bounds__(1024 / (TM)) void realm_gemm_##NAME(          \
+        GemmArgs g)                                                                       \
+    {                                                                                     \
+        gemm_body<FMT, 1, TM, 16 / (TM), LO, WIDE, LORA, 16 / (TM), LO>(g);                \
+    }
 
 // Instantiation set: (TN, TM, KSPLIT) tiles for decode (KSPLIT 4, TN 1) and
 // prefill (KSPLIT 1, TN 2); LO = f32 activations; Q6_K narrow/wide scales.
+#define GEMM_SMALL(FNAME, FMT, WIDE, LORA, SUF)                                           \
+    GEMM_KERNEL_S(FNAME##_s1_f32##SUF, FMT, 1, true, WIDE, LORA)                          \
+    GEMM_KERNEL_S(FNAME##_s2_f32##SUF, FMT, 2, true, WIDE, LORA)                          \
+    GEMM_KERNEL_S(FNAME##_s4_f32##SUF, FMT, 4, true, WIDE, LORA)                          \
+    GEMM_KERNEL_S(FNAME##_s1_bf16##SUF, FMT, 1, false, WIDE, LORA)                        \
+    GEMM_KERNEL_S(FNAME##_s2_bf16##SUF, FMT, 2, false, WIDE, LORA)
 #define GEMM_TILES(FNAME, FMT, WIDE, LORA, SUF)                                           \
+    GEMM_SMALL(FNAME, FMT, WIDE, LORA, SUF)                                               \
     GEMM_KERNEL(FNAME##_d1_f32##SUF, FMT, 1, 1, 4, true, WIDE, LORA)                      \
     GEMM_KERNEL(FNAME##_d2_f32##SUF, FMT, 1, 2, 4, true, WIDE, LORA)                      \
     GEMM_KERNEL(FNAME##_d4_f32##SUF, FMT, 1, 4, 4, true, WIDE, LORA)                      \
