@@ -525,24 +525,23 @@ int gemm_launch(const Weight &w, const XPrep &p, bool bf16, size_t M, const Gemm
     void *u = nullptr;
     if (lora) {
         const AdapterSet &set = *lora->set;
-        CHECK(ws_get(s, WS_U, p.Mp * (size_t)set.rmax * 4, &u));
+        CHECK(ws_get(s, WS_U, p.Mp * (size_t)round_up(set.rmax, 8) * 4, &u));
         const void *table = set.table;
         const int32_t *ids = lora->d_ids;
         void *xh = p.xh, *xl = p.xl, *ts = p.ts;
-        int iM = (int)M, iK = (int)w.k, iKX = (int)w.kx, rmax = set.rmax;
+        int iM = (int)M, iK = (int)w.k, iKX = (int)w.kx, rmax = (int)round_up(set.rmax, 8);
         void *args[] = {&xh, &xl, &ts, (void *)&ids, (void *)&table, &u, &iM, &iK, &iKX, &rmax};
         std::string name = std::string("realm_lora_shrink_") + fmt_name(w.type) +
                            (bf16 ? "_bf16" : "_f32");
         CHECK(launch(name,
                      dim3((unsigned)set.count, (unsigned)((set.rmax + 15) / 16),
                           (unsigned)((M + 15) / 16)),
-                     dim3(256), 0, s, args));
+                     dim3(1024), 0, s, args));
     }
     std::string fmt = fmt_name(w.type);
     if (w.type == GGML_Q6_K && w.wide)
         fmt = "q6kw";
-    std::string name = "realm_gemm_" + fmt + "_" + tile.name + (bf16 ? "_bf16" : "_f32") +
-                       (lora ? "_lora" : "");
+    std::string name = "realm_gemm_" + fmt + "_" + tile.name + (bf16 ? "_bf16" : "_f32");
     GemmArgs g;
     std::memset(&g, 0, sizeof g);
     g.w0 = w.w0;
@@ -558,17 +557,22 @@ int gemm_launch(const Weight &w, const XPrep &p, bool bf16, size_t M, const Gemm
     g.KX = (int)w.kx;
     g.M = (int)M;
     g.nan_fb = g_nan_fb.load();
-    if (lora) {
-        g.ids = lora->d_ids;
-        g.table = (const LoraEntry *)lora->set->table;
-        g.n_adapters = (int)lora->set->count;
-        g.u = (const float *)u;
-        g.rmax = lora->set->rmax;
-    }
     void *args[] = {&g};
     dim3 grid((unsigned)((w.n + tile.rows_per_wg - 1) / tile.rows_per_wg),
               (unsigned)((p.Mp + tile.toks_per_wg - 1) / tile.toks_per_wg));
-    return launch(name, grid, dim3(tile.threads), 0, s, args);
+    CHECK(launch(name, grid, dim3(tile.threads), 0, s, args));
+    if (lora) {
+        // y += scale_a B_a u per token, one workgroup per (adapter, 64 rows)
+        const AdapterSet &set = *lora->set;
+        const void *table = set.table;
+        const int32_t *ids = lora->d_ids;
+        int iM = (int)M, iN = (int)w.n, rmax = (int)round_up(set.rmax, 8);
+        void *eargs[] = {&u, (void *)&ids, (void *)&table, (void *)&d_y, &iM, &iN, &rmax};
+        CHECK(launch("realm_lora_expand",
+                     dim3((unsigned)set.count, (unsigned)((w.n + 63) / 64)), dim3(256), 0, s,
+                     eargs));
+    }
+    return REALM_OK;
 }
 
 int run_gemm(const Weight &w, const void *d_x, bool bf16, size_t M, float *d_y, hipStream_t s,

@@ -574,19 +574,53 @@ GEMM_TILES(q4k, FMT_Q4K, false, false, )
 GEMM_TILES(q6k, FMT_Q6K, false, false, )
 GEMM_TILES(q6kw, FMT_Q6K, true, false, )
 GEMM_TILES(q80, FMT_Q80, false, false, )
-GEMM_TILES(q4k, FMT_Q4K, false, true, _lora)
-GEMM_TILES(q6k, FMT_Q6K, false, true, _lora)
-GEMM_TILES(q6kw, FMT_Q6K, true, true, _lora)
-GEMM_TILES(q80, FMT_Q80, false, true, _lora)
 
 // ------------------------------------------------------------ LoRA shrink
 //
+// The tokens of adapter a, in token order, compacted into LDS by the whole
+// workgroup (a ballot per wave and a prefix over the waves); at most 1024
+// (the host rejects larger batches).
+REALM_DEV void adapter_tokens(const int *__restrict__ ids, int M, int a, int *toks, int *count,
+                              int *wsum)
+{
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int nwaves = blockDim.x >> 6;
+    int base_pos = 0;
+    for (int base = 0; base < M; base += blockDim.x) {
+        const int t = base + threadIdx.x;
+        const bool hit = t < M && ids[t] == a;
+        const unsigned long long m = __ballot(hit);
+        if (lane == 0)
+            wsum[wave] = __popcll(m);
+        __syncthreads();
+        int before = base_pos;
+        for (int w = 0; w < wave; ++w)
+            before += wsum[w];
+        int total = 0;
+        for (int w = 0; w < nwaves; ++w)
+            total += wsum[w];
+        if (hit) {
+            const int pos = before + __popcll(m & ((1ull << lane) - 1ull));
+            if (pos < 1024)
+                toks[pos] = t;
+        }
+        base_pos += total;
+        __syncthreads();
+    }
+    if (threadIdx.x == 0)
+        *count = base_pos < 1024 ? base_pos : 1024;
+    __syncthreads();
+}
+
 // u[t][j] = sum_k A_a[j][k] x[t][k] for the tokens t whose adapter is a,
 // j < rank_a.  Grid (adapter, 16-row chunk of A, 16-token chunk of the
-// adapter's tokens); the four waves split K and meet in LDS.  Activations are
-// the xprep fragments of the base matmul (same slot order), adapter rows are
-// read at the matching k and split into f16 hi/lo (exact for f16 adapters,
-// whose lo part is zero).
+// adapter's tokens); the 16 waves split K and meet in LDS (few workgroups:
+// the split keeps enough adapter loads in flight).  Activations are
+// the xprep fragments of the base matmul (same slot order); an adapter row's
+// 8 consecutive k of a slot window are one vector load, permuted to the
+// slot order and split into f16 hi/lo (exact for f16 adapters, whose lo part
+// is zero).
+#define SHRINK_WAVES 16
 template <int FMT, bool LO>
 REALM_DEV void lora_shrink(const _Float16 *__restrict__ xh, const _Float16 *__restrict__ xl,
                            const float *__restrict__ tscale, const int *__restrict__ ids,
@@ -595,16 +629,10 @@ REALM_DEV void lora_shrink(const _Float16 *__restrict__ xh, const _Float16 *__re
 {
     __shared__ int toks[1024];
     __shared__ int count;
-    __shared__ float red[4][4][64];
+    __shared__ int wsum[SHRINK_WAVES];
+    __shared__ float red[SHRINK_WAVES][4][64];
     const int a = blockIdx.x;
-    if (threadIdx.x == 0) {
-        int n = 0;
-        for (int t = 0; t < M; ++t)
-            if (ids[t] == a && n < 1024)
-                toks[n++] = t;
-        count = n;
-    }
-    __syncthreads();
+    adapter_tokens(ids, M, a, toks, &count, wsum);
     const LoraEntry e = table[a];
     const int jc = blockIdx.y * 16, tc = blockIdx.z * 16;
     if (tc >= count || jc >= e.rank)
@@ -616,23 +644,36 @@ REALM_DEV void lora_shrink(const _Float16 *__restrict__ xh, const _Float16 *__re
     const int j = jc + r16;
     floatx4 P = {0.f, 0.f, 0.f, 0.f};
     const int steps = KX / 32;
-    for (int s = wave; s < steps; s += 4) {
+    for (int s = wave; s < steps; s += SHRINK_WAVES) {
         half8_t ah = {}, al = {};
         if (tok >= 0) {
             ah = ld_h8(xh + (size_t)tok * KX + 32 * s + 8 * c);
             if (LO)
                 al = ld_h8(xl + (size_t)tok * KX + 32 * s + 8 * c);
         }
-        int k0 = kwin<FMT>(4 * s + c);
+        const int k0 = kwin<FMT>(4 * s + c);
         half8_t bh = {}, bl = {};
-        if (j < e.rank) {
+        if (j < e.rank && k0 < K) { // K is a multiple of 32: the window is whole
+            float v[8];
+            if (e.dtype) {
+                const uint4 raw = ldg16(reinterpret_cast<const _Float16 *>(e.a) + (size_t)j * K + k0);
+                const half8_t hv = __builtin_bit_cast(half8_t, raw);
+#pragma unroll
+                for (int q = 0; q < 8; ++q)
+                    v[q] = (float)hv[q];
+            } else {
+                const float4 *src = reinterpret_cast<const float4 *>(
+                    reinterpret_cast<const float *>(e.a) + (size_t)j * K + k0);
+                const float4 f0 = src[0], f1 = src[1];
+                v[0] = f0.x; v[1] = f0.y; v[2] = f0.z; v[3] = f0.w;
+                v[4] = f1.x; v[5] = f1.y; v[6] = f1.z; v[7] = f1.w;
+            }
 #pragma unroll
             for (int q = 0; q < 8; ++q) {
-                int k = k0 + pi8(q);
-                float v = k < K ? lora_elem(e.a, e.dtype, (size_t)j * K + k) : 0.f;
-                _Float16 h = (_Float16)v;
+                const float vv = v[pi8(q)];
+                const _Float16 h = (_Float16)vv;
                 bh[q] = h;
-                bl[q] = (_Float16)(v - (float)h);
+                bl[q] = (_Float16)(vv - (float)h);
             }
         }
         P = mfma(ah, bh, P);
@@ -648,24 +689,108 @@ REALM_DEV void lora_shrink(const _Float16 *__restrict__ xh, const _Float16 *__re
         return;
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-        float s = red[0][v][lane] + red[1][v][lane] + red[2][v][lane] + red[3][v][lane];
+        float sum = 0.f;
+#pragma unroll
+        for (int w = 0; w < SHRINK_WAVES; ++w)
+            sum += red[w][v][lane];
         // D[token slot 4c+v][adapter row r16]
         int tj = tc + 4 * c + v;
         if (tj < count && j < e.rank) {
             int t = toks[tj];
-            u[(size_t)t * rmax + j] = s * tscale[t];
+            u[(size_t)t * rmax + j] = sum * tscale[t];
         }
     }
 }
 
+// ------------------------------------------------------------ LoRA expand
+//
+// y[t][n] += scale_a * sum_j u[t][j] B_a[n][j] for the tokens t of adapter a
+// (y already holds the base product).  Grid (adapter, 64-row tile); each of
+// the four waves owns 16 rows and walks the adapter's tokens 16 at a time:
+// MFMA with A = u (token slots x rank, f32 split into f16 hi/lo), B = B_a^T
+// (rank x rows, f16 exact or f32 split).  Every (t, n) belongs to one
+// adapter, so the read-modify-write of y has no conflicts.
+REALM_DEV void lora_expand(const float *__restrict__ u, const int *__restrict__ ids,
+                           const LoraEntry *__restrict__ table, float *__restrict__ y, int M,
+                           int N, int rmax)
+{
+    __shared__ int toks[1024];
+    __shared__ int count;
+    __shared__ int wsum[4];
+    const int a = blockIdx.x;
+    adapter_tokens(ids, M, a, toks, &count, wsum);
+    const LoraEntry e = table[a];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int r16 = lane & 15, c = lane >> 4;
+    const int row = blockIdx.y * 64 + wave * 16 + r16;
+    const int ksteps = (e.rank + 31) / 32;
+    for (int tc = 0; tc < count; tc += 16) {
+        const int ti = tc + r16;
+        const int tok = ti < count ? toks[ti] : -1;
+        floatx4 P = {0.f, 0.f, 0.f, 0.f};
+        for (int kk = 0; kk < ksteps; ++kk) {
+            const int j0 = 32 * kk + 8 * c; // this lane's 8 ranks
+            half8_t ah = {}, al = {}, bh = {}, bl = {};
+            if (tok >= 0 && j0 < e.rank) {
+                // u rows are padded to a multiple of 8; entries past this
+                // adapter's rank hold another call's values and are masked
+                const float4 *up = reinterpret_cast<const float4 *>(u + (size_t)tok * rmax + j0);
+                const float4 u0 = up[0], u1 = up[1];
+                const float uv[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    const float vq = j0 + q < e.rank ? uv[q] : 0.f;
+                    const _Float16 h = (_Float16)vq;
+                    ah[q] = h;
+                    al[q] = (_Float16)(vq - (float)h);
+                }
+            }
+            if (row < N && j0 < e.rank) {
+                if (e.dtype && (e.rank & 7) == 0) { // one aligned 16-byte load
+                    bh = ld_h8(reinterpret_cast<const _Float16 *>(e.b) + (size_t)row * e.rank + j0);
+                } else {
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) {
+                        const float vv = j0 + q < e.rank
+                                             ? lora_elem(e.b, e.dtype, (size_t)row * e.rank + j0 + q)
+                                             : 0.f;
+                        const _Float16 h = (_Float16)vv;
+                        bh[q] = h;
+                        bl[q] = (_Float16)(vv - (float)h);
+                    }
+                }
+            }
+            P = mfma(ah, bh, P);
+            P = mfma(al, bh, P);
+            if (!e.dtype)
+                P = mfma(ah, bl, P);
+        }
+        // D[token slot 4c+v][row r16]
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int tj = tc + 4 * c + v;
+            if (tj < count && row < N) {
+                float *dst = y + (size_t)toks[tj] * N + row;
+                *dst += e.scale * P[v];
+            }
+        }
+    }
+}
+
+extern "C" __global__ __launch_bounds__(256) void realm_lora_expand(
+    const float *u, const int *ids, const LoraEntry *table, float *y, int M, int N, int rmax)
+{
+    lora_expand(u, ids, table, y, M, N, rmax);
+}
+
 #define DEF_SHRINK(NAME, FMT)                                                              \
-    extern "C" __global__ __launch_bounds__(256) void realm_lora_shrink_##NAME##_f32(     \
+    extern "C" __global__ __launch_bounds__(1024) void realm_lora_shrink_##NAME##_f32(     \
         const _Float16 *xh, const _Float16 *xl, const float *tscale, const int *ids,      \
         const LoraEntry *table, float *u, int M, int K, int KX, int rmax)                 \
     {                                                                                      \
         lora_shrink<FMT, true>(xh, xl, tscale, ids, table, u, M, K, KX, rmax);             \
     }                                                                                      \
-    extern "C" __global__ __launch_bounds__(256) void realm_lora_shrink_##NAME##_bf16(    \
+    extern "C" __global__ __launch_bounds__(1024) void realm_lora_shrink_##NAME##_bf16(    \
         const _Float16 *xh, const _Float16 *xl, const float *tscale, const int *ids,      \
         const LoraEntry *table, float *u, int M, int K, int KX, int rmax)                 \
     {                                                                                      \
