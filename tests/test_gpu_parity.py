@@ -229,6 +229,29 @@ def test_config2_prefill_bf16(backend, oracle, t):
     assert np.isfinite(got).all()
 
 
+@pytest.mark.parametrize("m", [1, 32])
+def test_config4_70b_shapes(backend, oracle, m):
+    """LLaMA-70B-shape matrices (hidden 8192, FFN 28672, 8 KV heads): Wk
+    (1024 x 8192 Q4_K), a 384-row slice of W_gate's 8192-wide rows (Q4_K) and
+    a 256-row slice of W_down's 28672-wide rows (Q6_K), at decode batch 1 and
+    32; row slices keep the CPU reference within seconds while K, the
+    dimension the kernels loop over, is full size."""
+    g = synth.rng(70)
+    for name, t, n, k in (("wk", GGML_Q4_K, 1024, 8192), ("w_gate", GGML_Q4_K, 384, 8192),
+                          ("w_down", GGML_Q6_K, 256, 28672)):
+        blocks = synth.blocks(g, t, n, k)
+        x = synth.activations(g, m, k)
+        h = backend.register_weights(t, blocks, n, k)
+        try:
+            got = backend.weights_matmul(h, x)
+        finally:
+            backend.release_weights(h)
+        rc, ref = oracle.candle_fused(t, blocks, x, m, n, k)
+        err = rel_l2(got, ref)
+        print(f"70b {name} m={m} rel_l2={err:.3e}")
+        assert rc == 0 and err < REL_TOL, name
+
+
 def test_q6k_wide_scales(backend, oracle):
     """Q6_K sub-scales over the full int8 range use the split-scale path."""
     g = synth.rng(66)
