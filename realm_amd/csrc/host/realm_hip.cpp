@@ -28,8 +28,9 @@
 #define REALM_STR2(x) #x
 #define REALM_STR(x) REALM_STR2(x)
 
-// The code objects (REALM_HSACO_COUNT of them: the non-GEMV kernels and the
-// GEMV variants of each weight format), embedded at link time.
+// The code objects (REALM_HSACO_COUNT of them: the non-GEMV kernels, the
+// GEMV variants of each weight format and the LDS-tiled GEMM), embedded at
+// link time.
 #define REALM_EMBED(I, FILE)                                                                   \
     __asm__(".pushsection .rodata.realm_hsaco" #I ",\"a\",@progbits\n"                        \
             ".balign 4096\n"                                                                  \
@@ -44,9 +45,10 @@ REALM_EMBED(0, REALM_HSACO_FILE0)
 REALM_EMBED(1, REALM_HSACO_FILE1)
 REALM_EMBED(2, REALM_HSACO_FILE2)
 REALM_EMBED(3, REALM_HSACO_FILE3)
-static_assert(REALM_HSACO_COUNT == 4, "the build embeds four code objects");
-static const unsigned char *const realm_hsacos[REALM_HSACO_COUNT] = {realm_hsaco0, realm_hsaco1,
-                                                                      realm_hsaco2, realm_hsaco3};
+REALM_EMBED(4, REALM_HSACO_FILE4)
+static_assert(REALM_HSACO_COUNT == 5, "the build embeds five code objects");
+static const unsigned char *const realm_hsacos[REALM_HSACO_COUNT] = {
+    realm_hsaco0, realm_hsaco1, realm_hsaco2, realm_hsaco3, realm_hsaco4};
 
 #define REALM_API extern "C" __attribute__((visibility("default")))
 
@@ -204,7 +206,7 @@ int pick_stream(void *user, hipStream_t *s)
 
 // Per-stream scratch buffers (grow-only).  Work on one stream is ordered, so
 // reusing a stream's buffers for its next call is safe.
-enum Slot { WS_RAW, WS_WEIGHT, WS_X, WS_Y, WS_XH, WS_XL, WS_XM, WS_TS, WS_U, WS_IDS, WS_N };
+enum Slot { WS_RAW, WS_WEIGHT, WS_X, WS_Y, WS_XH, WS_XL, WS_XM, WS_TS, WS_U, WS_IDS, WS_PART, WS_N };
 
 struct Workspace {
     void *buf[WS_N] = {};
@@ -462,22 +464,70 @@ int run_gemv(const Weight *const *ws, int count, const float *d_x, float *const 
 struct GemmTile {
     std::string name;
     unsigned rows_per_wg, toks_per_wg, threads;
+    bool tiled = false; // LDS-tiled kernel (gemm_tiled.hip): 1-D grid over tiles
+    int ord = 0;        // activation slot order the kernel reads
+    int ks = 1;         // tiled: K splits (parts summed by realm_gemm_reduce)
 };
 
-// small batches (16 rows x 8/16/32 tokens, K split over the workgroup's
-// 16/TM waves; f32 input packs a token's hi/lo parts into two MFMA slots),
-// decode tiles (16 rows x 64 tokens, K split over 4 waves) or the prefill
-// tile (128 rows x 64 tokens)
-GemmTile gemm_tile(size_t M, bool bf16)
+// LDS-tiled kernel "t<WR><WT><TN><TM><mode><NS>": WR x WT waves, each TN
+// 32-row tiles x TM 32-slot token tiles; mode p = packed f32 (16 tokens per
+// tile), s = f32 with separate lo MFMAs, b = bf16; NS pipeline stages.
+// Returns false for a malformed name or a mode that does not match the input.
+bool tiled_tile(const std::string &name, bool bf16, int ks, GemmTile *t)
 {
-    size_t M16 = round_up(M, 16);
-    if (!bf16 && M <= 32) {
-        if (M <= 8)
-            return {"s1", 16, 8, 1024};
-        return M <= 16 ? GemmTile{"s2", 16, 16, 512} : GemmTile{"s4", 16, 32, 256};
+    if (name.size() != 7 || name[0] != 't' || ks < 1 || ks > 64 || name[6] < '2' ||
+        name[6] > '4')
+        return false;
+    for (int i = 1; i < 5; ++i)
+        if (name[i] < '1' || name[i] > '8')
+            return false;
+    const unsigned wr = name[1] - '0', wt = name[2] - '0', tn = name[3] - '0', tm = name[4] - '0';
+    const char mode = name[5];
+    if ((mode == 'b') != bf16 || (mode != 'b' && mode != 'p' && mode != 's'))
+        return false;
+    *t = GemmTile{name, wr * tn * 32, wt * tm * (mode == 'p' ? 16u : 32u), wr * wt * 64, true, 1,
+                  ks};
+    return true;
+}
+
+// Kernel choice for a batched product with M tokens against w:
+//  * M <= 8 (f32) or M <= 32 (bf16): gemm.hip's small-batch tiles (16 rows x
+//    8..32 tokens, K split over the workgroup's waves);
+//  * otherwise, Q4_K / Q6_K (K a multiple of 256): the LDS-tiled kernel on
+//    32x32x16 MFMAs (gemm_tiled.hip) -- packed f32 (16 or 32 tokens per
+//    workgroup) or bf16 (64 tokens) -- with the K range split so that a
+//    launch has at least 256 workgroups;
+//  * Q8_0: gemm.hip's decode (16 rows x 16..64 tokens) or prefill (128 rows
+//    x 64 tokens) tiles.
+GemmTile gemm_tile(const Weight &w, size_t M, bool bf16)
+{
+    if (const char *env = getenv("REALM_GEMM_TILE")) { // tuning override
+        const char *ks = getenv("REALM_GEMM_KS");
+        GemmTile t;
+        if (tiled_tile(env, bf16, ks ? atoi(ks) : 1, &t))
+            return t;
     }
+    size_t M16 = round_up(M, 16);
+    if (!bf16 && M <= 8)
+        return {"s1", 16, 8, 1024};
     if (bf16 && M <= 32)
         return M <= 16 ? GemmTile{"s1", 16, 16, 1024} : GemmTile{"s2", 16, 32, 512};
+    if ((w.type == GGML_Q4_K || w.type == GGML_Q6_K) && w.kx % 256 == 0) {
+        GemmTile t;
+        const char *name = bf16 ? (w.type == GGML_Q4_K ? "t4112b2" : "t4112b3")
+                                : (M <= 16 ? "t4111p2" : "t4112p2");
+        tiled_tile(name, bf16, 1, &t);
+        const size_t tiles = ((w.n + t.rows_per_wg - 1) / t.rows_per_wg) *
+                             ((M + t.toks_per_wg - 1) / t.toks_per_wg);
+        const int nblk = (int)(w.kx / 256);
+        int ks = 1;
+        while ((size_t)ks * tiles < 256 && ks < 16 && 2 * ks <= nblk)
+            ks *= 2;
+        t.ks = ks;
+        return t;
+    }
+    if (!bf16 && M <= 32)
+        return M <= 16 ? GemmTile{"s2", 16, 16, 512} : GemmTile{"s4", 16, 32, 256};
     if (M16 >= 128)
         return {"p4", 128, 64, 256};
     if (M16 <= 16)
@@ -502,21 +552,23 @@ int prep_x(const Weight &w, const void *d_x, bool bf16, size_t M, const GemmTile
         return fail(REALM_INVALID_ARGUMENT,
                     "K " + std::to_string(w.k) + " exceeds the batched path's limit of " +
                         std::to_string(XPREP_MAX_KX));
-    // every token a workgroup reads must exist in the prepared activations
+    // every token a workgroup reads must exist in the prepared activations;
+    // the tiled kernels also read one all-zero token past them
     p->Mp = round_up(M, tile.toks_per_wg);
+    const size_t rows = p->Mp + (tile.tiled ? 1 : 0);
     size_t B = w.k / 256;
-    CHECK(ws_get(s, WS_XH, p->Mp * w.kx * 2, &p->xh));
+    CHECK(ws_get(s, WS_XH, rows * w.kx * 2, &p->xh));
     if (!bf16)
-        CHECK(ws_get(s, WS_XL, p->Mp * w.kx * 2, &p->xl));
+        CHECK(ws_get(s, WS_XL, rows * w.kx * 2, &p->xl));
     else
         p->xl = nullptr;
     if (w.type == GGML_Q4_K)
-        CHECK(ws_get(s, WS_XM, p->Mp * B * 64, &p->xm));
-    CHECK(ws_get(s, WS_TS, p->Mp * 4, &p->ts));
+        CHECK(ws_get(s, WS_XM, rows * B * 64, &p->xm));
+    CHECK(ws_get(s, WS_TS, rows * 4, &p->ts));
     int ibf = bf16 ? 1 : 0, iM = (int)M, iK = (int)w.k, iKX = (int)w.kx;
     void *args[] = {(void *)&d_x, &ibf, &p->xh, &p->xl, &p->xm, &p->ts, &iM, &iK, &iKX};
-    return launch(std::string("realm_xprep_") + fmt_name(w.type), dim3((unsigned)p->Mp),
-                  dim3(1024), 0, s, args);
+    return launch(std::string("realm_xprep_") + fmt_name(w.type) + (tile.ord ? "_o1" : ""),
+                  dim3((unsigned)rows), dim3(1024), 0, s, args);
 }
 
 int gemm_launch(const Weight &w, const XPrep &p, bool bf16, size_t M, const GemmTile &tile,
@@ -532,7 +584,7 @@ int gemm_launch(const Weight &w, const XPrep &p, bool bf16, size_t M, const Gemm
         int iM = (int)M, iK = (int)w.k, iKX = (int)w.kx, rmax = (int)round_up(set.rmax, 8);
         void *args[] = {&xh, &xl, &ts, (void *)&ids, (void *)&table, &u, &iM, &iK, &iKX, &rmax};
         std::string name = std::string("realm_lora_shrink_") + fmt_name(w.type) +
-                           (bf16 ? "_bf16" : "_f32");
+                           (bf16 ? "_bf16" : "_f32") + (tile.ord ? "_o1" : "");
         CHECK(launch(name,
                      dim3((unsigned)set.count, (unsigned)((set.rmax + 15) / 16),
                           (unsigned)((M + 15) / 16)),
@@ -541,7 +593,9 @@ int gemm_launch(const Weight &w, const XPrep &p, bool bf16, size_t M, const Gemm
     std::string fmt = fmt_name(w.type);
     if (w.type == GGML_Q6_K && w.wide)
         fmt = "q6kw";
-    std::string name = "realm_gemm_" + fmt + "_" + tile.name + (bf16 ? "_bf16" : "_f32");
+    std::string name = "realm_gemm_" + fmt + "_" + tile.name;
+    if (!tile.tiled)
+        name += bf16 ? "_bf16" : "_f32";
     GemmArgs g;
     std::memset(&g, 0, sizeof g);
     g.w0 = w.w0;
@@ -560,7 +614,37 @@ int gemm_launch(const Weight &w, const XPrep &p, bool bf16, size_t M, const Gemm
     void *args[] = {&g};
     dim3 grid((unsigned)((w.n + tile.rows_per_wg - 1) / tile.rows_per_wg),
               (unsigned)((p.Mp + tile.toks_per_wg - 1) / tile.toks_per_wg));
+    g.ksplit = 1;
+    if (tile.tiled) {
+        if (w.kx % 256)
+            return fail(REALM_INVALID_ARGUMENT, "tiled GEMM needs K padded to a multiple of 256");
+        const int nblk = (int)(w.kx / 256);
+        g.ksplit = tile.ks < nblk ? tile.ks : nblk;
+        if (g.ksplit > 1) {
+            void *part = nullptr;
+            CHECK(ws_get(s, WS_PART, (size_t)g.ksplit * M * w.n * 4, &part));
+            g.part = (float *)part;
+        }
+        // XCDs along the token tiles: enough that each XCD's share of the
+        // activations (f16, hi and lo for f32 input) stays within 2 MB of L2
+        const unsigned RT = grid.x, TT = grid.y;
+        const size_t xbytes = p.Mp * w.kx * (bf16 ? 2 : 4);
+        int xt = 1;
+        while (xt < 8 && (unsigned)xt < TT && xbytes / xt > ((size_t)2 << 20))
+            xt *= 2;
+        if (const char *env = getenv("REALM_GEMM_XT")) // tuning override
+            xt = atoi(env) == 1 || atoi(env) == 2 || atoi(env) == 4 || atoi(env) == 8 ? atoi(env) : xt;
+        g.xt = xt;
+        const unsigned xr = 8 / xt, rk = RT * (unsigned)g.ksplit;
+        grid = dim3(8 * ((rk + xr - 1) / xr) * ((TT + xt - 1) / xt));
+    }
     CHECK(launch(name, grid, dim3(tile.threads), 0, s, args));
+    if (g.ksplit > 1) {
+        int n = (int)(M * w.n), ks = g.ksplit;
+        void *rargs[] = {(void *)&g.part, (void *)&d_y, &n, &ks};
+        CHECK(launch("realm_gemm_reduce", dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
+                     rargs));
+    }
     if (lora) {
         // y += scale_a B_a u per token, one workgroup per (adapter, 64 rows)
         const AdapterSet &set = *lora->set;
@@ -580,7 +664,7 @@ int run_gemm(const Weight &w, const void *d_x, bool bf16, size_t M, float *d_y, 
 {
     if (M == 0 || w.n == 0)
         return REALM_OK;
-    const GemmTile tile = gemm_tile(M, bf16);
+    const GemmTile tile = gemm_tile(w, M, bf16);
     XPrep p;
     CHECK(prep_x(w, d_x, bf16, M, tile, s, &p));
     return gemm_launch(w, p, bf16, M, tile, d_y, s, lora);
@@ -981,7 +1065,7 @@ REALM_API int realm_hip_weights_matmul_group_dev(const uint64_t *handles, size_t
     // per matrix
     if (batch == 0)
         return REALM_OK;
-    const GemmTile tile = gemm_tile(batch, false);
+    const GemmTile tile = gemm_tile(w[0], batch, false);
     XPrep p;
     CHECK(prep_x(w[0], d_input, false, batch, tile, s, &p));
     for (size_t i = 0; i < count; ++i)

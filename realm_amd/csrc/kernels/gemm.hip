@@ -21,80 +21,30 @@
 // xprep writes activations in exactly that slot order.  D lane l holds rows
 // 4(l/16)+v (tokens) of column l%16 (a row n), so each lane scales its own
 // row's results with the block scale it decoded itself.
-#include "common.h"
+#include "mfma_common.h"
 #include "kernel_args.h"
 
 using namespace realm;
 
-typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
-typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
-typedef float floatx4 __attribute__((ext_vector_type(4)));
-
-#define FMT_Q4K 0
-#define FMT_Q6K 1
-#define FMT_Q80 2
-
-namespace {
-
-// Slot order inside an 8-slot group: nibble/byte pairs (0,2),(1,3),(4,6),(5,7)
-// come out of one mask each, so slot e holds element PI[e] of its window.
-REALM_DEV int pi8(int e) { return (e & 4) | ((e & 1) << 1) | ((e >> 1) & 1); }
-
-// Start (8-aligned) of the k window behind position group pg = p/8.
-template <int FMT>
-REALM_DEV int kwin(int pg)
-{
-    if (FMT == FMT_Q80)
-        return 8 * pg;
-    int b = pg >> 5, i = (pg >> 2) & 7, c = pg & 3;
-    if (FMT == FMT_Q4K)
-        return 256 * b + 64 * c + 32 * (i >> 2) + 8 * (i & 3);
-    return 256 * b + 128 * (c >> 1) + 16 * (c & 1) + 32 * (i >> 1) + 8 * (i & 1);
-}
-
-REALM_DEV half2_t h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
-REALM_DEV uint32_t u32(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
-REALM_DEV half8_t h8(uint32_t a, uint32_t b, uint32_t c, uint32_t d)
-{
-    uint4 v = make_uint4(a, b, c, d);
-    return __builtin_bit_cast(half8_t, v);
-}
-REALM_DEV half8_t ld_h8(const _Float16 *p) { return __builtin_bit_cast(half8_t, ldg16(p)); }
-REALM_DEV half2_t splat2(float v)
-{
-    _Float16 h = (_Float16)v;
-    half2_t r = {h, h};
-    return r;
-}
-
-REALM_DEV floatx4 mfma(half8_t a, half8_t b, floatx4 c)
-{
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-}
-
-REALM_DEV float load_x(const void *x, int bf16, size_t i)
-{
-    if (bf16)
-        return __uint_as_float((uint32_t)reinterpret_cast<const uint16_t *>(x)[i] << 16);
-    return reinterpret_cast<const float *>(x)[i];
-}
-
-} // namespace
-
 // ------------------------------------------------------------------ xprep
 //
-// One workgroup of 1024 threads per (padded) token.  Writes, for token t:
+// One workgroup of 1024 threads per (padded) token.  Writes, for token t, in
+// slot order ORD (mfma_common.h):
 //   xh[t][p], xl[t][p]  f16 hi/lo of x[t][k(p)] * 2^-e_t, p in [0, KX)
-//   xm[t][b][c][8]      Q4_K only: (Sxh(2c), Sxh(2c+1), Sxl(2c), Sxl(2c+1), 0...)
+//   xm                  Q4_K only, the 32-element sums Sx of x * 2^-e_t as
+//                       f16 hi/lo, laid out as the min-term MFMA reads them:
+//                       ORD 0: xm[t][b][c][8] = (Sxh(2c), Sxh(2c+1), Sxl(2c),
+//                              Sxl(2c+1), 0, 0, 0, 0)
+//                       ORD 1: xm[t][b][h][8] = (Sxh(4h..4h+3), Sxl(4h..4h+3))
 //   tscale[t] = 2^e_t
 // Tokens t >= M get zeros.  Position group pg = p/8 (8 slots) is handled by
-// thread pg % 1024: it loads the 8 consecutive x of its k window once, takes
-// part in the token's max, then converts them; the Q4_K 32-element sums come
-// from the four threads of a half group (lanes 4 apart in one DPP row).
+// thread pg % 1024: it loads the 8 x of its window once, takes part in the
+// token's max, then converts them; the Q4_K sums come from the threads that
+// share a sub-block (lanes of one 16-lane row).
 #define XPREP_TH 1024
 #define XPREP_R 4 // position-group rounds held in registers: KX <= 32768
 
-template <int FMT>
+template <int FMT, int ORD>
 REALM_DEV void xprep(const void *__restrict__ x, int bf16, _Float16 *__restrict__ xh,
                      _Float16 *__restrict__ xl, _Float16 *__restrict__ xm,
                      float *__restrict__ tscale, int M, int K, int KX)
@@ -104,17 +54,18 @@ REALM_DEV void xprep(const void *__restrict__ x, int bf16, _Float16 *__restrict_
     const bool live = t < M;
     const size_t xrow = (size_t)t * K;
     const int ngroups = KX >> 3;
+    constexpr int GAP = kgap<FMT, ORD>();
     float v[XPREP_R][8];
     float amax = 0.f;
 #pragma unroll
     for (int r = 0; r < XPREP_R; ++r) {
         const int pg = r * XPREP_TH + threadIdx.x;
-        const int k0 = pg < ngroups ? kwin<FMT>(pg) : 0;
+        const int k0 = pg < ngroups ? kwin<FMT, ORD>(pg) : 0;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const int k = k0 + e;
-            v[r][e] = (live && pg < ngroups && k < K) ? load_x(x, bf16, xrow + k) : 0.f;
-            amax = fmaxf(amax, fabsf(v[r][e]));
+        for (int w = 0; w < 8; ++w) {
+            const int k = k0 + (w & 3) + GAP * (w >> 2);
+            v[r][w] = (live && pg < ngroups && k < K) ? load_x(x, bf16, xrow + k) : 0.f;
+            amax = fmaxf(amax, fabsf(v[r][w]));
         }
     }
     // workgroup max: wave reduction (lane 63 ends with it), then LDS
@@ -143,21 +94,24 @@ REALM_DEV void xprep(const void *__restrict__ x, int bf16, _Float16 *__restrict_
     for (int r = 0; r < XPREP_R; ++r) {
         const int pg = r * XPREP_TH + threadIdx.x;
         _Float16 hv[8], lv[8];
-        float sum = 0.f; // of this thread's 8 x * down (its window)
+        float sum = 0.f, shi = 0.f; // of this thread's x * down: all 8 / the upper 4
 #pragma unroll
         for (int s2 = 0; s2 < 8; ++s2) {
             const float val = v[r][pi8(s2)] * down;
             const _Float16 h = (_Float16)val;
             hv[s2] = h;
             lv[s2] = (_Float16)(val - (float)h);
-            sum += val;
+            if (ORD == 1 && s2 >= 4)
+                shi += val;
+            else
+                sum += val;
         }
         if (pg < ngroups) {
             *reinterpret_cast<uint4 *>(xh + orow + 8 * pg) = __builtin_bit_cast(uint4, hv);
             if (xl)
                 *reinterpret_cast<uint4 *>(xl + orow + 8 * pg) = __builtin_bit_cast(uint4, lv);
         }
-        if (FMT == FMT_Q4K) {
+        if (FMT == FMT_Q4K && ORD == 0) {
             // pg = 32b + 4i + c: the half group (b, c, h = i/4) is the four
             // threads pg, pg+4, pg+8, pg+12 of one 16-lane DPP row
             sum += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sum), 0x124, 0xF, 0xF, false)); // row_ror:4
@@ -173,6 +127,25 @@ REALM_DEV void xprep(const void *__restrict__ x, int bf16, _Float16 *__restrict_
                     *reinterpret_cast<uint2 *>(dst + 4) = make_uint2(0u, 0u);
             }
         }
+        if (FMT == FMT_Q4K && ORD == 1) {
+            // pg = 32b + 2s + h: sub-blocks 4h + 2(s/8) (lower 4 of each
+            // window) and 4h + 2(s/8) + 1 (upper 4) gather the eight threads
+            // with equal b, h, s/8, i.e. lanes that differ in bits 1..3
+#pragma unroll
+            for (int off = 2; off <= 8; off <<= 1) {
+                sum += __shfl_xor(sum, off, 64);
+                shi += __shfl_xor(shi, off, 64);
+            }
+            const int b = pg >> 5, q = (pg >> 4) & 1, h = pg & 1;
+            if (pg < ngroups && b < B && (pg & 14) == 0) {
+                _Float16 *dst = xm + (((size_t)t * B + b) * 2 + h) * 8;
+                const _Float16 lh = (_Float16)sum, hh = (_Float16)shi;
+                dst[2 * q] = lh;
+                dst[2 * q + 4] = (_Float16)(sum - (float)lh);
+                dst[2 * q + 1] = hh;
+                dst[2 * q + 5] = (_Float16)(shi - (float)hh);
+            }
+        }
     }
 }
 
@@ -181,7 +154,13 @@ REALM_DEV void xprep(const void *__restrict__ x, int bf16, _Float16 *__restrict_
         const void *x, int bf16, _Float16 *xh, _Float16 *xl, _Float16 *xm, float *tscale, \
         int M, int K, int KX)                                                              \
     {                                                                                      \
-        xprep<FMT>(x, bf16, xh, xl, xm, tscale, M, K, KX);                                 \
+        xprep<FMT, 0>(x, bf16, xh, xl, xm, tscale, M, K, KX);                              \
+    }                                                                                      \
+    extern "C" __global__ __launch_bounds__(XPREP_TH) void realm_xprep_##NAME##_o1(       \
+        const void *x, int bf16, _Float16 *xh, _Float16 *xl, _Float16 *xm, float *tscale, \
+        int M, int K, int KX)                                                              \
+    {                                                                                      \
+        xprep<FMT, 1>(x, bf16, xh, xl, xm, tscale, M, K, KX);                              \
     }
 DEF_XPREP(q4k, FMT_Q4K)
 DEF_XPREP(q6k, FMT_Q6K)
@@ -203,7 +182,7 @@ REALM_DEV float lora_elem(const void *p, int dtype, size_t i)
 // (hi, lo) pairs, slot 2t + p = part p of token t, so one MFMA covers both
 // parts and the epilogue adds the pair; otherwise a slot is one token and
 // the lo part (LO) takes a second MFMA.
-template <int FMT, int TN, int TM, int KSPLIT, bool LO, bool WIDE, bool LORA, int WAVES = 4,
+template <int FMT, int TN, int TM, int KSPLIT, bool LO, bool WIDE, int WAVES = 4,
           bool PACK = false>
 REALM_DEV void gemm_body(const GemmArgs &g)
 {
@@ -499,7 +478,17 @@ REALM_DEV void gemm_body(const GemmArgs &g)
                         acc[a][bb][v] += red[wave + s][(a * TM + bb) * 4 + v][lane];
     }
 
-    // ---- epilogue: undo the token rescale, add the LoRA expand, store
+    // ---- epilogue: undo the token rescale and store.  The token scales are
+    // loaded before the first store: a load issued after stores would wait
+    // for them too (stores count in vmcnt).
+    float ts[TM][4];
+#pragma unroll
+    for (int bb = 0; bb < TM; ++bb)
+#pragma unroll
+        for (int v = 0; v < 4; v += (PACK ? 2 : 1)) {
+            const int tok = PACK ? t0 + TOK * bb + 2 * c + (v >> 1) : t0 + 16 * bb + 4 * c + v;
+            ts[bb][v] = g.tscale[tok]; // tokens are padded to the tile: every one has a scale
+        }
 #pragma unroll
     for (int bb = 0; bb < TM; ++bb)
 #pragma unroll
@@ -508,72 +497,54 @@ REALM_DEV void gemm_body(const GemmArgs &g)
             int tok = PACK ? t0 + TOK * bb + 2 * c + (v >> 1) : t0 + 16 * bb + 4 * c + v;
             if (tok >= g.M)
                 continue;
-            float ts = g.tscale[tok];
-            int aid = -1;
-            LoraEntry ent;
-            if (LORA) {
-                aid = g.ids[tok];
-                if (aid >= 0 && aid < g.n_adapters)
-                    ent = g.table[aid];
-                else
-                    aid = -1;
-            }
 #pragma unroll
             for (int a = 0; a < TN; ++a) {
                 int row = n0 + 16 * a + r16;
                 if (row >= N)
                     continue;
                 float sum = PACK ? acc[a][bb][v] + acc[a][bb][v + 1] : acc[a][bb][v];
-                float out = sum * ts;
-                if (LORA && aid >= 0) {
-                    const float *ut = g.u + (size_t)tok * g.rmax;
-                    float s = 0.f;
-                    for (int j = 0; j < ent.rank; ++j)
-                        s += lora_elem(ent.b, ent.dtype, (size_t)row * ent.rank + j) * ut[j];
-                    out += ent.scale * s;
-                }
-                g.y[(size_t)tok * N + row] = out;
+                g.y[(size_t)tok * N + row] = sum * ts[bb][v];
             }
         }
 }
 
-#define GEMM_KERNEL(NAME, FMT, TN, TM, KS, LO, WIDE, LORA)                                \
+#define GEMM_KERNEL(NAME, FMT, TN, TM, KS, LO, WIDE)                                      \
     extern "C" __global__ __launch_bounds__(256) void realm_gemm_##NAME(GemmArgs g)       \
     {                                                                                     \
-        gemm_body<FMT, TN, TM, KS, LO, WIDE, LORA>(g);                                    \
+        gemm_body<FMT, TN, TM, KS, LO, WIDE>(g);                                          \
     }
 // Small batches: one 16-row tile per workgroup with K split over all of its
 // 16/TM waves (more loads in flight per CU; the register budget of TM token
 // tiles bounds the wave count); f32 activations pack (hi, lo) slots.
-#define GEMM_KERNEL_S(NAME, FMT, TM, LO, WIDE, LORA)                                      \
+#define GEMM_KERNEL_S(NAME, FMT, TM, LO, WIDE)                                            \
     extern "C" __global__ __launch_bounds__(1024 / (TM)) void realm_gemm_##NAME(          \
         GemmArgs g)                                                                       \
     {                                                                                     \
-        gemm_body<FMT, 1, TM, 16 / (TM), LO, WIDE, LORA, 16 / (TM), LO>(g);                \
+        gemm_body<FMT, 1, TM, 16 / (TM), LO, WIDE, 16 / (TM), LO>(g);                      \
     }
 
 // Instantiation set: (TN, TM, KSPLIT) tiles for decode (KSPLIT 4, TN 1) and
 // prefill (KSPLIT 1, TN 2); LO = f32 activations; Q6_K narrow/wide scales.
-#define GEMM_SMALL(FNAME, FMT, WIDE, LORA, SUF)                                           \
-    GEMM_KERNEL_S(FNAME##_s1_f32##SUF, FMT, 1, true, WIDE, LORA)                          \
-    GEMM_KERNEL_S(FNAME##_s2_f32##SUF, FMT, 2, true, WIDE, LORA)                          \
-    GEMM_KERNEL_S(FNAME##_s4_f32##SUF, FMT, 4, true, WIDE, LORA)                          \
-    GEMM_KERNEL_S(FNAME##_s1_bf16##SUF, FMT, 1, false, WIDE, LORA)                        \
-    GEMM_KERNEL_S(FNAME##_s2_bf16##SUF, FMT, 2, false, WIDE, LORA)
-#define GEMM_TILES(FNAME, FMT, WIDE, LORA, SUF)                                           \
-    GEMM_SMALL(FNAME, FMT, WIDE, LORA, SUF)                                               \
-    GEMM_KERNEL(FNAME##_d1_f32##SUF, FMT, 1, 1, 4, true, WIDE, LORA)                      \
-    GEMM_KERNEL(FNAME##_d2_f32##SUF, FMT, 1, 2, 4, true, WIDE, LORA)                      \
-    GEMM_KERNEL(FNAME##_d4_f32##SUF, FMT, 1, 4, 4, true, WIDE, LORA)                      \
-    GEMM_KERNEL(FNAME##_p4_f32##SUF, FMT, 2, 4, 1, true, WIDE, LORA)                      \
-    GEMM_KERNEL(FNAME##_d1_bf16##SUF, FMT, 1, 1, 4, false, WIDE, LORA)                    \
-    GEMM_KERNEL(FNAME##_d4_bf16##SUF, FMT, 1, 4, 4, false, WIDE, LORA)                    \
-    GEMM_KERNEL(FNAME##_p4_bf16##SUF, FMT, 2, 4, 1, false, WIDE, LORA)
+#define GEMM_SMALL(FNAME, FMT, WIDE)                                                      \
+    GEMM_KERNEL_S(FNAME##_s1_f32, FMT, 1, true, WIDE)                                     \
+    GEMM_KERNEL_S(FNAME##_s2_f32, FMT, 2, true, WIDE)                                     \
+    GEMM_KERNEL_S(FNAME##_s4_f32, FMT, 4, true, WIDE)                                     \
+    GEMM_KERNEL_S(FNAME##_s1_bf16, FMT, 1, false, WIDE)                                   \
+    GEMM_KERNEL_S(FNAME##_s2_bf16, FMT, 2, false, WIDE)
+#define GEMM_TILES(FNAME, FMT, WIDE)                                                      \
+    GEMM_SMALL(FNAME, FMT, WIDE)                                                          \
+    GEMM_KERNEL(FNAME##_d1_f32, FMT, 1, 1, 4, true, WIDE)                                 \
+    GEMM_KERNEL(FNAME##_d2_f32, FMT, 1, 2, 4, true, WIDE)                                 \
+    GEMM_KERNEL(FNAME##_d4_f32, FMT, 1, 4, 4, true, WIDE)                                 \
+    GEMM_KERNEL(FNAME##_p4_f32, FMT, 2, 4, 1, true, WIDE)                                 \
+    GEMM_KERNEL(FNAME##_d1_bf16, FMT, 1, 1, 4, false, WIDE)                               \
+    GEMM_KERNEL(FNAME##_d4_bf16, FMT, 1, 4, 4, false, WIDE)                               \
+    GEMM_KERNEL(FNAME##_p4_bf16, FMT, 2, 4, 1, false, WIDE)
 
-GEMM_TILES(q4k, FMT_Q4K, false, false, )
-GEMM_TILES(q6k, FMT_Q6K, false, false, )
-GEMM_TILES(q6kw, FMT_Q6K, true, false, )
-GEMM_TILES(q80, FMT_Q80, false, false, )
+GEMM_TILES(q4k, FMT_Q4K, false)
+GEMM_TILES(q6k, FMT_Q6K, false)
+GEMM_TILES(q6kw, FMT_Q6K, true)
+GEMM_TILES(q80, FMT_Q80, false)
 
 // ------------------------------------------------------------ LoRA shrink
 //
@@ -616,12 +587,12 @@ REALM_DEV void adapter_tokens(const int *__restrict__ ids, int M, int a, int *to
 // j < rank_a.  Grid (adapter, 16-row chunk of A, 16-token chunk of the
 // adapter's tokens); the 16 waves split K and meet in LDS (few workgroups:
 // the split keeps enough adapter loads in flight).  Activations are
-// the xprep fragments of the base matmul (same slot order); an adapter row's
-// 8 consecutive k of a slot window are one vector load, permuted to the
-// slot order and split into f16 hi/lo (exact for f16 adapters, whose lo part
-// is zero).
+// the xprep fragments of the base matmul (slot order ORD, that of the base
+// kernel); an adapter row's k window of a slot group is one or two vector
+// loads, permuted to the slot order and split into f16 hi/lo (exact for f16
+// adapters, whose lo part is zero).
 #define SHRINK_WAVES 16
-template <int FMT, bool LO>
+template <int FMT, bool LO, int ORD>
 REALM_DEV void lora_shrink(const _Float16 *__restrict__ xh, const _Float16 *__restrict__ xl,
                            const float *__restrict__ tscale, const int *__restrict__ ids,
                            const LoraEntry *__restrict__ table, float *__restrict__ u, int M,
@@ -651,20 +622,22 @@ REALM_DEV void lora_shrink(const _Float16 *__restrict__ xh, const _Float16 *__re
             if (LO)
                 al = ld_h8(xl + (size_t)tok * KX + 32 * s + 8 * c);
         }
-        const int k0 = kwin<FMT>(4 * s + c);
+        const int k0 = kwin<FMT, ORD>(4 * s + c);
+        constexpr int GAP = kgap<FMT, ORD>(); // second 4 of the window at k0 + GAP
         half8_t bh = {}, bl = {};
-        if (j < e.rank && k0 < K) { // K is a multiple of 32: the window is whole
+        if (j < e.rank && k0 < K) { // whole blocks (K % 32 == 0): the window is whole
             float v[8];
             if (e.dtype) {
-                const uint4 raw = ldg16(reinterpret_cast<const _Float16 *>(e.a) + (size_t)j * K + k0);
-                const half8_t hv = __builtin_bit_cast(half8_t, raw);
+                const _Float16 *src = reinterpret_cast<const _Float16 *>(e.a) + (size_t)j * K + k0;
+                const uint2 r0 = ldg8(src), r1 = ldg8(src + GAP);
+                const half8_t hv = __builtin_bit_cast(half8_t, make_uint4(r0.x, r0.y, r1.x, r1.y));
 #pragma unroll
                 for (int q = 0; q < 8; ++q)
                     v[q] = (float)hv[q];
             } else {
-                const float4 *src = reinterpret_cast<const float4 *>(
-                    reinterpret_cast<const float *>(e.a) + (size_t)j * K + k0);
-                const float4 f0 = src[0], f1 = src[1];
+                const float *src = reinterpret_cast<const float *>(e.a) + (size_t)j * K + k0;
+                const float4 f0 = *reinterpret_cast<const float4 *>(src);
+                const float4 f1 = *reinterpret_cast<const float4 *>(src + GAP);
                 v[0] = f0.x; v[1] = f0.y; v[2] = f0.z; v[3] = f0.w;
                 v[4] = f1.x; v[5] = f1.y; v[6] = f1.z; v[7] = f1.w;
             }
@@ -783,19 +756,20 @@ extern "C" __global__ __launch_bounds__(256) void realm_lora_expand(
     lora_expand(u, ids, table, y, M, N, rmax);
 }
 
-#define DEF_SHRINK(NAME, FMT)                                                              \
-    extern "C" __global__ __launch_bounds__(1024) void realm_lora_shrink_##NAME##_f32(     \
+#define DEF_SHRINK1(NAME, FMT, ORD, SUF)                                                   \
+    extern "C" __global__ __launch_bounds__(1024) void realm_lora_shrink_##NAME##_f32##SUF(\
         const _Float16 *xh, const _Float16 *xl, const float *tscale, const int *ids,      \
         const LoraEntry *table, float *u, int M, int K, int KX, int rmax)                 \
     {                                                                                      \
-        lora_shrink<FMT, true>(xh, xl, tscale, ids, table, u, M, K, KX, rmax);             \
+        lora_shrink<FMT, true, ORD>(xh, xl, tscale, ids, table, u, M, K, KX, rmax);        \
     }                                                                                      \
-    extern "C" __global__ __launch_bounds__(1024) void realm_lora_shrink_##NAME##_bf16(    \
+    extern "C" __global__ __launch_bounds__(1024) void realm_lora_shrink_##NAME##_bf16##SUF(\
         const _Float16 *xh, const _Float16 *xl, const float *tscale, const int *ids,      \
         const LoraEntry *table, float *u, int M, int K, int KX, int rmax)                 \
     {                                                                                      \
-        lora_shrink<FMT, false>(xh, xl, tscale, ids, table, u, M, K, KX, rmax);            \
+        lora_shrink<FMT, false, ORD>(xh, xl, tscale, ids, table, u, M, K, KX, rmax);       \
     }
+#define DEF_SHRINK(NAME, FMT) DEF_SHRINK1(NAME, FMT, 0, ) DEF_SHRINK1(NAME, FMT, 1, _o1)
 DEF_SHRINK(q4k, FMT_Q4K)
 DEF_SHRINK(q6k, FMT_Q6K)
 DEF_SHRINK(q80, FMT_Q80)

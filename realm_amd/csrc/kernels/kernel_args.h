@@ -36,7 +36,10 @@ struct GemmArgs {
     const LoraEntry *table;       // LoRA: device table
     const float *u;               // LoRA: shrink output [Mp][rmax]
     int32_t rmax;
-    int32_t pad;
+    int32_t ksplit;               // tiled kernels: K splits (1 = none)
+    float *part;                  // tiled kernels, ksplit > 1: parts [ksplit][M][N]
+    int32_t xt;                   // tiled kernels: XCDs along the token tiles (1, 2, 4, 8)
+    int32_t pad2;
 };
 
 // Arguments of the realm_gemv_* kernels: up to 4 matrices of one format

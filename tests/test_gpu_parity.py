@@ -8,6 +8,8 @@ workload definition).  Full-size configurations are compared on the full
 output where the oracle finishes in seconds, otherwise on a seeded subset of
 rows.
 """
+import zlib
+
 import numpy as np
 import pytest
 
@@ -250,6 +252,57 @@ def test_config4_70b_shapes(backend, oracle, m):
         err = rel_l2(got, ref)
         print(f"70b {name} m={m} rel_l2={err:.3e}")
         assert rc == 0 and err < REL_TOL, name
+
+
+def _dev_matmul(backend, t, blocks, n, k, x, bf16):
+    """Resident weights, device activations (f32 or bf16 bits), one launch."""
+    h = backend.register_weights(t, blocks, n, k)
+    m = x.shape[0]
+    dx = backend.alloc(x.nbytes).upload(x)
+    dy = backend.alloc(m * n * 4)
+    try:
+        backend.matmul_dev(h, dx.ptr, m, dy.ptr, bf16=bf16)
+        backend.synchronize()
+        return dy.download(np.float32, m * n).reshape(m, n)
+    finally:
+        backend.release_weights(h)
+        dx.close()
+        dy.close()
+
+
+TILED = [("t4111p2", 1), ("t4111p2", 3), ("t4112p2", 1), ("t4112p2", 4), ("t4112p3", 2),
+         ("t8112p4", 1), ("t4112s2", 2), ("t4112b2", 1), ("t4112b2", 2), ("t4112b3", 1),
+         ("t4112b4", 3), ("t8112b3", 1), ("t8112b4", 2), ("t4114b2", 1), ("t8111b4", 1)]
+
+
+@pytest.mark.parametrize("tile,ks", TILED)
+@pytest.mark.parametrize("t", [GGML_Q4_K, GGML_Q6_K])
+def test_tiled_variants(backend, oracle, monkeypatch, tile, ks, t):
+    """Every LDS-tiled kernel variant (forced through the tuning override):
+    ragged rows (N = 300) and tokens, six 256-blocks split unevenly over K
+    splits, the packed / separate-lo / bf16 activation modes; Q6_K once
+    with sub-scales over the full int8 range (the split-scale decode)."""
+    monkeypatch.setenv("REALM_GEMM_TILE", tile)
+    monkeypatch.setenv("REALM_GEMM_KS", str(ks))
+    bf16 = tile.endswith(("b2", "b3", "b4"))
+    g = synth.rng(zlib.crc32(f"{tile}{ks}{t}".encode()) % 100000)
+    n, k = 300, 1536
+    blocks = synth.blocks(g, t, n, k)
+    if t == GGML_Q6_K and ks > 1:
+        blocks["scales"] = g.integers(-128, 128, blocks["scales"].shape, dtype=np.int8)
+    for m in (37, 70):
+        if bf16:
+            xb = synth.activations_bf16(g, m, k)
+            got = _dev_matmul(backend, t, blocks, n, k, xb, True)
+            x = synth.bf16_bits_to_f32(xb)
+        else:
+            x = synth.activations(g, m, k)
+            got = _dev_matmul(backend, t, blocks, n, k, x, False)
+        assert tile in backend.last_kernel() or "reduce" in backend.last_kernel()
+        rc, ref = oracle.candle_fused(t, blocks, x, m, n, k)
+        err = rel_l2(got, ref.reshape(m, n))
+        print(f"{tile} ks={ks} {NAMES[t]} m={m} rel_l2={err:.3e}")
+        assert rc == 0 and err < REL_TOL
 
 
 def test_q6k_wide_scales(backend, oracle):
