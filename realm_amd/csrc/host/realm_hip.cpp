@@ -575,20 +575,25 @@ int gemm_launch(const Weight &w, const XPrep &p, bool bf16, size_t M, const Gemm
                 float *d_y, hipStream_t s, const LoraCall *lora)
 {
     void *u = nullptr;
+    // shrink output: one part per 512 positions of K (summed by the expand)
+    const int nparts = (int)((w.kx + 511) / 512);
+    int pstride = 0;
     if (lora) {
         const AdapterSet &set = *lora->set;
-        CHECK(ws_get(s, WS_U, p.Mp * (size_t)round_up(set.rmax, 8) * 4, &u));
+        const int rmax = (int)round_up(set.rmax, 8);
+        pstride = (int)(p.Mp * rmax);
+        CHECK(ws_get(s, WS_U, (size_t)nparts * pstride * 4, &u));
         const void *table = set.table;
         const int32_t *ids = lora->d_ids;
         void *xh = p.xh, *xl = p.xl, *ts = p.ts;
-        int iM = (int)M, iK = (int)w.k, iKX = (int)w.kx, rmax = (int)round_up(set.rmax, 8);
-        void *args[] = {&xh, &xl, &ts, (void *)&ids, (void *)&table, &u, &iM, &iK, &iKX, &rmax};
+        int iM = (int)M, iK = (int)w.k, iKX = (int)w.kx, irmax = rmax;
+        void *args[] = {&xh,  &xl,  &ts,   (void *)&ids, (void *)&table, &u,
+                        &iM,  &iK,  &iKX,  &irmax,       &pstride};
         std::string name = std::string("realm_lora_shrink_") + fmt_name(w.type) +
                            (bf16 ? "_bf16" : "_f32") + (tile.ord ? "_o1" : "");
         CHECK(launch(name,
-                     dim3((unsigned)set.count, (unsigned)((set.rmax + 15) / 16),
-                          (unsigned)((M + 15) / 16)),
-                     dim3(1024), 0, s, args));
+                     dim3((unsigned)set.count, (unsigned)((set.rmax + 15) / 16), (unsigned)nparts),
+                     dim3(256), 0, s, args));
     }
     std::string fmt = fmt_name(w.type);
     if (w.type == GGML_Q6_K && w.wide)
@@ -650,11 +655,13 @@ int gemm_launch(const Weight &w, const XPrep &p, bool bf16, size_t M, const Gemm
         const AdapterSet &set = *lora->set;
         const void *table = set.table;
         const int32_t *ids = lora->d_ids;
-        int iM = (int)M, iN = (int)w.n, rmax = (int)round_up(set.rmax, 8);
-        void *eargs[] = {&u, (void *)&ids, (void *)&table, (void *)&d_y, &iM, &iN, &rmax};
+        int iM = (int)M, iN = (int)w.n, rmax = (int)round_up(set.rmax, 8), np = nparts;
+        void *eargs[] = {&u, (void *)&ids, (void *)&table, (void *)&d_y, &iM, &iN, &rmax, &np,
+                         &pstride};
         CHECK(launch("realm_lora_expand",
-                     dim3((unsigned)set.count, (unsigned)((w.n + 63) / 64)), dim3(256), 0, s,
-                     eargs));
+                     dim3((unsigned)set.count, (unsigned)((w.n + 511) / 512),
+                          (unsigned)((M + 15) / 16)),
+                     dim3(256), 0, s, eargs));
     }
     return REALM_OK;
 }

@@ -583,109 +583,107 @@ REALM_DEV void adapter_tokens(const int *__restrict__ ids, int M, int a, int *to
     __syncthreads();
 }
 
-// u[t][j] = sum_k A_a[j][k] x[t][k] for the tokens t whose adapter is a,
-// j < rank_a.  Grid (adapter, 16-row chunk of A, 16-token chunk of the
-// adapter's tokens); the 16 waves split K and meet in LDS (few workgroups:
-// the split keeps enough adapter loads in flight).  Activations are
-// the xprep fragments of the base matmul (slot order ORD, that of the base
-// kernel); an adapter row's k window of a slot group is one or two vector
-// loads, permuted to the slot order and split into f16 hi/lo (exact for f16
-// adapters, whose lo part is zero).
-#define SHRINK_WAVES 16
-template <int FMT, bool LO, int ORD>
-REALM_DEV void lora_shrink(const _Float16 *__restrict__ xh, const _Float16 *__restrict__ xl,
-                           const float *__restrict__ tscale, const int *__restrict__ ids,
-                           const LoraEntry *__restrict__ table, float *__restrict__ u, int M,
-                           int K, int KX, int rmax)
+// Shrink, u = A_a x, in parts over K: for the tokens t whose adapter is a and
+// j < rank_a,
+//   part[kc][t][j] = sum over positions [512 kc, 512 kc + 512) of
+//                    A_a[j][k(p)] x[t][k(p)]
+// (the expand adds the parts in kc order).  Grid (adapter, 16-row chunk of
+// A, 512-position chunk kc), so that a launch spreads over many CUs; the 4
+// waves take the adapter's tokens 16 at a time and the chunk's A fragments
+// stay in registers across them.  Activations are the xprep fragments of the
+// base matmul (slot order ORD, that of the base kernel); an adapter row's k
+// window of a slot group is one or two vector loads, permuted to the slot
+// order and split into f16 hi/lo (exact for f16 adapters, whose lo part is
+// zero and skipped).
+#define SHRINK_KC 512
+#define SHRINK_NS (SHRINK_KC / 32)
+template <int FMT, bool LO, int ORD, bool F16A>
+REALM_DEV void shrink_body(const _Float16 *__restrict__ xh, const _Float16 *__restrict__ xl,
+                           const float *__restrict__ tscale, const LoraEntry &e, const int *toks,
+                           int count, float *__restrict__ part, int K, int KX, int rmax,
+                           int pstride)
 {
-    __shared__ int toks[1024];
-    __shared__ int count;
-    __shared__ int wsum[SHRINK_WAVES];
-    __shared__ float red[SHRINK_WAVES][4][64];
-    const int a = blockIdx.x;
-    adapter_tokens(ids, M, a, toks, &count, wsum);
-    const LoraEntry e = table[a];
-    const int jc = blockIdx.y * 16, tc = blockIdx.z * 16;
-    if (tc >= count || jc >= e.rank)
-        return;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int r16 = lane & 15, c = lane >> 4;
-    const int ti = tc + r16;
-    const int tok = ti < count ? toks[ti] : -1;
+    const int jc = blockIdx.y * 16, kc = blockIdx.z;
     const int j = jc + r16;
-    floatx4 P = {0.f, 0.f, 0.f, 0.f};
-    const int steps = KX / 32;
-    for (int s = wave; s < steps; s += SHRINK_WAVES) {
-        half8_t ah = {}, al = {};
-        if (tok >= 0) {
-            ah = ld_h8(xh + (size_t)tok * KX + 32 * s + 8 * c);
-            if (LO)
-                al = ld_h8(xl + (size_t)tok * KX + 32 * s + 8 * c);
-        }
-        const int k0 = kwin<FMT, ORD>(4 * s + c);
-        constexpr int GAP = kgap<FMT, ORD>(); // second 4 of the window at k0 + GAP
-        half8_t bh = {}, bl = {};
-        if (j < e.rank && k0 < K) { // whole blocks (K % 32 == 0): the window is whole
-            float v[8];
-            if (e.dtype) {
-                const _Float16 *src = reinterpret_cast<const _Float16 *>(e.a) + (size_t)j * K + k0;
-                const uint2 r0 = ldg8(src), r1 = ldg8(src + GAP);
-                const half8_t hv = __builtin_bit_cast(half8_t, make_uint4(r0.x, r0.y, r1.x, r1.y));
+    // every load below reads valid memory: rows past the rank read the last
+    // row and token slots past the adapter's tokens read its first token;
+    // they only feed D rows / columns that are never stored.  Steps past the
+    // chunk (s >= ns) are zeroed.
+    const int jr = min(j, e.rank - 1);
+    const int s0 = kc * SHRINK_NS;
+    const int ns = min(SHRINK_NS, KX / 32 - s0); // 32-position steps in this chunk
+    constexpr int GAP = kgap<FMT, ORD>();        // second 4 of a window at k0 + GAP
+    half8_t bh[SHRINK_NS], bl[SHRINK_NS];
 #pragma unroll
-                for (int q = 0; q < 8; ++q)
-                    v[q] = (float)hv[q];
-            } else {
-                const float *src = reinterpret_cast<const float *>(e.a) + (size_t)j * K + k0;
-                const float4 f0 = *reinterpret_cast<const float4 *>(src);
-                const float4 f1 = *reinterpret_cast<const float4 *>(src + GAP);
-                v[0] = f0.x; v[1] = f0.y; v[2] = f0.z; v[3] = f0.w;
-                v[4] = f1.x; v[5] = f1.y; v[6] = f1.z; v[7] = f1.w;
-            }
+    for (int s = 0; s < SHRINK_NS; ++s) {
+        const int k0 = kwin<FMT, ORD>(4 * (s0 + min(s, ns - 1)) + c);
+        float v[8];
+        if (F16A) {
+            const _Float16 *src = reinterpret_cast<const _Float16 *>(e.a) + (size_t)jr * K + k0;
+            const uint2 r0 = ldg8(src), r1 = ldg8(src + GAP);
+            const half8_t hv = __builtin_bit_cast(half8_t, make_uint4(r0.x, r0.y, r1.x, r1.y));
 #pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                const float vv = v[pi8(q)];
-                const _Float16 h = (_Float16)vv;
-                bh[q] = h;
-                bl[q] = (_Float16)(vv - (float)h);
-            }
+            for (int q = 0; q < 8; ++q)
+                v[q] = (float)hv[q];
+        } else {
+            const float *src = reinterpret_cast<const float *>(e.a) + (size_t)jr * K + k0;
+            const float4 f0 = *reinterpret_cast<const float4 *>(src);
+            const float4 f1 = *reinterpret_cast<const float4 *>(src + GAP);
+            v[0] = f0.x; v[1] = f0.y; v[2] = f0.z; v[3] = f0.w;
+            v[4] = f1.x; v[5] = f1.y; v[6] = f1.z; v[7] = f1.w;
         }
-        P = mfma(ah, bh, P);
-        P = mfma(ah, bl, P);
-        if (LO)
-            P = mfma(al, bh, P);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const float vv = s < ns ? v[pi8(q)] : 0.f;
+            const _Float16 hq = (_Float16)vv;
+            bh[s][q] = hq;
+            bl[s][q] = (_Float16)(vv - (float)hq);
+        }
     }
+    float *pk = part + (size_t)kc * pstride;
+    for (int tc = 16 * wave; tc < count; tc += 64) {
+        const int ti = tc + r16;
+        const int tok = toks[ti < count ? ti : 0];
+        floatx4 P = {0.f, 0.f, 0.f, 0.f};
+        half8_t ah[SHRINK_NS], al[SHRINK_NS];
 #pragma unroll
-    for (int v = 0; v < 4; ++v)
-        red[wave][v][lane] = P[v];
-    __syncthreads();
-    if (wave != 0)
-        return;
+        for (int s = 0; s < SHRINK_NS; ++s) {
+            const int sc = s0 + min(s, ns - 1);
+            ah[s] = ld_h8(xh + (size_t)tok * KX + 32 * sc + 8 * c);
+            if (LO)
+                al[s] = ld_h8(xl + (size_t)tok * KX + 32 * sc + 8 * c);
+        }
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-        float sum = 0.f;
+        for (int s = 0; s < SHRINK_NS; ++s) {
+            P = mfma(ah[s], bh[s], P);
+            if (!F16A)
+                P = mfma(ah[s], bl[s], P);
+            if (LO)
+                P = mfma(al[s], bh[s], P);
+        }
+        float ts[4];
 #pragma unroll
-        for (int w = 0; w < SHRINK_WAVES; ++w)
-            sum += red[w][v][lane];
-        // D[token slot 4c+v][adapter row r16]
-        int tj = tc + 4 * c + v;
-        if (tj < count && j < e.rank) {
-            int t = toks[tj];
-            u[(size_t)t * rmax + j] = sum * tscale[t];
+        for (int v = 0; v < 4; ++v) {
+            const int tj = tc + 4 * c + v;
+            ts[v] = tscale[toks[tj < count ? tj : 0]];
+        }
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            // D[token slot 4c+v][adapter row r16]
+            const int tj = tc + 4 * c + v;
+            if (tj < count && j < e.rank)
+                pk[(size_t)toks[tj] * rmax + j] = P[v] * ts[v];
         }
     }
 }
 
-// ------------------------------------------------------------ LoRA expand
-//
-// y[t][n] += scale_a * sum_j u[t][j] B_a[n][j] for the tokens t of adapter a
-// (y already holds the base product).  Grid (adapter, 64-row tile); each of
-// the four waves owns 16 rows and walks the adapter's tokens 16 at a time:
-// MFMA with A = u (token slots x rank, f32 split into f16 hi/lo), B = B_a^T
-// (rank x rows, f16 exact or f32 split).  Every (t, n) belongs to one
-// adapter, so the read-modify-write of y has no conflicts.
-REALM_DEV void lora_expand(const float *__restrict__ u, const int *__restrict__ ids,
-                           const LoraEntry *__restrict__ table, float *__restrict__ y, int M,
-                           int N, int rmax)
+template <int FMT, bool LO, int ORD>
+REALM_DEV void lora_shrink(const _Float16 *__restrict__ xh, const _Float16 *__restrict__ xl,
+                           const float *__restrict__ tscale, const int *__restrict__ ids,
+                           const LoraEntry *__restrict__ table, float *__restrict__ part, int M,
+                           int K, int KX, int rmax, int pstride)
 {
     __shared__ int toks[1024];
     __shared__ int count;
@@ -693,81 +691,165 @@ REALM_DEV void lora_expand(const float *__restrict__ u, const int *__restrict__ 
     const int a = blockIdx.x;
     adapter_tokens(ids, M, a, toks, &count, wsum);
     const LoraEntry e = table[a];
+    if ((int)blockIdx.y * 16 >= e.rank || count == 0)
+        return;
+    if (e.dtype)
+        shrink_body<FMT, LO, ORD, true>(xh, xl, tscale, e, toks, count, part, K, KX, rmax, pstride);
+    else
+        shrink_body<FMT, LO, ORD, false>(xh, xl, tscale, e, toks, count, part, K, KX, rmax, pstride);
+}
+
+// ------------------------------------------------------------ LoRA expand
+//
+// y[t][n] += scale_a * sum_j u[t][j] B_a[n][j] for the tokens t of adapter a
+// (y already holds the base product).  Grid (adapter, group of 8 64-row
+// tiles, 16-token chunk of the adapter's tokens); a wave sums the shrink's
+// parts for its tokens once and sweeps 16 rows of each tile:
+// MFMA with A = u (token slots x rank, f32 split into f16 hi/lo), B = B_a^T
+// (rank x rows, f16 exact or f32 split).  Every (t, n) belongs to one
+// adapter, so the read-modify-write of y has no conflicts.
+#define EXPAND_RT 8  // 64-row tiles per workgroup
+#define EXPAND_KK 2  // rank steps of 32 held in registers: ranks up to 64
+REALM_DEV void lora_expand(const float *__restrict__ u, const int *__restrict__ ids,
+                           const LoraEntry *__restrict__ table, float *__restrict__ y, int M,
+                           int N, int rmax, int nparts, int pstride)
+{
+    __shared__ int toks[1024];
+    __shared__ int count;
+    __shared__ int wsum[4];
+    const int a = blockIdx.x;
+    adapter_tokens(ids, M, a, toks, &count, wsum);
+    const int tc = blockIdx.z * 16; // this workgroup's 16 tokens of the adapter
+    if (tc >= count)
+        return;
+    const LoraEntry e = table[a];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int r16 = lane & 15, c = lane >> 4;
-    const int row = blockIdx.y * 64 + wave * 16 + r16;
+    // loads read valid memory whatever the lane (rows past N read row N-1,
+    // token slots past the adapter's tokens its first token, ranks past the
+    // rank a valid group): such values only reach D entries that are never
+    // stored, or are masked to zero where they would enter a sum
+    const int ti = tc + r16;
+    const int tok = toks[ti < count ? ti : 0];
+    int toko[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        const int tj = tc + 4 * c + v;
+        toko[v] = toks[tj < count ? tj : 0];
+    }
     const int ksteps = (e.rank + 31) / 32;
-    for (int tc = 0; tc < count; tc += 16) {
-        const int ti = tc + r16;
-        const int tok = ti < count ? toks[ti] : -1;
-        floatx4 P = {0.f, 0.f, 0.f, 0.f};
-        for (int kk = 0; kk < ksteps; ++kk) {
-            const int j0 = 32 * kk + 8 * c; // this lane's 8 ranks
-            half8_t ah = {}, al = {}, bh = {}, bl = {};
-            if (tok >= 0 && j0 < e.rank) {
-                // u rows are padded to a multiple of 8; entries past this
-                // adapter's rank hold another call's values and are masked
-                const float4 *up = reinterpret_cast<const float4 *>(u + (size_t)tok * rmax + j0);
-                const float4 u0 = up[0], u1 = up[1];
-                const float uv[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+    for (int kk0 = 0; kk0 < ksteps; kk0 += EXPAND_KK) {
+        // this wave's A fragments (u of its 16 tokens, 64 ranks): the sum of
+        // the shrink's K parts, in part order, loads before the first add
+        half8_t ah[EXPAND_KK], al[EXPAND_KK];
+#pragma unroll
+        for (int q2 = 0; q2 < EXPAND_KK; ++q2) {
+            const int j0 = 32 * (kk0 + q2) + 8 * c; // this lane's 8 ranks
+            const int ju = min(j0, rmax - 8);
+            float uv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            for (int g0 = 0; g0 < nparts; g0 += 8) {
+                float4 p0[8], p1[8];
 #pragma unroll
                 for (int q = 0; q < 8; ++q) {
-                    const float vq = j0 + q < e.rank ? uv[q] : 0.f;
-                    const _Float16 h = (_Float16)vq;
-                    ah[q] = h;
-                    al[q] = (_Float16)(vq - (float)h);
+                    const int kp = min(g0 + q, nparts - 1);
+                    const float4 *up = reinterpret_cast<const float4 *>(
+                        u + (size_t)kp * pstride + (size_t)tok * rmax + ju);
+                    p0[q] = up[0];
+                    p1[q] = up[1];
                 }
-            }
-            if (row < N && j0 < e.rank) {
-                if (e.dtype && (e.rank & 7) == 0) { // one aligned 16-byte load
-                    bh = ld_h8(reinterpret_cast<const _Float16 *>(e.b) + (size_t)row * e.rank + j0);
-                } else {
 #pragma unroll
-                    for (int q = 0; q < 8; ++q) {
-                        const float vv = j0 + q < e.rank
-                                             ? lora_elem(e.b, e.dtype, (size_t)row * e.rank + j0 + q)
-                                             : 0.f;
-                        const _Float16 h = (_Float16)vv;
-                        bh[q] = h;
-                        bl[q] = (_Float16)(vv - (float)h);
+                for (int q = 0; q < 8; ++q) {
+                    if (g0 + q < nparts) {
+                        uv[0] += p0[q].x; uv[1] += p0[q].y; uv[2] += p0[q].z; uv[3] += p0[q].w;
+                        uv[4] += p1[q].x; uv[5] += p1[q].y; uv[6] += p1[q].z; uv[7] += p1[q].w;
                     }
                 }
             }
-            P = mfma(ah, bh, P);
-            P = mfma(al, bh, P);
-            if (!e.dtype)
-                P = mfma(ah, bl, P);
-        }
-        // D[token slot 4c+v][row r16]
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const int tj = tc + 4 * c + v;
-            if (tj < count && row < N) {
-                float *dst = y + (size_t)toks[tj] * N + row;
-                *dst += e.scale * P[v];
+            for (int q = 0; q < 8; ++q) {
+                const float vq = j0 + q < e.rank ? uv[q] : 0.f;
+                const _Float16 h = (_Float16)vq;
+                ah[q2][q] = h;
+                al[q2][q] = (_Float16)(vq - (float)h);
+            }
+        }
+        // the row tiles of this workgroup, 16 rows per wave each: all loads
+        // (y, B) of the 8 tiles first, then the MFMAs and stores
+        float yv[EXPAND_RT][4];
+        half8_t bh[EXPAND_RT][EXPAND_KK], bl[EXPAND_RT][EXPAND_KK];
+#pragma unroll
+        for (int rt = 0; rt < EXPAND_RT; ++rt) {
+            const int row = (blockIdx.y * EXPAND_RT + rt) * 64 + wave * 16 + r16;
+            const int rowc = min(row, N - 1);
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+                yv[rt][v] = y[(size_t)toko[v] * N + rowc];
+#pragma unroll
+            for (int q2 = 0; q2 < EXPAND_KK; ++q2) {
+                const int j0 = 32 * (kk0 + q2) + 8 * c;
+                if (e.dtype && (e.rank & 7) == 0) { // one aligned 16-byte load
+                    const half8_t bv = ld_h8(reinterpret_cast<const _Float16 *>(e.b) +
+                                             (size_t)rowc * e.rank + max(0, min(j0, e.rank - 8)));
+#pragma unroll
+                    for (int q = 0; q < 8; ++q)
+                        bh[rt][q2][q] = j0 + q < e.rank ? bv[q] : (_Float16)0.f;
+                    bl[rt][q2] = half8_t{};
+                } else {
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) {
+                        const float vv = lora_elem(e.b, e.dtype,
+                                                   (size_t)rowc * e.rank + min(j0 + q, e.rank - 1));
+                        const float vm = j0 + q < e.rank ? vv : 0.f;
+                        const _Float16 h = (_Float16)vm;
+                        bh[rt][q2][q] = h;
+                        bl[rt][q2][q] = (_Float16)(vm - (float)h);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int rt = 0; rt < EXPAND_RT; ++rt) {
+            const int row = (blockIdx.y * EXPAND_RT + rt) * 64 + wave * 16 + r16;
+            floatx4 P = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int q2 = 0; q2 < EXPAND_KK; ++q2) {
+                P = mfma(ah[q2], bh[rt][q2], P);
+                P = mfma(al[q2], bh[rt][q2], P);
+                if (!e.dtype)
+                    P = mfma(ah[q2], bl[rt][q2], P);
+            }
+            // D[token slot 4c+v][row r16]
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int tj = tc + 4 * c + v;
+                if (tj < count && row < N)
+                    y[(size_t)toks[tj] * N + row] = yv[rt][v] + e.scale * P[v];
             }
         }
     }
 }
 
 extern "C" __global__ __launch_bounds__(256) void realm_lora_expand(
-    const float *u, const int *ids, const LoraEntry *table, float *y, int M, int N, int rmax)
+    const float *u, const int *ids, const LoraEntry *table, float *y, int M, int N, int rmax,
+    int nparts, int pstride)
 {
-    lora_expand(u, ids, table, y, M, N, rmax);
+    lora_expand(u, ids, table, y, M, N, rmax, nparts, pstride);
 }
 
 #define DEF_SHRINK1(NAME, FMT, ORD, SUF)                                                   \
-    extern "C" __global__ __launch_bounds__(1024) void realm_lora_shrink_##NAME##_f32##SUF(\
+    extern "C" __global__ __launch_bounds__(256) void realm_lora_shrink_##NAME##_f32##SUF( \
         const _Float16 *xh, const _Float16 *xl, const float *tscale, const int *ids,      \
-        const LoraEntry *table, float *u, int M, int K, int KX, int rmax)                 \
+        const LoraEntry *table, float *part, int M, int K, int KX, int rmax, int pstride) \
     {                                                                                      \
-        lora_shrink<FMT, true, ORD>(xh, xl, tscale, ids, table, u, M, K, KX, rmax);        \
+        lora_shrink<FMT, true, ORD>(xh, xl, tscale, ids, table, part, M, K, KX, rmax,      \
+                                    pstride);                                              \
     }                                                                                      \
-    extern "C" __global__ __launch_bounds__(1024) void realm_lora_shrink_##NAME##_bf16##SUF(\
+    extern "C" __global__ __launch_bounds__(256) void realm_lora_shrink_##NAME##_bf16##SUF(\
         const _Float16 *xh, const _Float16 *xl, const float *tscale, const int *ids,      \
-        const LoraEntry *table, float *u, int M, int K, int KX, int rmax)                 \
+        const LoraEntry *table, float *part, int M, int K, int KX, int rmax, int pstride) \
     {                                                                                      \
-        lora_shrink<FMT, false, ORD>(xh, xl, tscale, ids, table, u, M, K, KX, rmax);       \
+        lora_shrink<FMT, false, ORD>(xh, xl, tscale, ids, table, part, M, K, KX, rmax,     \
+                                     pstride);                                             \
     }
 #define DEF_SHRINK(NAME, FMT) DEF_SHRINK1(NAME, FMT, 0, ) DEF_SHRINK1(NAME, FMT, 1, _o1)
 DEF_SHRINK(q4k, FMT_Q4K)

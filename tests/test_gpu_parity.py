@@ -364,13 +364,16 @@ def _oracle_lora(oracle, t, blocks, x, ids, adapters, n, k):
 
 @pytest.mark.parametrize("t", FORMATS)
 @pytest.mark.parametrize("dtype", [np.float16, np.float32])
-def test_multi_lora_small(backend, oracle, t, dtype):
-    g = synth.rng(300 + t)
-    n, k, m = 160, 512, 37
+@pytest.mark.parametrize("shape", [(160, 512, 37), (600, 1536, 70)])
+def test_multi_lora_small(backend, oracle, t, dtype, shape):
+    """Ranks 3 (not a multiple of 8) to 100 (past the 64 the expand holds in
+    registers); the second shape has several row groups and K parts."""
+    g = synth.rng(300 + t + shape[0])
+    n, k, m = shape
     blocks = synth.blocks(g, t, n, k)
     x = synth.activations(g, m, k)
     adapters, handles = [], []
-    for r in (8, 16, 64, 3):
+    for r in (8, 16, 64, 3, 100):
         a, b = synth.lora_adapter(g, r, k, n)
         a, b = a.astype(dtype), b.astype(dtype)
         adapters.append((a, b, r, 16.0))
