@@ -195,6 +195,25 @@ int thread_stream(hipStream_t *s)
     return REALM_OK;
 }
 
+// A second stream per thread, and a fork/join event pair, for work that can
+// run beside the main stream's (the LoRA shrink beside the base product).
+// Under graph capture the fork's event pulls the side stream into the graph.
+thread_local hipStream_t t_side = nullptr;
+thread_local hipEvent_t t_fork = nullptr, t_join = nullptr;
+
+int side_stream(hipStream_t *side, hipEvent_t *fork, hipEvent_t *join)
+{
+    if (!t_side) {
+        HIP_TRY(hipStreamCreateWithFlags(&t_side, hipStreamNonBlocking));
+        HIP_TRY(hipEventCreateWithFlags(&t_fork, hipEventDisableTiming));
+        HIP_TRY(hipEventCreateWithFlags(&t_join, hipEventDisableTiming));
+    }
+    *side = t_side;
+    *fork = t_fork;
+    *join = t_join;
+    return REALM_OK;
+}
+
 int pick_stream(void *user, hipStream_t *s)
 {
     if (user) {
@@ -591,9 +610,17 @@ int gemm_launch(const Weight &w, const XPrep &p, bool bf16, size_t M, const Gemm
                         &iM,  &iK,  &iKX,  &irmax,       &pstride};
         std::string name = std::string("realm_lora_shrink_") + fmt_name(w.type) +
                            (bf16 ? "_bf16" : "_f32") + (tile.ord ? "_o1" : "");
+        // the shrink needs only the prepared activations: it runs on the side
+        // stream beside the base product and joins before the expand
+        hipStream_t side;
+        hipEvent_t fork, join;
+        CHECK(side_stream(&side, &fork, &join));
+        HIP_TRY(hipEventRecord(fork, s));
+        HIP_TRY(hipStreamWaitEvent(side, fork, 0));
         CHECK(launch(name,
                      dim3((unsigned)set.count, (unsigned)((set.rmax + 15) / 16), (unsigned)nparts),
-                     dim3(256), 0, s, args));
+                     dim3(256), 0, side, args));
+        HIP_TRY(hipEventRecord(join, side));
     }
     std::string fmt = fmt_name(w.type);
     if (w.type == GGML_Q6_K && w.wide)
@@ -655,6 +682,10 @@ int gemm_launch(const Weight &w, const XPrep &p, bool bf16, size_t M, const Gemm
         const AdapterSet &set = *lora->set;
         const void *table = set.table;
         const int32_t *ids = lora->d_ids;
+        hipStream_t side;
+        hipEvent_t fork, join;
+        CHECK(side_stream(&side, &fork, &join));
+        HIP_TRY(hipStreamWaitEvent(s, join, 0));
         int iM = (int)M, iN = (int)w.n, rmax = (int)round_up(set.rmax, 8), np = nparts;
         void *eargs[] = {&u, (void *)&ids, (void *)&table, (void *)&d_y, &iM, &iN, &rmax, &np,
                          &pstride};
