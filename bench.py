@@ -291,6 +291,9 @@ def main() -> int:
     ap.add_argument("--traffic-probe", action="store_true",
                     help="no timing: one 256 MiB device copy (the counter reference) then "
                          "one gate/up GEMV launch per layer, for rocprofv3 --pmc runs")
+    ap.add_argument("--extra-only", choices=("batched", "lora", "prefill"),
+                    help="run one of the extra measurements alone (for kernel profiles) and "
+                         "print its result; no decode step, no JSON line")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
@@ -300,6 +303,12 @@ def main() -> int:
     from realm_amd.backend import HipGpuBackend
     be = HipGpuBackend(0)
     stream = be.stream()
+    if args.extra_only == "lora":
+        log(f"multi-LoRA: {lora_overhead(be, stream, 50)}")
+        return 0
+    if args.extra_only == "prefill":
+        log(f"prefill: {prefill(be, stream, 10)}")
+        return 0
     log(f"registering {args.layers} LLaMA-7B layers")
     model = Model7B(be, args.layers, 16)
     if args.traffic_probe:
@@ -341,6 +350,8 @@ def main() -> int:
                                "gb_per_s": round(value, 1)}}}
     roof = decode_roofline(be, model, stream, max(5, args.steps))
     log(f"roofline: {roof['achieved']} GB/s ({roof['frac'] * 100:.1f}% of peak)")
+    if args.extra_only == "batched":
+        args.skip_extra = False
     if not args.skip_extra:
         for mb in (4, 16):
             gr = capture(be, stream, lambda: model.step(mb, stream))
@@ -353,6 +364,8 @@ def main() -> int:
                                          "gb_per_s": round(gbs, 1)}
             log(f"decode b{mb}: {ms:.3f} ms/step, {gbs:.1f} GB/s")
     model.close()
+    if args.extra_only == "batched":
+        return 0
     cpu, cpu1 = None, None
     if not args.skip_extra:
         extra["multi_lora_config3"] = lora_overhead(be, stream, 50)
