@@ -61,12 +61,40 @@ REALM_DEV void xprep(const void *__restrict__ x, int bf16, _Float16 *__restrict_
     for (int r = 0; r < XPREP_R; ++r) {
         const int pg = r * XPREP_TH + threadIdx.x;
         const int k0 = pg < ngroups ? kwin<FMT, ORD>(pg) : 0;
+        // a window is 4 + 4 consecutive k (GAP apart): two vector loads when
+        // both halves are inside the row (K % 4 == 0 keeps them aligned)
+        const bool whole = live && pg < ngroups && k0 + GAP + 4 <= K && (K & 3) == 0 &&
+                           ((uintptr_t)x & (bf16 ? 7u : 15u)) == 0;
+        if (whole) {
 #pragma unroll
-        for (int w = 0; w < 8; ++w) {
-            const int k = k0 + (w & 3) + GAP * (w >> 2);
-            v[r][w] = (live && pg < ngroups && k < K) ? load_x(x, bf16, xrow + k) : 0.f;
-            amax = fmaxf(amax, fabsf(v[r][w]));
+            for (int hh = 0; hh < 2; ++hh) {
+                const size_t i0 = xrow + k0 + GAP * hh;
+                if (bf16) {
+                    const uint2 b = *reinterpret_cast<const uint2 *>(
+                        reinterpret_cast<const uint16_t *>(x) + i0);
+                    v[r][4 * hh + 0] = __uint_as_float(b.x << 16);
+                    v[r][4 * hh + 1] = __uint_as_float(b.x & 0xFFFF0000u);
+                    v[r][4 * hh + 2] = __uint_as_float(b.y << 16);
+                    v[r][4 * hh + 3] = __uint_as_float(b.y & 0xFFFF0000u);
+                } else {
+                    const float4 f = *reinterpret_cast<const float4 *>(
+                        reinterpret_cast<const float *>(x) + i0);
+                    v[r][4 * hh + 0] = f.x;
+                    v[r][4 * hh + 1] = f.y;
+                    v[r][4 * hh + 2] = f.z;
+                    v[r][4 * hh + 3] = f.w;
+                }
+            }
+        } else {
+#pragma unroll
+            for (int w = 0; w < 8; ++w) {
+                const int k = k0 + (w & 3) + GAP * (w >> 2);
+                v[r][w] = (live && pg < ngroups && k < K) ? load_x(x, bf16, xrow + k) : 0.f;
+            }
         }
+#pragma unroll
+        for (int w = 0; w < 8; ++w)
+            amax = fmaxf(amax, fabsf(v[r][w]));
     }
     // workgroup max: wave reduction (lane 63 ends with it), then LDS
     for (int off = 32; off > 0; off >>= 1)
