@@ -248,6 +248,95 @@ def prefill(be, stream: int, reps: int) -> dict:
     return out
 
 
+LAYER70 = [("wq", GGML_Q4_K, 8192, 8192), ("wk", GGML_Q4_K, 1024, 8192),
+           ("wv", GGML_Q4_K, 1024, 8192), ("wo", GGML_Q4_K, 8192, 8192),
+           ("w_gate", GGML_Q4_K, 28672, 8192), ("w_up", GGML_Q4_K, 28672, 8192),
+           ("w_down", GGML_Q6_K, 8192, 28672)]
+
+
+def config4(be, stream: int, reps: int) -> dict:
+    """Config 4: one LLaMA-70B-shape layer (541,851,648 packed bytes, more
+    than the 256 MB MALL, so every replay streams the weights from HBM).
+    decode: 32 tokens (f32 activations), the base set (QKV grouped, Wo,
+    gate/up grouped, W_down) against the same set with 8 rank-16 adapters on
+    q/k/v/o (Zipf(1.1) ids over 8, 10% without adapter).  prefill: 1024
+    tokens, bf16 activations, the seven products one after another."""
+    g = synth.rng(4)
+    hs = {name: be.register_weights(t, synth.blocks(g, t, n, k), n, k)
+          for name, t, n, k in LAYER70}
+    dims = {name: (n, k) for name, _t, n, k in LAYER70}
+    lora_on = ("wq", "wk", "wv", "wo")
+    adapters, sets = [], {}
+    for name in lora_on:
+        n, k = dims[name]
+        hl = [be.lora_register(*synth.lora_adapter(g, 16, k, n), 16, 16.0, k, n)
+              for _ in range(8)]
+        adapters += hl
+        sets[name] = be.lora_set_create(hl)
+    m_dec, m_pre = 32, 1024
+    ids = synth.adapter_ids(g, m_dec, 8)
+    d_ids = be.alloc(m_dec * 4).upload(ids)
+    xd = {k: be.alloc(m_dec * k * 4).upload(synth.activations(g, m_dec, k))
+          for k in (8192, 28672)}
+    xp = {k: be.alloc(m_pre * k * 2).upload(synth.activations_bf16(g, m_pre, k))
+          for k in (8192, 28672)}
+    y = {name: be.alloc(m_pre * n * 4) for name, (n, _k) in dims.items()}
+
+    def base():
+        be.matmul_group_dev([hs["wq"], hs["wk"], hs["wv"]], xd[8192].ptr, m_dec,
+                            [y["wq"].ptr, y["wk"].ptr, y["wv"].ptr], stream=stream)
+        be.matmul_dev(hs["wo"], xd[8192].ptr, m_dec, y["wo"].ptr, stream=stream)
+        be.matmul_group_dev([hs["w_gate"], hs["w_up"]], xd[8192].ptr, m_dec,
+                            [y["w_gate"].ptr, y["w_up"].ptr], stream=stream)
+        be.matmul_dev(hs["w_down"], xd[28672].ptr, m_dec, y["w_down"].ptr, stream=stream)
+
+    def with_lora():
+        for name in lora_on:
+            be.multi_lora_matmul_dev(hs[name], sets[name], xd[8192].ptr, m_dec, d_ids.ptr,
+                                     y[name].ptr, stream=stream)
+        be.matmul_group_dev([hs["w_gate"], hs["w_up"]], xd[8192].ptr, m_dec,
+                            [y["w_gate"].ptr, y["w_up"].ptr], stream=stream)
+        be.matmul_dev(hs["w_down"], xd[28672].ptr, m_dec, y["w_down"].ptr, stream=stream)
+
+    def pre():
+        for name, _t, _n, k in LAYER70:
+            be.matmul_dev(hs[name], xp[k].ptr, m_pre, y[name].ptr, stream=stream, bf16=True)
+
+    res = {}
+    wbytes = sum(weight_bytes(t, n, k) for _name, t, n, k in LAYER70)
+    distinct = len({int(i) for i in ids if i >= 0})
+    lbytes = distinct * sum(2 * 16 * (dims[nm][0] + dims[nm][1]) for nm in lora_on)
+    act = 4 * m_dec * (8192 * 4 + 28672) + 4 * m_dec * sum(n for n, _k in dims.values())
+    times = {}
+    for mode, fn in (("base", base), ("lora", with_lora), ("prefill", pre)):
+        gr = capture(be, stream, fn)
+        time_graph(be, gr, stream, 2)
+        times[mode] = time_graph(be, gr, stream, reps)
+        be.graph_release(gr)
+    tb, tl, tp = times["base"], times["lora"], times["prefill"]
+    res["decode_m32"] = {
+        "base_us": round(tb * 1e3, 1), "lora_us": round(tl * 1e3, 1),
+        "lora_overhead_pct": round((tl / tb - 1) * 100, 1),
+        "base_gb_per_s": round((wbytes + act) / (tb * 1e-3) / 1e9, 1),
+        "lora_gb_per_s": round((wbytes + act + lbytes) / (tl * 1e-3) / 1e9, 1),
+        "tok_per_s_80_layers": round(m_dec / (80 * tb * 1e-3), 1),
+        "distinct_adapters": distinct, "adapter_bytes": lbytes}
+    flops = 2.0 * m_pre * sum(n * k for _name, _t, n, k in LAYER70)
+    res["prefill_1024"] = {"us": round(tp * 1e3, 1),
+                           "tflops": round(flops / (tp * 1e-3) / 1e12, 1),
+                           "frac_mfma_peak": round(flops / (tp * 1e-3) / 1e12
+                                                   / MFMA_F16_PEAK_TFLOPS, 4)}
+    for s in sets.values():
+        be.lora_set_release(s)
+    for h in adapters:
+        be.lora_release(h)
+    for h in hs.values():
+        be.release_weights(h)
+    for b in [d_ids] + list(xd.values()) + list(xp.values()) + list(y.values()):
+        b.close()
+    return res
+
+
 def cpu_baseline(seconds: float) -> tuple[dict, dict]:
     """The oracle's C restatement of realm-compute-cpu on this host's cores:
     Q4_K 4096x4096 matvec (batch 1), dequantize-row-then-dot on all cores, and
@@ -291,7 +380,7 @@ def main() -> int:
     ap.add_argument("--traffic-probe", action="store_true",
                     help="no timing: one 256 MiB device copy (the counter reference) then "
                          "one gate/up GEMV launch per layer, for rocprofv3 --pmc runs")
-    ap.add_argument("--extra-only", choices=("batched", "lora", "prefill"),
+    ap.add_argument("--extra-only", choices=("batched", "lora", "prefill", "config4"),
                     help="run one of the extra measurements alone (for kernel profiles) and "
                          "print its result; no decode step, no JSON line")
     args = ap.parse_args()
@@ -308,6 +397,9 @@ def main() -> int:
         return 0
     if args.extra_only == "prefill":
         log(f"prefill: {prefill(be, stream, 10)}")
+        return 0
+    if args.extra_only == "config4":
+        log(f"config4: {config4(be, stream, 10)}")
         return 0
     log(f"registering {args.layers} LLaMA-7B layers")
     model = Model7B(be, args.layers, 16)
@@ -372,6 +464,8 @@ def main() -> int:
         log(f"multi-LoRA: {extra['multi_lora_config3']}")
         extra["prefill_config2"] = prefill(be, stream, 10)
         log(f"prefill: {extra['prefill_config2']}")
+        extra["config4_70b_layer"] = config4(be, stream, 10)
+        log(f"config4: {extra['config4_70b_layer']}")
         cpu, cpu1 = cpu_baseline(args.cpu_seconds)
         extra["cpu_baseline_1thread"] = cpu1
         log(f"cpu baseline: {cpu}")

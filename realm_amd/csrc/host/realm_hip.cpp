@@ -485,7 +485,7 @@ struct GemmTile {
     unsigned rows_per_wg, toks_per_wg, threads;
     bool tiled = false; // LDS-tiled kernel (gemm_tiled.hip): 1-D grid over tiles
     int ord = 0;        // activation slot order the kernel reads
-    int ks = 1;         // tiled: K splits (parts summed by realm_gemm_reduce)
+    int ks = 1;         // tiled: K splits (parts summed by realm_gemm_tiled_reduce)
 };
 
 // LDS-tiled kernel "t<WR><WT><TN><TM><mode><NS>": WR x WT waves, each TN
@@ -520,10 +520,11 @@ bool tiled_tile(const std::string &name, bool bf16, int ks, GemmTile *t)
 //    x 64 tokens) tiles.
 GemmTile gemm_tile(const Weight &w, size_t M, bool bf16)
 {
-    if (const char *env = getenv("REALM_GEMM_TILE")) { // tuning override
+    if (const char *env = getenv("REALM_GEMM_TILE")) { // tuning override (Q4_K, Q6_K)
         const char *ks = getenv("REALM_GEMM_KS");
         GemmTile t;
-        if (tiled_tile(env, bf16, ks ? atoi(ks) : 1, &t))
+        if ((w.type == GGML_Q4_K || w.type == GGML_Q6_K) && w.kx % 256 == 0 &&
+            tiled_tile(env, bf16, ks ? atoi(ks) : 1, &t))
             return t;
     }
     size_t M16 = round_up(M, 16);
@@ -590,6 +591,92 @@ int prep_x(const Weight &w, const void *d_x, bool bf16, size_t M, const GemmTile
                   dim3((unsigned)rows), dim3(1024), 0, s, args);
 }
 
+// One launch of the LDS-tiled kernel over 1..4 matrices of one format and K
+// that share the prepared activations (Q/K/V, gate/up), each padded to whole
+// row tiles.  With a K split, realm_gemm_tiled_reduce then sums each tile's
+// parts in split order (deterministic) into the matrices' outputs.
+int tiled_launch(const Weight *const *w, float *const *d_y, int count, const XPrep &p, bool bf16,
+                 size_t M, const GemmTile &tile, hipStream_t s)
+{
+    if (count < 1 || count > REALM_GEMM_MAX_SEGS)
+        return fail(REALM_INVALID_ARGUMENT, "a tiled launch takes 1..4 matrices");
+    const Weight &w0 = *w[0];
+    if (w0.kx % 256)
+        return fail(REALM_INVALID_ARGUMENT, "tiled GEMM needs K padded to a multiple of 256");
+    // Q6_K with some sub-scale beyond +-63 needs the wide decode; it is exact
+    // for every Q6_K matrix, so a group with one such matrix uses it for all
+    bool wide = false;
+    for (int i = 0; i < count; ++i)
+        wide = wide || (w[i]->type == GGML_Q6_K && w[i]->wide);
+    const std::string name =
+        "realm_gemm_" + std::string(wide ? "q6kw" : fmt_name(w0.type)) + "_" + tile.name;
+    GemmArgs g;
+    std::memset(&g, 0, sizeof g);
+    g.w0 = w0.w0;
+    g.w1 = w0.w1;
+    g.w2 = w0.w2;
+    g.y = d_y[0];
+    g.N = (int)w0.n;
+    g.xh = p.xh;
+    g.xl = p.xl;
+    g.xm = p.xm;
+    g.tscale = (const float *)p.ts;
+    g.K = (int)w0.k;
+    g.KX = (int)w0.kx;
+    g.M = (int)M;
+    g.nan_fb = g_nan_fb.load();
+    g.nseg = count;
+    size_t rt = 0;
+    for (int i = 0; i < REALM_GEMM_MAX_SEGS; ++i) {
+        g.seg_tile[i] = i < count ? (int)rt : INT32_MAX;
+        if (i >= count)
+            continue;
+        g.seg_n[i] = (int)w[i]->n;
+        g.seg_w0[i] = w[i]->w0;
+        g.seg_w1[i] = w[i]->w1;
+        g.seg_w2[i] = w[i]->w2;
+        g.seg_y[i] = d_y[i];
+        rt += (w[i]->n + tile.rows_per_wg - 1) / tile.rows_per_wg;
+    }
+    g.seg_tile[REALM_GEMM_MAX_SEGS] = INT32_MAX;
+    const size_t TT = (p.Mp + tile.toks_per_wg - 1) / tile.toks_per_wg;
+    if (rt * TT * 8 > (size_t)INT32_MAX)
+        return fail(REALM_INVALID_ARGUMENT, "batched product too large for one launch");
+    g.rtiles = (int)rt;
+    const int nblk = (int)(w0.kx / 256);
+    g.ksplit = tile.ks < nblk ? tile.ks : nblk;
+    if (g.ksplit > 1) {
+        void *part = nullptr;
+        CHECK(ws_get(s, WS_PART,
+                     rt * TT * g.ksplit * tile.rows_per_wg * tile.toks_per_wg * sizeof(float),
+                     &part));
+        g.part = (float *)part;
+    }
+    // XCDs along the token tiles: enough that each XCD's share of the
+    // activations (f16, hi and lo for f32 input) stays within 2 MB of L2
+    const size_t xbytes = p.Mp * w0.kx * (bf16 ? 2 : 4);
+    int xt = 1;
+    while (xt < 8 && (size_t)xt < TT && xbytes / xt > ((size_t)2 << 20))
+        xt *= 2;
+    if (const char *env = getenv("REALM_GEMM_XT")) { // tuning override
+        const int e = atoi(env);
+        xt = e == 1 || e == 2 || e == 4 || e == 8 ? e : xt;
+    }
+    g.xt = xt;
+    const size_t xr = 8 / xt, rk = rt * (size_t)g.ksplit;
+    const dim3 grid((unsigned)(8 * ((rk + xr - 1) / xr) * ((TT + xt - 1) / xt)));
+    void *args[] = {&g};
+    CHECK(launch(name, grid, dim3(tile.threads), 0, s, args));
+    if (g.ksplit > 1) {
+        int grows = (int)tile.rows_per_wg, gtok = (int)tile.toks_per_wg;
+        void *rargs[] = {&g, &grows, &gtok};
+        CHECK(launch("realm_gemm_tiled_reduce",
+                     dim3((unsigned)(rt * TT), (unsigned)((grows * gtok + 255) / 256)), dim3(256),
+                     0, s, rargs));
+    }
+    return REALM_OK;
+}
+
 int gemm_launch(const Weight &w, const XPrep &p, bool bf16, size_t M, const GemmTile &tile,
                 float *d_y, hipStream_t s, const LoraCall *lora)
 {
@@ -622,60 +709,34 @@ int gemm_launch(const Weight &w, const XPrep &p, bool bf16, size_t M, const Gemm
                      dim3(256), 0, side, args));
         HIP_TRY(hipEventRecord(join, side));
     }
-    std::string fmt = fmt_name(w.type);
-    if (w.type == GGML_Q6_K && w.wide)
-        fmt = "q6kw";
-    std::string name = "realm_gemm_" + fmt + "_" + tile.name;
-    if (!tile.tiled)
-        name += bf16 ? "_bf16" : "_f32";
-    GemmArgs g;
-    std::memset(&g, 0, sizeof g);
-    g.w0 = w.w0;
-    g.w1 = w.w1;
-    g.w2 = w.w2;
-    g.xh = p.xh;
-    g.xl = p.xl;
-    g.xm = p.xm;
-    g.tscale = (const float *)p.ts;
-    g.y = d_y;
-    g.N = (int)w.n;
-    g.K = (int)w.k;
-    g.KX = (int)w.kx;
-    g.M = (int)M;
-    g.nan_fb = g_nan_fb.load();
-    void *args[] = {&g};
-    dim3 grid((unsigned)((w.n + tile.rows_per_wg - 1) / tile.rows_per_wg),
-              (unsigned)((p.Mp + tile.toks_per_wg - 1) / tile.toks_per_wg));
-    g.ksplit = 1;
     if (tile.tiled) {
-        if (w.kx % 256)
-            return fail(REALM_INVALID_ARGUMENT, "tiled GEMM needs K padded to a multiple of 256");
-        const int nblk = (int)(w.kx / 256);
-        g.ksplit = tile.ks < nblk ? tile.ks : nblk;
-        if (g.ksplit > 1) {
-            void *part = nullptr;
-            CHECK(ws_get(s, WS_PART, (size_t)g.ksplit * M * w.n * 4, &part));
-            g.part = (float *)part;
-        }
-        // XCDs along the token tiles: enough that each XCD's share of the
-        // activations (f16, hi and lo for f32 input) stays within 2 MB of L2
-        const unsigned RT = grid.x, TT = grid.y;
-        const size_t xbytes = p.Mp * w.kx * (bf16 ? 2 : 4);
-        int xt = 1;
-        while (xt < 8 && (unsigned)xt < TT && xbytes / xt > ((size_t)2 << 20))
-            xt *= 2;
-        if (const char *env = getenv("REALM_GEMM_XT")) // tuning override
-            xt = atoi(env) == 1 || atoi(env) == 2 || atoi(env) == 4 || atoi(env) == 8 ? atoi(env) : xt;
-        g.xt = xt;
-        const unsigned xr = 8 / xt, rk = RT * (unsigned)g.ksplit;
-        grid = dim3(8 * ((rk + xr - 1) / xr) * ((TT + xt - 1) / xt));
-    }
-    CHECK(launch(name, grid, dim3(tile.threads), 0, s, args));
-    if (g.ksplit > 1) {
-        int n = (int)(M * w.n), ks = g.ksplit;
-        void *rargs[] = {(void *)&g.part, (void *)&d_y, &n, &ks};
-        CHECK(launch("realm_gemm_reduce", dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
-                     rargs));
+        const Weight *wp = &w;
+        CHECK(tiled_launch(&wp, &d_y, 1, p, bf16, M, tile, s));
+    } else {
+        std::string fmt = fmt_name(w.type);
+        if (w.type == GGML_Q6_K && w.wide)
+            fmt = "q6kw";
+        const std::string name = "realm_gemm_" + fmt + "_" + tile.name + (bf16 ? "_bf16" : "_f32");
+        GemmArgs g;
+        std::memset(&g, 0, sizeof g);
+        g.w0 = w.w0;
+        g.w1 = w.w1;
+        g.w2 = w.w2;
+        g.xh = p.xh;
+        g.xl = p.xl;
+        g.xm = p.xm;
+        g.tscale = (const float *)p.ts;
+        g.y = d_y;
+        g.N = (int)w.n;
+        g.K = (int)w.k;
+        g.KX = (int)w.kx;
+        g.M = (int)M;
+        g.nan_fb = g_nan_fb.load();
+        g.ksplit = 1;
+        void *args[] = {&g};
+        const dim3 grid((unsigned)((w.n + tile.rows_per_wg - 1) / tile.rows_per_wg),
+                        (unsigned)((p.Mp + tile.toks_per_wg - 1) / tile.toks_per_wg));
+        CHECK(launch(name, grid, dim3(tile.threads), 0, s, args));
     }
     if (lora) {
         // y += scale_a B_a u per token, one workgroup per (adapter, 64 rows)
@@ -1103,9 +1164,27 @@ REALM_API int realm_hip_weights_matmul_group_dev(const uint64_t *handles, size_t
     // per matrix
     if (batch == 0)
         return REALM_OK;
-    const GemmTile tile = gemm_tile(w[0], batch, false);
+    // the tile and K split are chosen for the group's rows together
+    Weight all = w[0];
+    all.n = 0;
+    for (size_t i = 0; i < count; ++i)
+        all.n += w[i].n;
+    if (all.n == 0)
+        return REALM_OK;
+    const GemmTile tile = gemm_tile(all, batch, false);
     XPrep p;
     CHECK(prep_x(w[0], d_input, false, batch, tile, s, &p));
+    if (tile.tiled) { // one launch for the whole group
+        const Weight *live[REALM_GEMV_MAX_MATS];
+        float *ys[REALM_GEMV_MAX_MATS];
+        int nlive = 0;
+        for (size_t i = 0; i < count; ++i)
+            if (w[i].n) {
+                live[nlive] = &w[i];
+                ys[nlive++] = d_outs[i];
+            }
+        return tiled_launch(live, ys, nlive, p, false, batch, tile, s);
+    }
     for (size_t i = 0; i < count; ++i)
         if (w[i].n)
             CHECK(gemm_launch(w[i], p, false, batch, tile, d_outs[i], s, nullptr));

@@ -42,6 +42,12 @@ REALM_DEV floatx16 mfma32(half8_t a, half8_t b, floatx16 c)
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
+// One matrix of a launch: its weight streams and shape.
+struct Mat {
+    const void *w0, *w1, *w2;
+    int N, K, KX;
+};
+
 // Raw weight bytes of one 32-row tile and one 256-k block as lane
 // (r32 = row within the tile, h = lane half) needs them: k 128h .. 128h+127
 // of the block (Q4_K, Q6_K), or bytes 8h..8h+7 of every 16-byte chunk (Q8_0).
@@ -66,7 +72,7 @@ struct Raw<FMT_Q80> {
 
 // Rows past N read row N-1 (always resident); their results land in D
 // columns that are never stored.
-REALM_DEV void load_raw(Raw<FMT_Q4K> &r, const GemmArgs &g, int row, int blk, int h)
+REALM_DEV void load_raw(Raw<FMT_Q4K> &r, const Mat &g, int row, int blk, int h)
 {
     const int B = g.K >> 8;
     const size_t U = (size_t)(g.K >> 6);
@@ -77,7 +83,7 @@ REALM_DEV void load_raw(Raw<FMT_Q4K> &r, const GemmArgs &g, int row, int blk, in
     r.q[3] = ldg16(qp + U * 16 + 16);
     r.hd = ldg16((const uint8_t *)g.w0 + ((size_t)row * B + blk) * 16);
 }
-REALM_DEV void load_raw(Raw<FMT_Q6K> &r, const GemmArgs &g, int row, int blk, int h)
+REALM_DEV void load_raw(Raw<FMT_Q6K> &r, const Mat &g, int row, int blk, int h)
 {
     const int B = g.K >> 8;
     const size_t U = 4 * (size_t)B, bi = (size_t)row * B + blk;
@@ -91,7 +97,7 @@ REALM_DEV void load_raw(Raw<FMT_Q6K> &r, const GemmArgs &g, int row, int blk, in
     r.sc = ldg8((const int8_t *)g.w1 + bi * 16 + 8 * h);
     r.d = *reinterpret_cast<const uint16_t *>((const uint8_t *)g.w0 + bi * 2);
 }
-REALM_DEV void load_raw(Raw<FMT_Q80> &r, const GemmArgs &g, int row, int blk, int h)
+REALM_DEV void load_raw(Raw<FMT_Q80> &r, const Mat &g, int row, int blk, int h)
 {
     const size_t U = (size_t)(g.KX >> 6), B32 = (size_t)(g.KX >> 5);
     const uint8_t *qrow = (const uint8_t *)g.w1 + (size_t)row * g.KX + 8 * h;
@@ -281,7 +287,7 @@ REALM_DEV void gemm_tiled(const GemmArgs &g)
     // activations while its row tiles' weights stream through.  Workgroup ids
     // past an XCD's block exit at once.
     const int KS = g.ksplit, XT = g.xt, XR = 8 / XT;
-    const int RT = (g.N + GROWS - 1) / GROWS;
+    const int RT = g.rtiles;
     const int TT = (g.M + GTOK - 1) / GTOK;
     const int RK = RT * KS;
     const int RKX = (RK + XR - 1) / XR, TTX = (TT + XT - 1) / XT;
@@ -291,8 +297,20 @@ REALM_DEV void gemm_tiled(const GemmArgs &g)
     if (jr >= RKX || rk >= RK || tt >= TT)
         return;
     const int kc = rk % KS, rt = rk / KS;
+    // the matrix (segment) of row tile rt; selects, not an indexed array, so
+    // that nothing lands in scratch memory
+    const int seg = (rt >= g.seg_tile[1]) + (rt >= g.seg_tile[2]) + (rt >= g.seg_tile[3]);
+    auto pick = [&](auto a0, auto a1, auto a2, auto a3) {
+        return seg == 0 ? a0 : seg == 1 ? a1 : seg == 2 ? a2 : a3;
+    };
+    const Mat mat{pick(g.seg_w0[0], g.seg_w0[1], g.seg_w0[2], g.seg_w0[3]),
+                  pick(g.seg_w1[0], g.seg_w1[1], g.seg_w1[2], g.seg_w1[3]),
+                  pick(g.seg_w2[0], g.seg_w2[1], g.seg_w2[2], g.seg_w2[3]),
+                  pick(g.seg_n[0], g.seg_n[1], g.seg_n[2], g.seg_n[3]), g.K, g.KX};
+    float *const yseg = pick(g.seg_y[0], g.seg_y[1], g.seg_y[2], g.seg_y[3]);
+    const int rtl = rt - pick(g.seg_tile[0], g.seg_tile[1], g.seg_tile[2], g.seg_tile[3]);
     const int m0 = tt * GTOK;
-    const int row0 = rt * GROWS + wr * TN * 32 + r32; // this lane's row in tile a: row0 + 32a
+    const int row0 = rtl * GROWS + wr * TN * 32 + r32; // this lane's row in tile a: row0 + 32a
     const int nblk = (FMT == FMT_Q80 ? g.KX : g.K) >> 8;
     const int b0 = kc * nblk / KS, b1 = (kc + 1) * nblk / KS;
 
@@ -394,7 +412,7 @@ REALM_DEV void gemm_tiled(const GemmArgs &g)
         stage(buf, blk);
 #pragma unroll
         for (int a = 0; a < TN; ++a)
-            load_raw(w[a], g, min(row0 + 32 * a, g.N - 1), blk, h);
+            load_raw(w[a], mat, min(row0 + 32 * a, mat.N - 1), blk, h);
         __builtin_amdgcn_sched_barrier(0);
     };
 
@@ -563,10 +581,9 @@ REALM_DEV void gemm_tiled(const GemmArgs &g)
         }
     }
 
-    // ---- epilogue: undo the token rescale; store y, or this K split's part.
-    // All token scales are loaded before the first store: a load issued
-    // after stores would wait for them too (stores count in vmcnt).
-    float *out = KS > 1 ? g.part + (size_t)kc * g.M * g.N : g.y;
+    // ---- epilogue: undo the token rescale.  All token scales are loaded
+    // before the first store: a load issued after stores would wait for them
+    // too (stores count in vmcnt).
     const int tw = m0 + wt * TM * TOK;
     float ts[TM][16];
 #pragma unroll
@@ -586,22 +603,51 @@ REALM_DEV void gemm_tiled(const GemmArgs &g)
                 ts[bb][4 * q4 + 3] = t4.w;
             }
         }
+    // this workgroup's sums: vals[bb][v / VS][a] for token slot(s) v of tile
+    // bb (packed: slots v, v + 1 are one token's hi and lo), row tile a
+    constexpr int VS = PACK ? 2 : 1, NV = 16 / VS;
+    float vals[TM][NV][TN];
 #pragma unroll
     for (int bb = 0; bb < TM; ++bb)
 #pragma unroll
-        for (int v = 0; v < 16; v += (PACK ? 2 : 1)) {
-            // slot 8(v/4) + 4h + v%4; packed: slots 2t, 2t+1 are token t's (hi, lo)
-            const int slot = 8 * (v >> 2) + 4 * h + (v & 3);
-            const int tok = PACK ? tw + 16 * bb + (slot >> 1) : tw + 32 * bb + slot;
+        for (int v = 0; v < 16; v += VS)
+#pragma unroll
+            for (int a = 0; a < TN; ++a)
+                vals[bb][v / VS][a] = (PACK ? acc[a][bb][v] + acc[a][bb][v + 1] : acc[a][bb][v]) *
+                                      ts[bb][v];
+    // the position of value (bb, v, a) within the tile: token tl, row rl
+    auto tloc = [&](int bb, int v) {
+        const int slot = 8 * (v >> 2) + 4 * h + (v & 3);
+        return wt * TM * TOK + (PACK ? 16 * bb + (slot >> 1) : 32 * bb + slot);
+    };
+    const int rl0 = wr * TN * 32 + r32; // + 32a
+    if (KS > 1) {
+        // this split's part of the tile; realm_gemm_tiled_reduce adds the
+        // parts in split order
+        constexpr int TILE = GROWS * GTOK;
+        float *pt = g.part + ((size_t)(rt * TT + tt) * KS + kc) * TILE;
+#pragma unroll
+        for (int bb = 0; bb < TM; ++bb)
+#pragma unroll
+            for (int v = 0; v < 16; v += VS)
+#pragma unroll
+                for (int a = 0; a < TN; ++a)
+                    pt[tloc(bb, v) * GROWS + rl0 + 32 * a] = vals[bb][v / VS][a];
+        return;
+    }
+#pragma unroll
+    for (int bb = 0; bb < TM; ++bb)
+#pragma unroll
+        for (int v = 0; v < 16; v += VS) {
+            const int tok = m0 + tloc(bb, v);
             if (tok >= g.M)
                 continue;
 #pragma unroll
             for (int a = 0; a < TN; ++a) {
                 const int row = row0 + 32 * a;
-                if (row >= g.N)
+                if (row >= mat.N)
                     continue;
-                const float sum = PACK ? acc[a][bb][v] + acc[a][bb][v + 1] : acc[a][bb][v];
-                out[(size_t)tok * g.N + row] = sum * ts[bb][v];
+                yseg[(size_t)tok * mat.N + row] = vals[bb][v / VS][a];
             }
         }
 }
@@ -632,17 +678,33 @@ REALM_DEV void gemm_tiled(const GemmArgs &g)
 GEMM_TILED_SET(q4k, FMT_Q4K, false)
 GEMM_TILED_SET(q6k, FMT_Q6K, false)
 GEMM_TILED_SET(q6kw, FMT_Q6K, true)
-GEMM_TILED_SET(q80, FMT_Q80, false)
 
-// y = sum over the K splits of the parts, in split order (deterministic)
-extern "C" __global__ __launch_bounds__(256) void realm_gemm_reduce(const float *part, float *y,
-                                                                    int n, int ks)
+// y = the sum of a tiled launch's K-split parts, in split order (so results
+// are deterministic).  Workgroup (tile, chunk): 256 of the tile's
+// grows x gtok values; tile = row tile x token tiles + token tile, and the
+// row tile's segment names the output matrix.
+extern "C" __global__ __launch_bounds__(256) void realm_gemm_tiled_reduce(GemmArgs g, int grows,
+                                                                          int gtok)
 {
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= n)
+    const int TT = (g.M + gtok - 1) / gtok, tile = blockIdx.x;
+    const int rt = tile / TT, tt = tile - rt * TT;
+    const int e = blockIdx.y * 256 + threadIdx.x, TILE = grows * gtok;
+    if (e >= TILE)
         return;
-    float s = part[i];
-    for (int k = 1; k < ks; ++k)
-        s += part[(size_t)k * n + i];
-    y[i] = s;
+    const int seg = (rt >= g.seg_tile[1]) + (rt >= g.seg_tile[2]) + (rt >= g.seg_tile[3]);
+    auto pick = [&](auto a0, auto a1, auto a2, auto a3) {
+        return seg == 0 ? a0 : seg == 1 ? a1 : seg == 2 ? a2 : a3;
+    };
+    const int N = pick(g.seg_n[0], g.seg_n[1], g.seg_n[2], g.seg_n[3]);
+    float *const y = pick(g.seg_y[0], g.seg_y[1], g.seg_y[2], g.seg_y[3]);
+    const int rtl = rt - pick(g.seg_tile[0], g.seg_tile[1], g.seg_tile[2], g.seg_tile[3]);
+    const int tl = e / grows, rl = e - tl * grows;
+    const int row = rtl * grows + rl, tok = tt * gtok + tl;
+    if (row >= N || tok >= g.M)
+        return;
+    const float *p = g.part + (size_t)tile * g.ksplit * TILE + e;
+    float sum = p[0];
+    for (int c = 1; c < g.ksplit; ++c)
+        sum += p[(size_t)c * TILE];
+    y[(size_t)tok * N + row] = sum;
 }

@@ -19,6 +19,8 @@ struct LoraEntry {
     int32_t pad;
 };
 
+#define REALM_GEMM_MAX_SEGS 4
+
 // Arguments of the realm_gemm_* kernels.
 struct GemmArgs {
     const void *w0;     // Q4_K hdr | Q6_K d  | Q8_0 d
@@ -37,9 +39,20 @@ struct GemmArgs {
     const float *u;               // LoRA: shrink output [Mp][rmax]
     int32_t rmax;
     int32_t ksplit;               // tiled kernels: K splits (1 = none)
-    float *part;                  // tiled kernels, ksplit > 1: parts [ksplit][M][N]
+    float *part;                  // tiled kernels, ksplit > 1: parts, tile-major
+                                  // [tile][ksplit][token in tile][row in tile]
     int32_t xt;                   // tiled kernels: XCDs along the token tiles (1, 2, 4, 8)
-    int32_t pad2;
+    // tiled kernels: the matrices of one launch (up to 4 sharing the input,
+    // e.g. Q/K/V), each padded to whole row tiles; segment i owns row tiles
+    // seg_tile[i] .. seg_tile[i + 1] - 1 (unused entries hold INT32_MAX)
+    int32_t nseg;
+    int32_t rtiles;               // row tiles of all segments
+    int32_t seg_tile[REALM_GEMM_MAX_SEGS + 1];
+    int32_t seg_n[REALM_GEMM_MAX_SEGS];
+    const void *seg_w0[REALM_GEMM_MAX_SEGS];
+    const void *seg_w1[REALM_GEMM_MAX_SEGS];
+    const void *seg_w2[REALM_GEMM_MAX_SEGS];
+    float *seg_y[REALM_GEMM_MAX_SEGS];
 };
 
 // Arguments of the realm_gemv_* kernels: up to 4 matrices of one format

@@ -305,6 +305,67 @@ def test_tiled_variants(backend, oracle, monkeypatch, tile, ks, t):
         assert rc == 0 and err < REL_TOL
 
 
+@pytest.mark.parametrize("t", FORMATS)
+@pytest.mark.parametrize("m", [1, 4, 16, 37])
+def test_grouped_launch(backend, oracle, t, m):
+    """Up to four matrices that share the input in one call (Q/K/V-like,
+    ragged row counts): the grouped GEMV at batch 1, per-matrix
+    small-batch tiles, and one LDS-tiled launch over all row tiles (Q4_K /
+    Q6_K from 16 tokens), each output against the oracle."""
+    g = synth.rng(zlib.crc32(f"group{t}{m}".encode()) % 100000)
+    k = 1536
+    ns = (300, 128, 77)
+    blocks = [synth.blocks(g, t, n, k) for n in ns]
+    x = synth.activations(g, m, k)
+    hs = [backend.register_weights(t, b, n, k) for b, n in zip(blocks, ns)]
+    dx = backend.alloc(x.nbytes).upload(x)
+    dys = [backend.alloc(m * n * 4) for n in ns]
+    try:
+        outs = []
+        for rep in range(2):
+            backend.matmul_group_dev(hs, dx.ptr, m, [d.ptr for d in dys])
+            backend.synchronize()
+            outs.append([d.download(np.float32, m * n).reshape(m, n) for d, n in zip(dys, ns)])
+        kernel = backend.last_kernel()
+    finally:
+        for h in hs:
+            backend.release_weights(h)
+        dx.close()
+        for d in dys:
+            d.close()
+    if m >= 16 and t != GGML_Q8_0:
+        assert "_t41" in kernel or "tiled_reduce" in kernel, kernel
+    for i, (b, n) in enumerate(zip(blocks, ns)):
+        assert bits_equal(outs[0][i], outs[1][i])  # repeatable
+        rc, ref = oracle.candle_fused(t, b, x, m, n, k)
+        err = rel_l2(outs[0][i], ref.reshape(m, n))
+        print(f"group {NAMES[t]} m={m} mat {i} n={n} rel_l2={err:.3e}")
+        assert rc == 0 and err < REL_TOL
+
+
+@pytest.mark.parametrize("ks", [2, 3, 6])
+def test_tiled_ksplit_repeat(backend, oracle, monkeypatch, ks):
+    """K-split parts summed in split order: results are bit-identical from
+    call to call, also when calls of different shapes (and part-buffer
+    sizes) alternate on one stream."""
+    monkeypatch.setenv("REALM_GEMM_TILE", "t4112p2")
+    monkeypatch.setenv("REALM_GEMM_KS", str(ks))
+    g = synth.rng(500 + ks)
+    k = 1536
+    cases = [(GGML_Q4_K, 300, 37), (GGML_Q6_K, 520, 70), (GGML_Q4_K, 129, 16)]
+    data = [(t, n, m, synth.blocks(g, t, n, k), synth.activations(g, m, k)) for t, n, m in cases]
+    first = {}
+    for rep in range(3):
+        for i, (t, n, m, b, x) in enumerate(data):
+            got = _dev_matmul(backend, t, b, n, k, x, False)
+            if rep == 0:
+                first[i] = got
+                rc, ref = oracle.candle_fused(t, b, x, m, n, k)
+                assert rc == 0 and rel_l2(got, ref.reshape(m, n)) < REL_TOL
+            else:
+                assert bits_equal(got, first[i]), (rep, i)
+
+
 def test_q6k_wide_scales(backend, oracle):
     """Q6_K sub-scales over the full int8 range use the split-scale path."""
     g = synth.rng(66)
