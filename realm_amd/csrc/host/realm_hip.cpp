@@ -518,13 +518,19 @@ bool tiled_tile(const std::string &name, bool bf16, int ks, GemmTile *t)
 //    launch has at least 256 workgroups;
 //  * Q8_0: gemm.hip's decode (16 rows x 16..64 tokens) or prefill (128 rows
 //    x 64 tokens) tiles.
+// The tiled kernel's formats; its per-lane weight offsets are 32-bit.
+bool tiled_ok(const Weight &w)
+{
+    return (w.type == GGML_Q4_K || w.type == GGML_Q6_K) && w.kx % 256 == 0 &&
+           w.bytes < ((size_t)1 << 32);
+}
+
 GemmTile gemm_tile(const Weight &w, size_t M, bool bf16)
 {
     if (const char *env = getenv("REALM_GEMM_TILE")) { // tuning override (Q4_K, Q6_K)
         const char *ks = getenv("REALM_GEMM_KS");
         GemmTile t;
-        if ((w.type == GGML_Q4_K || w.type == GGML_Q6_K) && w.kx % 256 == 0 &&
-            tiled_tile(env, bf16, ks ? atoi(ks) : 1, &t))
+        if (tiled_ok(w) && tiled_tile(env, bf16, ks ? atoi(ks) : 1, &t))
             return t;
     }
     size_t M16 = round_up(M, 16);
@@ -532,7 +538,7 @@ GemmTile gemm_tile(const Weight &w, size_t M, bool bf16)
         return {"s1", 16, 8, 1024};
     if (bf16 && M <= 32)
         return M <= 16 ? GemmTile{"s1", 16, 16, 1024} : GemmTile{"s2", 16, 32, 512};
-    if ((w.type == GGML_Q4_K || w.type == GGML_Q6_K) && w.kx % 256 == 0) {
+    if (tiled_ok(w)) {
         GemmTile t;
         const char *name = bf16 ? (w.type == GGML_Q4_K ? "t4112b2" : "t4112b3")
                                 : (M <= 16 ? "t4111p2" : "t4112p2");
@@ -1167,8 +1173,10 @@ REALM_API int realm_hip_weights_matmul_group_dev(const uint64_t *handles, size_t
     // the tile and K split are chosen for the group's rows together
     Weight all = w[0];
     all.n = 0;
-    for (size_t i = 0; i < count; ++i)
+    for (size_t i = 0; i < count; ++i) {
         all.n += w[i].n;
+        all.bytes = std::max(all.bytes, w[i].bytes); // each matrix within the tiled limit
+    }
     if (all.n == 0)
         return REALM_OK;
     const GemmTile tile = gemm_tile(all, batch, false);

@@ -70,41 +70,59 @@ struct Raw<FMT_Q80> {
     uint4 d;     // the eight f16 block scales
 };
 
-// Rows past N read row N-1 (always resident); their results land in D
-// columns that are never stored.
-REALM_DEV void load_raw(Raw<FMT_Q4K> &r, const Mat &g, int row, int blk, int h)
+// Byte offsets of a lane's weights (its row, lane half h) in the weight
+// streams, fixed for the kernel.  A block adds a workgroup-uniform amount, so
+// every weight load is a scalar base plus this 32-bit offset (the host keeps
+// tiled weights under 4 GB).  Rows past N read row N-1 (always resident);
+// their results land in D columns that are never stored.
+struct LaneOff {
+    uint32_t o0, o1, o2;
+};
+template <int FMT>
+REALM_DEV LaneOff lane_off(const Mat &g, int row, int h)
 {
-    const int B = g.K >> 8;
-    const size_t U = (size_t)(g.K >> 6);
-    const uint8_t *qp = (const uint8_t *)g.w1 + (size_t)row * (U * 32) + (4 * blk + 2 * h) * 16;
-    r.q[0] = ldg16(qp);
-    r.q[1] = ldg16(qp + U * 16);
-    r.q[2] = ldg16(qp + 16);
-    r.q[3] = ldg16(qp + U * 16 + 16);
-    r.hd = ldg16((const uint8_t *)g.w0 + ((size_t)row * B + blk) * 16);
+    const uint32_t r = (uint32_t)row;
+    if constexpr (FMT == FMT_Q4K) // w0 header [row][blk] 16 B; w1 qs planes, K/2 B per row
+        return {r * (uint32_t)(g.K >> 8) * 16u, r * (uint32_t)(g.K >> 1) + 32u * h, 0u};
+    else if constexpr (FMT == FMT_Q6K) // w0 d [row][blk] 2 B; w1 sc 16 B; w2 planes, 3K/4 B
+        return {r * (uint32_t)(g.K >> 8) * 2u, r * (uint32_t)(g.K >> 8) * 16u + 8u * h,
+                r * (uint32_t)(g.K >> 6) * 48u + 32u * h};
+    else // Q8_0: w0 d [row][KX/32] 2 B; w1 q planes, KX B per row
+        return {r * (uint32_t)(g.KX >> 5) * 2u, r * (uint32_t)g.KX + 8u * h, 0u};
 }
-REALM_DEV void load_raw(Raw<FMT_Q6K> &r, const Mat &g, int row, int blk, int h)
+
+REALM_DEV void load_raw(Raw<FMT_Q4K> &r, const Mat &g, const LaneOff &o, int blk)
 {
-    const int B = g.K >> 8;
-    const size_t U = 4 * (size_t)B, bi = (size_t)row * B + blk;
-    const uint8_t *qp = (const uint8_t *)g.w2 + (size_t)row * (U * 48) + (4 * blk + 2 * h) * 16;
+    const size_t U = (size_t)(g.K >> 6);
+    const uint8_t *q0 = (const uint8_t *)g.w1 + (size_t)blk * 64, *q1 = q0 + U * 16;
+    r.q[0] = ldg16(q0 + o.o1);
+    r.q[1] = ldg16(q1 + o.o1);
+    r.q[2] = ldg16(q0 + o.o1 + 16);
+    r.q[3] = ldg16(q1 + o.o1 + 16);
+    r.hd = ldg16((const uint8_t *)g.w0 + (size_t)blk * 16 + o.o0);
+}
+REALM_DEV void load_raw(Raw<FMT_Q6K> &r, const Mat &g, const LaneOff &o, int blk)
+{
+    const size_t U = (size_t)(g.K >> 6);
+    const uint8_t *p0 = (const uint8_t *)g.w2 + (size_t)blk * 64, *p1 = p0 + U * 16,
+                  *p2 = p0 + U * 32;
 #pragma unroll
     for (int is = 0; is < 2; ++is) {
-        r.a[is] = ldg16(qp + 16 * is);
-        r.b[is] = ldg16(qp + U * 16 + 16 * is);
-        r.hq[is] = ldg16(qp + U * 32 + 16 * is);
+        r.a[is] = ldg16(p0 + o.o2 + 16 * is);
+        r.b[is] = ldg16(p1 + o.o2 + 16 * is);
+        r.hq[is] = ldg16(p2 + o.o2 + 16 * is);
     }
-    r.sc = ldg8((const int8_t *)g.w1 + bi * 16 + 8 * h);
-    r.d = *reinterpret_cast<const uint16_t *>((const uint8_t *)g.w0 + bi * 2);
+    r.sc = ldg8((const int8_t *)g.w1 + (size_t)blk * 16 + o.o1);
+    r.d = *reinterpret_cast<const uint16_t *>((const uint8_t *)g.w0 + (size_t)blk * 2 + o.o0);
 }
-REALM_DEV void load_raw(Raw<FMT_Q80> &r, const Mat &g, int row, int blk, int h)
+REALM_DEV void load_raw(Raw<FMT_Q80> &r, const Mat &g, const LaneOff &o, int blk)
 {
-    const size_t U = (size_t)(g.KX >> 6), B32 = (size_t)(g.KX >> 5);
-    const uint8_t *qrow = (const uint8_t *)g.w1 + (size_t)row * g.KX + 8 * h;
+    const size_t U = (size_t)(g.KX >> 6);
+    const uint8_t *q = (const uint8_t *)g.w1 + (size_t)blk * 64;
 #pragma unroll
     for (int s = 0; s < 16; ++s) // Q8_0 block 8 blk + s/2: unit 4 blk + s/4, plane s & 3
-        r.q[s] = ldg8(qrow + (s & 3) * (U * 16) + (4 * blk + (s >> 2)) * 16);
-    r.d = ldg16((const uint8_t *)g.w0 + ((size_t)row * B32 + 8 * blk) * 2);
+        r.q[s] = ldg8(q + (s & 3) * (U * 16) + (s >> 2) * 16 + o.o1);
+    r.d = ldg16((const uint8_t *)g.w0 + (size_t)blk * 16 + o.o0);
 }
 
 // Per-block decode of a Raw tile into B fragments of k-step s (0..15).
@@ -125,11 +143,11 @@ struct Dec<FMT_Q4K, WIDE> {
     REALM_MEMBER void init(const Raw<FMT_Q4K> &r, int h, int nan_fb)
     {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) { // the device layout stores high nibbles XOR 8
-            w[4 * i + 0] = r.q[i].x ^ 0x80808080u;
-            w[4 * i + 1] = r.q[i].y ^ 0x80808080u;
-            w[4 * i + 2] = r.q[i].z ^ 0x80808080u;
-            w[4 * i + 3] = r.q[i].w ^ 0x80808080u;
+        for (int i = 0; i < 4; ++i) { // as stored: high nibbles XOR 8 (undone in frag)
+            w[4 * i + 0] = r.q[i].x;
+            w[4 * i + 1] = r.q[i].y;
+            w[4 * i + 2] = r.q[i].z;
+            w[4 * i + 3] = r.q[i].w;
         }
         d = fix_scale(f16_bits_to_f32(r.hd.x), 0.00000006f, nan_fb);
         dm = fix_scale(f16_bits_to_f32(r.hd.x >> 16), 0.00000024f, nan_fb);
@@ -164,12 +182,14 @@ struct Dec<FMT_Q4K, WIDE> {
         const int sb = 2 * (s >> 3);
         // the masks live in VGPRs so that mask-and-merge is one v_and_or_b32
         // (VOP3 takes no literal, and one SGPR at most)
-        uint32_t mlo = 0x000F000Fu, mhi = 0x00F000F0u;
-        __asm__("" : "+v"(mlo), "+v"(mhi));
+        uint32_t mlo = 0x000F000Fu, mhi = 0x00F000F0u, chi = 0x64806480u;
+        __asm__("" : "+v"(mlo), "+v"(mhi), "+v"(chi));
         const uint32_t p0 = (x & mlo) | 0x64006400u; // bytes 0, 2 low nibbles
         const uint32_t p1 = (y & mlo) | 0x64006400u; // bytes 1, 3 low nibbles
-        const uint32_t p2 = (x & mhi) | 0x64006400u; // bytes 0, 2 high nibbles
-        const uint32_t p3 = (y & mhi) | 0x64006400u; // bytes 1, 3 high nibbles
+        // high nibbles: bitop3 table 0x6A is mhi ? x ^ chi : chi, i.e. the
+        // nibble with its stored XOR 8 undone (chi bit 7) merged into 0x6400
+        const uint32_t p2 = __builtin_amdgcn_bitop3_b32(x, mhi, chi, 0x6A); // bytes 0, 2
+        const uint32_t p3 = __builtin_amdgcn_bitop3_b32(y, mhi, chi, 0x6A); // bytes 1, 3
         return h8(u32(__builtin_elementwise_fma(h2(p0), sc2[sb], cc2[sb])),
                   u32(__builtin_elementwise_fma(h2(p1), sc2[sb], cc2[sb])),
                   u32(__builtin_elementwise_fma(h2(p2), sd2[sb + 1], cd2[sb + 1])),
@@ -407,12 +427,16 @@ REALM_DEV void gemm_tiled(const GemmArgs &g)
         else
             __builtin_amdgcn_s_waitcnt(0x0F70);
     };
+    LaneOff woff[TN];
+#pragma unroll
+    for (int a = 0; a < TN; ++a)
+        woff[a] = lane_off<FMT>(mat, min(row0 + 32 * a, mat.N - 1), h);
     // issue the loads of block blk (activations into buf, weights into w)
     auto issue = [&](int blk, uint8_t *buf, Raw<FMT> (&w)[TN]) {
         stage(buf, blk);
 #pragma unroll
         for (int a = 0; a < TN; ++a)
-            load_raw(w[a], mat, min(row0 + 32 * a, mat.N - 1), blk, h);
+            load_raw(w[a], mat, woff[a], blk);
         __builtin_amdgcn_sched_barrier(0);
     };
 
