@@ -683,6 +683,16 @@ int tiled_launch(const Weight *const *w, float *const *d_y, int count, const XPr
     return REALM_OK;
 }
 
+// Whether the LoRA shrink runs on the per-thread side stream beside the base
+// product (REALM_LORA_SIDE=1, for tuning) or on the caller's stream before it
+// (default: on MI355X the cross-queue fork and join of a graph cost more, 5-10
+// us each, than the overlap saves).
+bool lora_side()
+{
+    const char *e = getenv("REALM_LORA_SIDE");
+    return e && e[0] == '1';
+}
+
 int gemm_launch(const Weight &w, const XPrep &p, bool bf16, size_t M, const GemmTile &tile,
                 float *d_y, hipStream_t s, const LoraCall *lora)
 {
@@ -703,17 +713,25 @@ int gemm_launch(const Weight &w, const XPrep &p, bool bf16, size_t M, const Gemm
                         &iM,  &iK,  &iKX,  &irmax,       &pstride};
         std::string name = std::string("realm_lora_shrink_") + fmt_name(w.type) +
                            (bf16 ? "_bf16" : "_f32") + (tile.ord ? "_o1" : "");
-        // the shrink needs only the prepared activations: it runs on the side
-        // stream beside the base product and joins before the expand
-        hipStream_t side;
-        hipEvent_t fork, join;
-        CHECK(side_stream(&side, &fork, &join));
-        HIP_TRY(hipEventRecord(fork, s));
-        HIP_TRY(hipStreamWaitEvent(side, fork, 0));
+        // the shrink needs only the prepared activations (optionally on the
+        // side stream, joined again before the expand)
+        const bool use_side = lora_side();
+        hipStream_t side = s;
+        if (use_side) {
+            hipEvent_t fork, join;
+            CHECK(side_stream(&side, &fork, &join));
+            HIP_TRY(hipEventRecord(fork, s));
+            HIP_TRY(hipStreamWaitEvent(side, fork, 0));
+        }
         CHECK(launch(name,
                      dim3((unsigned)set.count, (unsigned)((set.rmax + 15) / 16), (unsigned)nparts),
                      dim3(256), 0, side, args));
-        HIP_TRY(hipEventRecord(join, side));
+        if (use_side) {
+            hipStream_t sd;
+            hipEvent_t fork, join;
+            CHECK(side_stream(&sd, &fork, &join));
+            HIP_TRY(hipEventRecord(join, sd));
+        }
     }
     if (tile.tiled) {
         const Weight *wp = &w;
@@ -749,10 +767,12 @@ int gemm_launch(const Weight &w, const XPrep &p, bool bf16, size_t M, const Gemm
         const AdapterSet &set = *lora->set;
         const void *table = set.table;
         const int32_t *ids = lora->d_ids;
-        hipStream_t side;
-        hipEvent_t fork, join;
-        CHECK(side_stream(&side, &fork, &join));
-        HIP_TRY(hipStreamWaitEvent(s, join, 0));
+        if (lora_side()) {
+            hipStream_t side;
+            hipEvent_t fork, join;
+            CHECK(side_stream(&side, &fork, &join));
+            HIP_TRY(hipStreamWaitEvent(s, join, 0));
+        }
         int iM = (int)M, iN = (int)w.n, rmax = (int)round_up(set.rmax, 8), np = nparts;
         void *eargs[] = {&u, (void *)&ids, (void *)&table, (void *)&d_y, &iM, &iN, &rmax, &np,
                          &pstride};

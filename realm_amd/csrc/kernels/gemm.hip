@@ -196,11 +196,21 @@ DEF_XPREP(q80, FMT_Q80)
 
 // --------------------------------------------------------- LoRA adapter table
 
+// Adapter factors are device allocations reached through pointers read from
+// the adapter table: cast to the global address space so that their loads
+// are global loads (a flat load also counts against the LDS/scalar counter
+// and makes every LDS wait wait for it too).
+typedef __attribute__((address_space(1))) const _Float16 gf16_t;
+typedef __attribute__((address_space(1))) const float gf32_t;
+typedef __attribute__((address_space(1))) const uint4 gu4_t;
+typedef __attribute__((address_space(1))) const uint2 gu2_t;
+typedef __attribute__((address_space(1))) const float4 gf4_t;
+
 REALM_DEV float lora_elem(const void *p, int dtype, size_t i)
 {
     if (dtype)
-        return (float)reinterpret_cast<const _Float16 *>(p)[i];
-    return reinterpret_cast<const float *>(p)[i];
+        return (float)((gf16_t *)p)[i];
+    return ((gf32_t *)p)[i];
 }
 
 // ------------------------------------------------------------- main kernel
@@ -649,16 +659,16 @@ REALM_DEV void shrink_body(const _Float16 *__restrict__ xh, const _Float16 *__re
         const int k0 = kwin<FMT, ORD>(4 * (s0 + min(s, ns - 1)) + c);
         float v[8];
         if (F16A) {
-            const _Float16 *src = reinterpret_cast<const _Float16 *>(e.a) + (size_t)jr * K + k0;
-            const uint2 r0 = ldg8(src), r1 = ldg8(src + GAP);
+            gf16_t *src = (gf16_t *)e.a + (size_t)jr * K + k0;
+            const uint2 r0 = *(gu2_t *)src, r1 = *(gu2_t *)(src + GAP);
             const half8_t hv = __builtin_bit_cast(half8_t, make_uint4(r0.x, r0.y, r1.x, r1.y));
 #pragma unroll
             for (int q = 0; q < 8; ++q)
                 v[q] = (float)hv[q];
         } else {
-            const float *src = reinterpret_cast<const float *>(e.a) + (size_t)jr * K + k0;
-            const float4 f0 = *reinterpret_cast<const float4 *>(src);
-            const float4 f1 = *reinterpret_cast<const float4 *>(src + GAP);
+            gf32_t *src = (gf32_t *)e.a + (size_t)jr * K + k0;
+            const float4 f0 = *(gf4_t *)src;
+            const float4 f1 = *(gf4_t *)(src + GAP);
             v[0] = f0.x; v[1] = f0.y; v[2] = f0.z; v[3] = f0.w;
             v[4] = f1.x; v[5] = f1.y; v[6] = f1.z; v[7] = f1.w;
         }
@@ -738,19 +748,17 @@ REALM_DEV void lora_shrink(const _Float16 *__restrict__ xh, const _Float16 *__re
 // adapter, so the read-modify-write of y has no conflicts.
 #define EXPAND_RT 8  // 64-row tiles per workgroup
 #define EXPAND_KK 2  // rank steps of 32 held in registers: ranks up to 64
-REALM_DEV void lora_expand(const float *__restrict__ u, const int *__restrict__ ids,
-                           const LoraEntry *__restrict__ table, float *__restrict__ y, int M,
+// One pass of rank steps kk0 .. kk0 + EXPAND_KK - 1 for this wave's 16 rows of
+// each of the workgroup's 8 row tiles.  FAST: f16 B with a rank that is a
+// multiple of 8, read 8 ranks per 16-byte load; otherwise f32 B (split into
+// f16 hi + lo) or f16 B element by element.  All loads of y and B are issued
+// before the u loads, and no loaded value is used before those are issued
+// too (a use right after a load makes the wave wait for it).
+template <bool FAST>
+REALM_DEV void expand_body(const float *__restrict__ u, const LoraEntry &e,
+                           const int *__restrict__ toks, int count, int tc, float *__restrict__ y,
                            int N, int rmax, int nparts, int pstride)
 {
-    __shared__ int toks[1024];
-    __shared__ int count;
-    __shared__ int wsum[4];
-    const int a = blockIdx.x;
-    adapter_tokens(ids, M, a, toks, &count, wsum);
-    const int tc = blockIdx.z * 16; // this workgroup's 16 tokens of the adapter
-    if (tc >= count)
-        return;
-    const LoraEntry e = table[a];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int r16 = lane & 15, c = lane >> 4;
     // loads read valid memory whatever the lane (rows past N read row N-1,
@@ -765,13 +773,39 @@ REALM_DEV void lora_expand(const float *__restrict__ u, const int *__restrict__ 
         const int tj = tc + 4 * c + v;
         toko[v] = toks[tj < count ? tj : 0];
     }
+    auto brow = [&](int rt) {
+        return min((int)(blockIdx.y * EXPAND_RT + rt) * 64 + wave * 16 + r16, N - 1);
+    };
     const int ksteps = (e.rank + 31) / 32;
     for (int kk0 = 0; kk0 < ksteps; kk0 += EXPAND_KK) {
-        // this wave's A fragments (u of its 16 tokens, 64 ranks): the sum of
-        // the shrink's K parts, in part order, loads before the first add
+        const int nkk = min(EXPAND_KK, ksteps - kk0); // rank steps of this pass (uniform)
+        float yv[EXPAND_RT][4];
+        half8_t bh[EXPAND_RT][EXPAND_KK], bl[EXPAND_RT][EXPAND_KK];
+#pragma unroll
+        for (int rt = 0; rt < EXPAND_RT; ++rt)
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+                yv[rt][v] = y[(size_t)toko[v] * N + brow(rt)];
+        if constexpr (FAST) {
+#pragma unroll
+            for (int rt = 0; rt < EXPAND_RT; ++rt)
+#pragma unroll
+                for (int q2 = 0; q2 < EXPAND_KK; ++q2) {
+                    const int j0 = 32 * (kk0 + q2) + 8 * c;
+                    gf16_t *src = (gf16_t *)e.b + (size_t)brow(rt) * e.rank + min(j0, e.rank - 8);
+                    bh[rt][q2] = __builtin_bit_cast(half8_t, *(gu4_t *)src);
+                }
+        }
+        // this wave's A fragments (u of its 16 tokens, up to 64 ranks): the
+        // sum of the shrink's K parts, in part order, loads before the first
+        // add; rank steps past the adapter's rank are skipped (uniform)
         half8_t ah[EXPAND_KK], al[EXPAND_KK];
 #pragma unroll
         for (int q2 = 0; q2 < EXPAND_KK; ++q2) {
+            ah[q2] = half8_t{};
+            al[q2] = half8_t{};
+            if (q2 >= nkk)
+                continue;
             const int j0 = 32 * (kk0 + q2) + 8 * c; // this lane's 8 ranks
             const int ju = min(j0, rmax - 8);
             float uv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
@@ -801,40 +835,27 @@ REALM_DEV void lora_expand(const float *__restrict__ u, const int *__restrict__ 
                 al[q2][q] = (_Float16)(vq - (float)h);
             }
         }
-        // the row tiles of this workgroup, 16 rows per wave each: all loads
-        // (y, B) of the 8 tiles first, then the MFMAs and stores
-        float yv[EXPAND_RT][4];
-        half8_t bh[EXPAND_RT][EXPAND_KK], bl[EXPAND_RT][EXPAND_KK];
 #pragma unroll
-        for (int rt = 0; rt < EXPAND_RT; ++rt) {
-            const int row = (blockIdx.y * EXPAND_RT + rt) * 64 + wave * 16 + r16;
-            const int rowc = min(row, N - 1);
-#pragma unroll
-            for (int v = 0; v < 4; ++v)
-                yv[rt][v] = y[(size_t)toko[v] * N + rowc];
+        for (int rt = 0; rt < EXPAND_RT; ++rt)
 #pragma unroll
             for (int q2 = 0; q2 < EXPAND_KK; ++q2) {
                 const int j0 = 32 * (kk0 + q2) + 8 * c;
-                if (e.dtype && (e.rank & 7) == 0) { // one aligned 16-byte load
-                    const half8_t bv = ld_h8(reinterpret_cast<const _Float16 *>(e.b) +
-                                             (size_t)rowc * e.rank + max(0, min(j0, e.rank - 8)));
+                if constexpr (FAST) { // ranks past the adapter's enter the sum as zero
 #pragma unroll
                     for (int q = 0; q < 8; ++q)
-                        bh[rt][q2][q] = j0 + q < e.rank ? bv[q] : (_Float16)0.f;
-                    bl[rt][q2] = half8_t{};
+                        bh[rt][q2][q] = j0 + q < e.rank ? bh[rt][q2][q] : (_Float16)0.f;
                 } else {
 #pragma unroll
                     for (int q = 0; q < 8; ++q) {
-                        const float vv = lora_elem(e.b, e.dtype,
-                                                   (size_t)rowc * e.rank + min(j0 + q, e.rank - 1));
+                        const float vv =
+                            lora_elem(e.b, e.dtype, (size_t)brow(rt) * e.rank + min(j0 + q, e.rank - 1));
                         const float vm = j0 + q < e.rank ? vv : 0.f;
-                        const _Float16 h = (_Float16)vm;
-                        bh[rt][q2][q] = h;
-                        bl[rt][q2][q] = (_Float16)(vm - (float)h);
+                        const _Float16 hq = (_Float16)vm;
+                        bh[rt][q2][q] = hq;
+                        bl[rt][q2][q] = (_Float16)(vm - (float)hq);
                     }
                 }
             }
-        }
 #pragma unroll
         for (int rt = 0; rt < EXPAND_RT; ++rt) {
             const int row = (blockIdx.y * EXPAND_RT + rt) * 64 + wave * 16 + r16;
@@ -843,7 +864,7 @@ REALM_DEV void lora_expand(const float *__restrict__ u, const int *__restrict__ 
             for (int q2 = 0; q2 < EXPAND_KK; ++q2) {
                 P = mfma(ah[q2], bh[rt][q2], P);
                 P = mfma(al[q2], bh[rt][q2], P);
-                if (!e.dtype)
+                if (!FAST && !e.dtype)
                     P = mfma(ah[q2], bl[rt][q2], P);
             }
             // D[token slot 4c+v][row r16]
@@ -855,6 +876,25 @@ REALM_DEV void lora_expand(const float *__restrict__ u, const int *__restrict__ 
             }
         }
     }
+}
+
+REALM_DEV void lora_expand(const float *__restrict__ u, const int *__restrict__ ids,
+                           const LoraEntry *__restrict__ table, float *__restrict__ y, int M,
+                           int N, int rmax, int nparts, int pstride)
+{
+    __shared__ int toks[1024];
+    __shared__ int count;
+    __shared__ int wsum[4];
+    const int a = blockIdx.x;
+    adapter_tokens(ids, M, a, toks, &count, wsum);
+    const int tc = blockIdx.z * 16; // this workgroup's 16 tokens of the adapter
+    if (tc >= count)
+        return;
+    const LoraEntry e = table[a];
+    if (e.dtype && (e.rank & 7) == 0)
+        expand_body<true>(u, e, toks, count, tc, y, N, rmax, nparts, pstride);
+    else
+        expand_body<false>(u, e, toks, count, tc, y, N, rmax, nparts, pstride);
 }
 
 extern "C" __global__ __launch_bounds__(256) void realm_lora_expand(
