@@ -685,21 +685,31 @@ REALM_DEV void shrink_body(const _Float16 *__restrict__ xh, const _Float16 *__re
         const int ti = tc + r16;
         const int tok = toks[ti < count ? ti : 0];
         floatx4 P = {0.f, 0.f, 0.f, 0.f};
-        half8_t ah[SHRINK_NS], al[SHRINK_NS];
+        // the chunk's steps in two halves: each half's activation loads are
+        // all in flight before its first MFMA (left alone, the scheduler
+        // interleaves them with the MFMAs, one memory round trip per two
+        // steps); halves keep the registers at two waves per SIMD
+        constexpr int HS = SHRINK_NS / 2;
 #pragma unroll
-        for (int s = 0; s < SHRINK_NS; ++s) {
-            const int sc = s0 + min(s, ns - 1);
-            ah[s] = ld_h8(xh + (size_t)tok * KX + 32 * sc + 8 * c);
-            if (LO)
-                al[s] = ld_h8(xl + (size_t)tok * KX + 32 * sc + 8 * c);
-        }
+        for (int hf = 0; hf < 2; ++hf) {
+            half8_t ah[HS], al[HS];
 #pragma unroll
-        for (int s = 0; s < SHRINK_NS; ++s) {
-            P = mfma(ah[s], bh[s], P);
-            if (!F16A)
-                P = mfma(ah[s], bl[s], P);
-            if (LO)
-                P = mfma(al[s], bh[s], P);
+            for (int i = 0; i < HS; ++i) {
+                const int sc = s0 + min(hf * HS + i, ns - 1);
+                ah[i] = ld_h8(xh + (size_t)tok * KX + 32 * sc + 8 * c);
+                if (LO)
+                    al[i] = ld_h8(xl + (size_t)tok * KX + 32 * sc + 8 * c);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < HS; ++i) {
+                const int s = hf * HS + i;
+                P = mfma(ah[i], bh[s], P);
+                if (!F16A)
+                    P = mfma(ah[i], bl[s], P);
+                if (LO)
+                    P = mfma(al[i], bh[s], P);
+            }
         }
         float ts[4];
 #pragma unroll
