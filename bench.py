@@ -259,7 +259,8 @@ def config4(be, stream: int, reps: int) -> dict:
     than the 256 MB MALL, so every replay streams the weights from HBM).
     decode: 32 tokens (f32 activations), the base set (QKV grouped, Wo,
     gate/up grouped, W_down) against the same set with 8 rank-16 adapters on
-    q/k/v/o (Zipf(1.1) ids over 8, 10% without adapter).  prefill: 1024
+    q/k/v/o (Zipf(1.1) ids over 8, 10% without adapter; q/k/v in one grouped
+    multi-LoRA call).  prefill: 1024
     tokens, bf16 activations, the seven products one after another."""
     g = synth.rng(4)
     hs = {name: be.register_weights(t, synth.blocks(g, t, n, k), n, k)
@@ -291,9 +292,12 @@ def config4(be, stream: int, reps: int) -> dict:
         be.matmul_dev(hs["w_down"], xd[28672].ptr, m_dec, y["w_down"].ptr, stream=stream)
 
     def with_lora():
-        for name in lora_on:
-            be.multi_lora_matmul_dev(hs[name], sets[name], xd[8192].ptr, m_dec, d_ids.ptr,
-                                     y[name].ptr, stream=stream)
+        qkv = ("wq", "wk", "wv")
+        be.multi_lora_matmul_group_dev([hs[n] for n in qkv], [sets[n] for n in qkv],
+                                       xd[8192].ptr, m_dec, d_ids.ptr, [y[n].ptr for n in qkv],
+                                       stream=stream)
+        be.multi_lora_matmul_dev(hs["wo"], sets["wo"], xd[8192].ptr, m_dec, d_ids.ptr,
+                                 y["wo"].ptr, stream=stream)
         be.matmul_group_dev([hs["w_gate"], hs["w_up"]], xd[8192].ptr, m_dec,
                             [y["w_gate"].ptr, y["w_up"].ptr], stream=stream)
         be.matmul_dev(hs["w_down"], xd[28672].ptr, m_dec, y["w_down"].ptr, stream=stream)

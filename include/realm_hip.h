@@ -216,6 +216,18 @@ int realm_hip_multi_lora_matmul_dev(uint64_t weight_handle, uint64_t set_handle,
                                     const int32_t *d_adapter_ids, float *d_out,
                                     void *stream);
 
+/* Grouped form for 1..4 projections of one format and K that share the input
+ * and the token adapter ids (q/k/v of realm_forward_layer,
+ * crates/realm-runtime/src/memory64_host.rs:2078-2308, with LoRA applied per
+ * projection as at :625-680): d_outs[i] = multi-LoRA matmul of weight i with
+ * adapter set i.  The input is prepared once and the base products run as
+ * one launch.  Device pointers, asynchronous on `stream`. */
+int realm_hip_multi_lora_matmul_group_dev(const uint64_t *weight_handles,
+                                          const uint64_t *set_handles, size_t count,
+                                          const float *d_input, size_t batch,
+                                          const int32_t *d_adapter_ids,
+                                          float *const *d_outs, void *stream);
+
 /* -------------------------------------------------------- HIP graphs */
 
 /* Capture the device-pointer calls issued on `stream` (not NULL) between

@@ -53,6 +53,9 @@ SIGNATURES = {
                                             c_void_p]),
     "realm_hip_multi_lora_matmul_dev": (c_int, [c_uint64, c_uint64, c_void_p, c_size_t,
                                                 c_void_p, c_void_p, c_void_p]),
+    "realm_hip_multi_lora_matmul_group_dev": (c_int, [POINTER(c_uint64), POINTER(c_uint64),
+                                                      c_size_t, c_void_p, c_size_t, c_void_p,
+                                                      POINTER(c_void_p), c_void_p]),
     "realm_hip_graph_begin": (c_int, [c_void_p]),
     "realm_hip_graph_end": (c_int, [c_void_p, POINTER(c_uint64)]),
     "realm_hip_graph_launch": (c_int, [c_uint64, c_void_p]),

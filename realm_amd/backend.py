@@ -303,6 +303,18 @@ class HipGpuBackend:
         self._check(self.lib.realm_hip_multi_lora_matmul_dev(
             wh, sh, c_void_p(d_x), batch, c_void_p(d_ids), c_void_p(d_y), c_void_p(stream or 0)))
 
+    def multi_lora_matmul_group_dev(self, whs, shs, d_x: int, batch: int, d_ids: int, d_ys,
+                                    stream=None) -> None:
+        """Projections sharing x and the token adapter ids (e.g. q/k/v), each
+        with its own adapter set: one activation prep, one base launch."""
+        if len(whs) != len(shs) or len(whs) != len(d_ys):
+            raise InvalidShape(INVALID_ARGUMENT, "one adapter set and output per weight")
+        ws = (c_uint64 * len(whs))(*whs)
+        ss = (c_uint64 * len(shs))(*shs)
+        ys = (c_void_p * len(d_ys))(*d_ys)
+        self._check(self.lib.realm_hip_multi_lora_matmul_group_dev(
+            ws, ss, len(whs), c_void_p(d_x), batch, c_void_p(d_ids), ys, c_void_p(stream or 0)))
+
 
 __all__ = ["HipGpuBackend", "RealmError", "InvalidShape", "BackendError", "DeviceBuffer",
            "DTYPE_F32", "DTYPE_F16"]

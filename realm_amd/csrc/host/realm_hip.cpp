@@ -693,45 +693,80 @@ bool lora_side()
     return e && e[0] == '1';
 }
 
+// LoRA shrink output: one part per 512 positions of K (summed by the
+// expand), [part][token][rmax rounded to 8] f32 per matrix
+struct LoraU {
+    int nparts, pstride;
+    size_t bytes() const { return (size_t)nparts * pstride * 4; }
+};
+LoraU lora_u(const Weight &w, const AdapterSet &set, const XPrep &p)
+{
+    return {(int)((w.kx + 511) / 512), (int)(p.Mp * round_up(set.rmax, 8))};
+}
+
+// u = A_a x for every token's adapter a, from the prepared activations
+// (optionally on the side stream, joined again before the expand).
+int lora_shrink_launch(const Weight &w, const LoraCall &lc, const XPrep &p, bool bf16, size_t M,
+                       const GemmTile &tile, void *u, hipStream_t s)
+{
+    const AdapterSet &set = *lc.set;
+    const LoraU lu = lora_u(w, set, p);
+    const void *table = set.table;
+    const int32_t *ids = lc.d_ids;
+    void *xh = p.xh, *xl = p.xl, *ts = p.ts;
+    int iM = (int)M, iK = (int)w.k, iKX = (int)w.kx, irmax = (int)round_up(set.rmax, 8),
+        pstride = lu.pstride;
+    void *args[] = {&xh, &xl, &ts, (void *)&ids, (void *)&table, &u,
+                    &iM, &iK, &iKX, &irmax, &pstride};
+    const std::string name = std::string("realm_lora_shrink_") + fmt_name(w.type) +
+                             (bf16 ? "_bf16" : "_f32") + (tile.ord ? "_o1" : "");
+    const bool use_side = lora_side();
+    hipStream_t side = s;
+    hipEvent_t fork = nullptr, join = nullptr;
+    if (use_side) {
+        CHECK(side_stream(&side, &fork, &join));
+        HIP_TRY(hipEventRecord(fork, s));
+        HIP_TRY(hipStreamWaitEvent(side, fork, 0));
+    }
+    CHECK(launch(name,
+                 dim3((unsigned)set.count, (unsigned)((set.rmax + 15) / 16), (unsigned)lu.nparts),
+                 dim3(256), 0, side, args));
+    if (use_side)
+        HIP_TRY(hipEventRecord(join, side));
+    return REALM_OK;
+}
+
+// y += scale_a B_a u per token, one workgroup per (adapter, 512 rows, 16
+// tokens); y already holds the base product.
+int lora_expand_launch(const Weight &w, const LoraCall &lc, const XPrep &p, size_t M, void *u,
+                       float *d_y, hipStream_t s)
+{
+    const AdapterSet &set = *lc.set;
+    const LoraU lu = lora_u(w, set, p);
+    const void *table = set.table;
+    const int32_t *ids = lc.d_ids;
+    if (lora_side()) {
+        hipStream_t side;
+        hipEvent_t fork, join;
+        CHECK(side_stream(&side, &fork, &join));
+        HIP_TRY(hipStreamWaitEvent(s, join, 0));
+    }
+    int iM = (int)M, iN = (int)w.n, rmax = (int)round_up(set.rmax, 8), np = lu.nparts,
+        pstride = lu.pstride;
+    void *eargs[] = {&u, (void *)&ids, (void *)&table, (void *)&d_y, &iM, &iN, &rmax, &np,
+                     &pstride};
+    return launch("realm_lora_expand",
+                  dim3((unsigned)set.count, (unsigned)((w.n + 511) / 512), (unsigned)((M + 15) / 16)),
+                  dim3(256), 0, s, eargs);
+}
+
 int gemm_launch(const Weight &w, const XPrep &p, bool bf16, size_t M, const GemmTile &tile,
                 float *d_y, hipStream_t s, const LoraCall *lora)
 {
     void *u = nullptr;
-    // shrink output: one part per 512 positions of K (summed by the expand)
-    const int nparts = (int)((w.kx + 511) / 512);
-    int pstride = 0;
     if (lora) {
-        const AdapterSet &set = *lora->set;
-        const int rmax = (int)round_up(set.rmax, 8);
-        pstride = (int)(p.Mp * rmax);
-        CHECK(ws_get(s, WS_U, (size_t)nparts * pstride * 4, &u));
-        const void *table = set.table;
-        const int32_t *ids = lora->d_ids;
-        void *xh = p.xh, *xl = p.xl, *ts = p.ts;
-        int iM = (int)M, iK = (int)w.k, iKX = (int)w.kx, irmax = rmax;
-        void *args[] = {&xh,  &xl,  &ts,   (void *)&ids, (void *)&table, &u,
-                        &iM,  &iK,  &iKX,  &irmax,       &pstride};
-        std::string name = std::string("realm_lora_shrink_") + fmt_name(w.type) +
-                           (bf16 ? "_bf16" : "_f32") + (tile.ord ? "_o1" : "");
-        // the shrink needs only the prepared activations (optionally on the
-        // side stream, joined again before the expand)
-        const bool use_side = lora_side();
-        hipStream_t side = s;
-        if (use_side) {
-            hipEvent_t fork, join;
-            CHECK(side_stream(&side, &fork, &join));
-            HIP_TRY(hipEventRecord(fork, s));
-            HIP_TRY(hipStreamWaitEvent(side, fork, 0));
-        }
-        CHECK(launch(name,
-                     dim3((unsigned)set.count, (unsigned)((set.rmax + 15) / 16), (unsigned)nparts),
-                     dim3(256), 0, side, args));
-        if (use_side) {
-            hipStream_t sd;
-            hipEvent_t fork, join;
-            CHECK(side_stream(&sd, &fork, &join));
-            HIP_TRY(hipEventRecord(join, sd));
-        }
+        CHECK(ws_get(s, WS_U, lora_u(w, *lora->set, p).bytes(), &u));
+        CHECK(lora_shrink_launch(w, *lora, p, bf16, M, tile, u, s));
     }
     if (tile.tiled) {
         const Weight *wp = &w;
@@ -762,25 +797,8 @@ int gemm_launch(const Weight &w, const XPrep &p, bool bf16, size_t M, const Gemm
                         (unsigned)((p.Mp + tile.toks_per_wg - 1) / tile.toks_per_wg));
         CHECK(launch(name, grid, dim3(tile.threads), 0, s, args));
     }
-    if (lora) {
-        // y += scale_a B_a u per token, one workgroup per (adapter, 64 rows)
-        const AdapterSet &set = *lora->set;
-        const void *table = set.table;
-        const int32_t *ids = lora->d_ids;
-        if (lora_side()) {
-            hipStream_t side;
-            hipEvent_t fork, join;
-            CHECK(side_stream(&side, &fork, &join));
-            HIP_TRY(hipStreamWaitEvent(s, join, 0));
-        }
-        int iM = (int)M, iN = (int)w.n, rmax = (int)round_up(set.rmax, 8), np = nparts;
-        void *eargs[] = {&u, (void *)&ids, (void *)&table, (void *)&d_y, &iM, &iN, &rmax, &np,
-                         &pstride};
-        CHECK(launch("realm_lora_expand",
-                     dim3((unsigned)set.count, (unsigned)((w.n + 511) / 512),
-                          (unsigned)((M + 15) / 16)),
-                     dim3(256), 0, s, eargs));
-    }
+    if (lora)
+        CHECK(lora_expand_launch(w, *lora, p, M, u, d_y, s));
     return REALM_OK;
 }
 
@@ -1400,6 +1418,64 @@ REALM_API int realm_hip_multi_lora_matmul_dev(uint64_t weight_handle, uint64_t s
     CHECK(pick_stream(stream, &s));
     LoraCall lc{&set, d_adapter_ids};
     return run_gemm(w, d_input, false, batch, d_out, s, &lc);
+}
+
+REALM_API int realm_hip_multi_lora_matmul_group_dev(const uint64_t *weight_handles,
+                                                    const uint64_t *set_handles, size_t count,
+                                                    const float *d_input, size_t batch,
+                                                    const int32_t *d_adapter_ids,
+                                                    float *const *d_outs, void *stream)
+{
+    if (!weight_handles || !set_handles || !d_outs || count == 0 ||
+        count > REALM_GEMM_MAX_SEGS)
+        return fail(REALM_INVALID_ARGUMENT, "group needs 1..4 weight and adapter-set handles");
+    Weight w[REALM_GEMM_MAX_SEGS];
+    AdapterSet set[REALM_GEMM_MAX_SEGS];
+    for (size_t i = 0; i < count; ++i) {
+        CHECK(lora_lookup(weight_handles[i], set_handles[i], batch, &w[i], &set[i]));
+        if (w[i].type != w[0].type || w[i].k != w[0].k)
+            return fail(REALM_INVALID_ARGUMENT, "grouped weights must share format and K");
+    }
+    CHECK(ensure_init());
+    hipStream_t s;
+    CHECK(pick_stream(stream, &s));
+    if (batch == 0)
+        return REALM_OK;
+    Weight all = w[0];
+    all.n = 0;
+    for (size_t i = 0; i < count; ++i) {
+        all.n += w[i].n;
+        all.bytes = std::max(all.bytes, w[i].bytes);
+    }
+    const GemmTile tile = gemm_tile(all, batch, false);
+    XPrep p;
+    CHECK(prep_x(w[0], d_input, false, batch, tile, s, &p));
+    LoraCall lc[REALM_GEMM_MAX_SEGS];
+    for (size_t i = 0; i < count; ++i)
+        lc[i] = LoraCall{&set[i], d_adapter_ids};
+    if (!tile.tiled) { // per matrix: shrink, base product, expand
+        for (size_t i = 0; i < count; ++i)
+            CHECK(gemm_launch(w[i], p, false, batch, tile, d_outs[i], s, &lc[i]));
+        return REALM_OK;
+    }
+    // the shrinks (each into its own slice of the u workspace), one launch of
+    // the base products, then the expands
+    size_t uoff[REALM_GEMM_MAX_SEGS], ubytes = 0;
+    for (size_t i = 0; i < count; ++i) {
+        uoff[i] = ubytes;
+        ubytes += align256(lora_u(w[i], set[i], p).bytes());
+    }
+    void *u = nullptr;
+    CHECK(ws_get(s, WS_U, ubytes, &u));
+    for (size_t i = 0; i < count; ++i)
+        CHECK(lora_shrink_launch(w[i], lc[i], p, false, batch, tile, (uint8_t *)u + uoff[i], s));
+    const Weight *wp[REALM_GEMM_MAX_SEGS];
+    for (size_t i = 0; i < count; ++i)
+        wp[i] = &w[i];
+    CHECK(tiled_launch(wp, d_outs, (int)count, p, false, batch, tile, s));
+    for (size_t i = 0; i < count; ++i)
+        CHECK(lora_expand_launch(w[i], lc[i], p, batch, (uint8_t *)u + uoff[i], d_outs[i], s));
+    return REALM_OK;
 }
 
 REALM_API int realm_hip_multi_lora_matmul(uint64_t weight_handle, uint64_t set_handle,

@@ -457,6 +457,56 @@ def test_multi_lora_small(backend, oracle, t, dtype, shape):
     assert np.array_equal(got[none], base[none]) or rel_l2(got[none], base[none]) < 1e-6
 
 
+@pytest.mark.parametrize("t", [GGML_Q4_K, GGML_Q6_K])
+@pytest.mark.parametrize("m", [4, 37])
+def test_multi_lora_group(backend, oracle, t, m):
+    """q/k/v-like projections with their own adapter sets in one grouped
+    call (ragged rows; ranks 3 to 100; f16 and f32 factors), against the
+    oracle per projection: per-matrix launches at 4 tokens, one tiled base
+    launch for the group at 37."""
+    g = synth.rng(zlib.crc32(f"lgroup{t}{m}".encode()) % 100000)
+    k = 1536
+    specs = [(300, (8, 16, 3), np.float16), (128, (64,), np.float32), (77, (100, 8), np.float16)]
+    x = synth.activations(g, m, k)
+    ids = synth.adapter_ids(g, m, 3)
+    ids[1] = 7  # unknown slot where a projection has fewer adapters: base only
+    whs, shs, lhs, refs, ns = [], [], [], [], []
+    dx = backend.alloc(x.nbytes).upload(x)
+    d_ids = backend.alloc(ids.nbytes).upload(ids)
+    dys = []
+    try:
+        for n, ranks, dt in specs:
+            blocks = synth.blocks(g, t, n, k)
+            adapters, hs = [], []
+            for r in ranks:
+                a, b = synth.lora_adapter(g, r, k, n)
+                a, b = a.astype(dt), b.astype(dt)
+                adapters.append((a, b, r, 16.0))
+                hs.append(backend.lora_register(a, b, r, 16.0, k, n))
+            lhs += hs
+            whs.append(backend.register_weights(t, blocks, n, k))
+            shs.append(backend.lora_set_create(hs))
+            refs.append(_oracle_lora(oracle, t, blocks, x, ids, adapters, n, k))
+            ns.append(n)
+            dys.append(backend.alloc(m * n * 4))
+        backend.multi_lora_matmul_group_dev(whs, shs, dx.ptr, m, d_ids.ptr, [d.ptr for d in dys])
+        backend.synchronize()
+        got = [d.download(np.float32, m * n).reshape(m, n) for d, n in zip(dys, ns)]
+    finally:
+        for sh in shs:
+            backend.lora_set_release(sh)
+        for h in lhs:
+            backend.lora_release(h)
+        for wh in whs:
+            backend.release_weights(wh)
+        for d in [dx, d_ids] + dys:
+            d.close()
+    for i, (gi, ref) in enumerate(zip(got, refs)):
+        err = rel_l2(gi, ref)
+        print(f"lora group {NAMES[t]} m={m} proj {i} rel_l2={err:.3e}")
+        assert err < REL_TOL
+
+
 def test_multi_lora_config3(backend, oracle):
     """16 tenants, ranks from {8,16,64}, 64 tokens with Zipf(1.1) ids and 10%
     no-adapter, on a shared Q4_K 4096 x 4096 projection."""
