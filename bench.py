@@ -164,8 +164,10 @@ def decode_roofline(be, model: Model7B, stream: int, reps: int) -> dict:
 def lora_overhead(be, stream: int, reps: int) -> dict:
     """Config 3: q_proj and v_proj (Q4_K 4096x4096) for 64 tokens, 16 adapters
     with ranks from {8,16,64}, Zipf(1.1) tenant ids, 10% without adapter.
-    warm: the same weights and adapters every replay; cold: 8 rotated copies
-    (base + adapters), 8 x 47 MB, so the adapters are re-read from HBM."""
+    q and v share the input, so base and multi-LoRA products run as grouped
+    calls; warm: the same weights and adapters every replay; cold: 8 rotated
+    copies (base + adapters), 8 x 47 MB, so the adapters are re-read from
+    HBM; warm_per_projection: one call per projection instead."""
     g = synth.rng(3)
     n = k = 4096
     m = 64
@@ -188,19 +190,30 @@ def lora_overhead(be, stream: int, reps: int) -> dict:
         weights.append(ws)
         sets.append(ss)
 
+    # q and v share their input: grouped calls (one activation prep, one
+    # base launch) for the base and for the multi-LoRA product
     def base(c):
+        be.matmul_group_dev(weights[c], x.ptr, m, [yy.ptr for yy in y], stream=stream)
+
+    def lora(c):
+        be.multi_lora_matmul_group_dev(weights[c], sets[c], x.ptr, m, d_ids.ptr,
+                                       [yy.ptr for yy in y], stream=stream)
+
+    # one call per projection
+    def base1(c):
         for p in range(2):
             be.matmul_dev(weights[c][p], x.ptr, m, y[p].ptr, stream=stream)
 
-    def lora(c):
+    def lora1(c):
         for p in range(2):
             be.multi_lora_matmul_dev(weights[c][p], sets[c][p], x.ptr, m, d_ids.ptr, y[p].ptr,
                                      stream=stream)
 
     res = {}
-    for mode, cs in (("warm", [0]), ("cold", list(range(copies)))):
-        gb = capture(be, stream, lambda: [base(c) for c in cs])
-        gl = capture(be, stream, lambda: [lora(c) for c in cs])
+    for mode, cs, fb, fl in (("warm", [0], base, lora), ("cold", list(range(copies)), base, lora),
+                             ("warm_per_projection", [0], base1, lora1)):
+        gb = capture(be, stream, lambda: [fb(c) for c in cs])
+        gl = capture(be, stream, lambda: [fl(c) for c in cs])
         time_graph(be, gb, stream, 5)
         time_graph(be, gl, stream, 5)
         tb = time_graph(be, gb, stream, reps) / len(cs)
