@@ -354,6 +354,31 @@ def config4(be, stream: int, reps: int) -> dict:
     return res
 
 
+def dense(be, stream: int, reps: int) -> dict:
+    """The dense f32 product behind candle_matmul on device pointers:
+    4096 x 4096 x 4096 (both B layouts) and a decode-shaped 32 x 4096 x 4096;
+    2mnk flops against the 157.3 TFLOP/s dense f32 MFMA peak."""
+    g = synth.rng(5)
+    out = {}
+    for name, m, k, n, tr in (("4096^3", 4096, 4096, 4096, False),
+                              ("4096^3_bt", 4096, 4096, 4096, True),
+                              ("32x4096x4096_bt", 32, 4096, 4096, True)):
+        a = be.alloc(m * k * 4).upload(g.standard_normal((m, k), dtype=np.float32))
+        b = be.alloc(k * n * 4).upload(g.standard_normal((k, n), dtype=np.float32))
+        c = be.alloc(m * n * 4)
+        gr = capture(be, stream, lambda: be.dense_matmul_dev(a.ptr, b.ptr, c.ptr, m, k, n,
+                                                             transposed=tr, stream=stream))
+        time_graph(be, gr, stream, 2)
+        ms = time_graph(be, gr, stream, reps)
+        be.graph_release(gr)
+        tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+        out[name] = {"us": round(ms * 1e3, 1), "tflops": round(tf, 1),
+                     "frac_f32_mfma_peak": round(tf / 157.3, 4)}
+        for d in (a, b, c):
+            d.close()
+    return out
+
+
 def cpu_baseline(seconds: float) -> tuple[dict, dict]:
     """The oracle's C restatement of realm-compute-cpu on this host's cores:
     Q4_K 4096x4096 matvec (batch 1), dequantize-row-then-dot on all cores, and
@@ -397,7 +422,7 @@ def main() -> int:
     ap.add_argument("--traffic-probe", action="store_true",
                     help="no timing: one 256 MiB device copy (the counter reference) then "
                          "one gate/up GEMV launch per layer, for rocprofv3 --pmc runs")
-    ap.add_argument("--extra-only", choices=("batched", "lora", "prefill", "config4"),
+    ap.add_argument("--extra-only", choices=("batched", "lora", "prefill", "config4", "dense"),
                     help="run one of the extra measurements alone (for kernel profiles) and "
                          "print its result; no decode step, no JSON line")
     args = ap.parse_args()
@@ -417,6 +442,9 @@ def main() -> int:
         return 0
     if args.extra_only == "config4":
         log(f"config4: {config4(be, stream, 10)}")
+        return 0
+    if args.extra_only == "dense":
+        log(f"dense: {dense(be, stream, 10)}")
         return 0
     log(f"registering {args.layers} LLaMA-7B layers")
     model = Model7B(be, args.layers, 16)
@@ -483,6 +511,8 @@ def main() -> int:
         log(f"prefill: {extra['prefill_config2']}")
         extra["config4_70b_layer"] = config4(be, stream, 10)
         log(f"config4: {extra['config4_70b_layer']}")
+        extra["dense_f32"] = dense(be, stream, 10)
+        log(f"dense: {extra['dense_f32']}")
         cpu, cpu1 = cpu_baseline(args.cpu_seconds)
         extra["cpu_baseline_1thread"] = cpu1
         log(f"cpu baseline: {cpu}")

@@ -91,6 +91,14 @@ int realm_hip_set_nan_fallback(int enable);
 int realm_hip_matmul(const float *a, size_t a_len, const float *b, size_t b_len,
                      uint32_t m, uint32_t k, uint32_t n, float *out);
 
+/* The same product on device pointers, asynchronous on `stream` (NULL = this
+ * thread's stream), for callers whose operands already live on the device:
+ * C [m,n] = A [m,k] @ B, B [k,n] row-major, or B^T with B [n,k] when
+ * b_transposed is non-zero (candle_matmul_transposed,
+ * memory64_host.rs:971-1086).  f32 products and sums on MFMA. */
+int realm_hip_matmul_dev(const float *d_a, const float *d_b, float *d_c, uint32_t m,
+                         uint32_t k, uint32_t n, int b_transposed, void *stream);
+
 /* GpuBackendTrait::fused_dequant_matmul_q4k / _q6k / _q80
  * (gpu_backend_trait.rs:22-29, 42-49, 122-129).  Validation as in the
  * reference backends (crates/realm-compute-gpu/src/candle_backend.rs:448-464,

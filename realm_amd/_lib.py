@@ -20,6 +20,8 @@ SIGNATURES = {
     "realm_hip_set_nan_fallback": (c_int, [c_int]),
     "realm_hip_matmul": (c_int, [c_void_p, c_size_t, c_void_p, c_size_t, c_uint32, c_uint32,
                                  c_uint32, c_void_p]),
+    "realm_hip_matmul_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32,
+                                     c_int, c_void_p]),
     "realm_hip_fused_dequant_matmul_q4k": (c_int, [c_void_p, c_size_t, c_void_p, c_size_t,
                                                    c_size_t, c_size_t, c_size_t, c_void_p]),
     "realm_hip_fused_dequant_matmul_q6k": (c_int, [c_void_p, c_size_t, c_void_p, c_size_t,

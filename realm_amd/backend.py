@@ -115,6 +115,13 @@ class HipGpuBackend:
                                               _ptr(out)))
         return out
 
+    def dense_matmul_dev(self, d_a: int, d_b: int, d_c: int, m: int, k: int, n: int,
+                         transposed: bool = False, stream=None) -> None:
+        """C = A @ B (B [k,n]) or A @ B^T (B [n,k]) on device pointers."""
+        self._check(self.lib.realm_hip_matmul_dev(c_void_p(d_a), c_void_p(d_b), c_void_p(d_c),
+                                                  m, k, n, 1 if transposed else 0,
+                                                  c_void_p(stream or 0)))
+
     def _fused(self, ggml_type: int, blocks, input, batch_size: int, n: int, k: int):
         blocks = np.ascontiguousarray(blocks)
         if blocks.dtype != DTYPES[ggml_type]:

@@ -892,6 +892,37 @@ int fused_host(int type, const void *blocks, size_t n_blocks, const float *input
     return REALM_OK;
 }
 
+// Dense f32 C = A @ B (or A @ B^T, bt = 1) on device pointers; m, n, k >= 1
+// and below 2^31.  One workgroup per 128 x 128 tile of C.
+int dense_launch(const float *da, const float *db, float *dc, size_t m, size_t k, size_t n,
+                 int bt, hipStream_t s)
+{
+    // K splits (parts summed in split order) until the launch has 256
+    // workgroups, keeping at least 256 positions of K per split
+    const size_t tiles = ((n + 127) / 128) * ((m + 127) / 128);
+    int ks = 1;
+    while (tiles * ks < 256 && k / (2 * (size_t)ks) >= 256 && ks < 32)
+        ks *= 2;
+    if (const char *env = getenv("REALM_DENSE_KS")) // tuning override
+        ks = std::max(1, std::min(64, atoi(env)));
+    ks = (int)std::min<size_t>((size_t)ks, k); // every split owns at least one k
+    void *part = nullptr;
+    if (ks > 1)
+        CHECK(ws_get(s, WS_PART, (size_t)ks * m * n * sizeof(float), &part));
+    int M = (int)m, N = (int)n, K = (int)k;
+    void *args[] = {(void *)&da, (void *)&db, (void *)&dc, &M, &N, &K, &bt, &ks, &part};
+    CHECK(launch("realm_dense_f32",
+                 dim3((unsigned)((n + 127) / 128), (unsigned)((m + 127) / 128), (unsigned)ks),
+                 dim3(256), 0, s, args));
+    if (ks > 1) {
+        long long total = (long long)(m * n);
+        void *rargs[] = {&part, (void *)&dc, &total, &ks};
+        CHECK(launch("realm_dense_reduce", dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+                     rargs));
+    }
+    return REALM_OK;
+}
+
 // Dense f32 C = A @ B (or A @ B^T) with host pointers.
 int dense_host(const float *a, const float *b, float *c, size_t m, size_t k, size_t n, int bt)
 {
@@ -912,10 +943,7 @@ int dense_host(const float *a, const float *b, float *c, size_t m, size_t k, siz
     CHECK(ws_get(s, WS_Y, m * n * 4, &dc));
     HIP_TRY(hipMemcpyAsync(da, a, m * k * 4, hipMemcpyHostToDevice, s));
     HIP_TRY(hipMemcpyAsync(db, b, k * n * 4, hipMemcpyHostToDevice, s));
-    int M = (int)m, N = (int)n, K = (int)k;
-    void *args[] = {&da, &db, &dc, &M, &N, &K, &bt};
-    CHECK(launch("realm_dense_f32", dim3((unsigned)((n + 63) / 64), (unsigned)((m + 63) / 64)),
-                 dim3(256), 0, s, args));
+    CHECK(dense_launch((const float *)da, (const float *)db, (float *)dc, m, k, n, bt, s));
     HIP_TRY(hipMemcpyAsync(c, dc, m * n * 4, hipMemcpyDeviceToHost, s));
     HIP_TRY(hipStreamSynchronize(s));
     return REALM_OK;
@@ -980,6 +1008,25 @@ REALM_API int realm_hip_matmul(const float *a, size_t a_len, const float *b, siz
     if (a_len != (size_t)m * k || b_len != (size_t)k * n)
         return fail(REALM_GENERIC_FAILURE, "Candle GPU tensor creation failed: shape mismatch");
     return dense_host(a, b, out, m, k, n, 0);
+}
+
+REALM_API int realm_hip_matmul_dev(const float *d_a, const float *d_b, float *d_c, uint32_t m,
+                                   uint32_t k, uint32_t n, int b_transposed, void *stream)
+{
+    if ((m && k && !d_a) || (k && n && !d_b) || (m && n && !d_c))
+        return fail(REALM_INVALID_ARGUMENT, "null pointer argument");
+    CHECK(ensure_init());
+    hipStream_t s;
+    CHECK(pick_stream(stream, &s));
+    if (m == 0 || n == 0)
+        return REALM_OK;
+    if (m > (uint32_t)INT32_MAX || n > (uint32_t)INT32_MAX || k > (uint32_t)INT32_MAX)
+        return fail(REALM_INVALID_ARGUMENT, "dimension exceeds 2^31-1");
+    if (k == 0) {
+        HIP_TRY(hipMemsetAsync(d_c, 0, (size_t)m * n * sizeof(float), s));
+        return REALM_OK;
+    }
+    return dense_launch(d_a, d_b, d_c, m, k, n, b_transposed ? 1 : 0, s);
 }
 
 REALM_API int realm_hip_fused_dequant_matmul_q4k(const void *blocks, size_t n_blocks,

@@ -1,63 +1,152 @@
 // Dense f32 GEMM behind GpuBackendTrait::matmul and the candle_matmul host
 // functions: C[m,n] = sum_k A[m,k] B'[k,n] with B' = B ([k,n] row-major) or,
-// for the transposed form, B' = B^T with B stored [n,k].  f32 FMA on VALU,
-// 64x64 tiles, 16-deep K slices staged in LDS, 4x4 outputs per thread.
+// for the transposed form, B' = B^T with B stored [n,k].
+//
+// On v_mfma_f32_32x32x2_f32: f32 products and f32 sums, so results differ
+// from a CPU f32 loop only in the order of the additions.  Lane l = r32 + 32h
+// supplies A[r32][h] and B[h][r32]; element v of its result is
+// D[8(v/4) + 4h + v%4][r32] (checked on the GPU).
+//
+//  * A workgroup (4 waves, 2 x 2) owns 128 rows x 128 columns of C; a wave
+//    owns 64 x 64, four 32 x 32 MFMA tiles.
+//  * Launches with few tiles (skinny products) split K over blockIdx.z.
+//  * K goes in slices of 16, staged in LDS k-major (As[k][m], Bs[k][n], rows
+//    padded to 132 floats), double buffered: the next slice's global loads
+//    are in flight while the current one is multiplied, one barrier per
+//    slice.  Out-of-range elements load as zero (clamped address, select),
+//    so edges need no branches around loads.
 #include "common.h"
 
 namespace {
-constexpr int TILE = 64, KT = 16;
+constexpr int TM = 128, TN = 128, KT = 16, LP = TM + 4;
+typedef float floatx16 __attribute__((ext_vector_type(16)));
 }
 
+// blockIdx.z = K split: the workgroup sums k in [z K/ks, (z+1) K/ks) and,
+// with ks > 1, writes its part to part + z M N (realm_dense_reduce adds the
+// parts in split order).
 extern "C" __global__ __launch_bounds__(256) void realm_dense_f32(
     const float *__restrict__ A, const float *__restrict__ B, float *__restrict__ C, int M,
-    int N, int K, int b_trans)
+    int N, int K, int b_trans, int ks, float *__restrict__ part)
 {
-    __shared__ float As[KT][TILE + 4];
-    __shared__ float Bs[KT][TILE + 4];
-    const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
-    const int m0 = blockIdx.y * TILE, n0 = blockIdx.x * TILE;
-    float acc[4][4] = {};
-    for (int k0 = 0; k0 < K; k0 += KT) {
-        // 64x16 slice of A and 16x64 slice of B': 1024 elements each, 4 per thread
-        for (int e = threadIdx.x; e < TILE * KT; e += 256) {
-            int r = e / KT, kk = e % KT; // A: row r, column k0+kk
-            int gm = m0 + r, gk = k0 + kk;
-            As[kk][r] = (gm < M && gk < K) ? A[(size_t)gm * K + gk] : 0.f;
-            float bv;
-            if (b_trans) {
-                int gn = n0 + r; // B[n][k]
-                bv = (gn < N && gk < K) ? B[(size_t)gn * K + gk] : 0.f;
-                Bs[kk][r] = bv;
-            } else {
-                int kk2 = e / TILE, c = e % TILE; // B[k][n]
-                int gk2 = k0 + kk2, gn = n0 + c;
-                bv = (gk2 < K && gn < N) ? B[(size_t)gk2 * N + gn] : 0.f;
-                Bs[kk2][c] = bv;
+    __shared__ float As[2][KT][LP];
+    __shared__ float Bs[2][KT][LP];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int r32 = lane & 31, h = lane >> 5;
+    const int wm = wave & 1, wn = wave >> 1;
+    const int m0 = blockIdx.y * TM, n0 = blockIdx.x * TN;
+    const int kb = (int)(((long long)K * blockIdx.z) / ks), ke = (int)(((long long)K * (blockIdx.z + 1)) / ks);
+    float *const out = ks > 1 ? part + (size_t)blockIdx.z * M * N : C;
+
+    // global -> register staging of one slice: 8 values of A and 8 of B per
+    // thread.  A (and B^T): thread t reads k = t % 16 of rows t / 16 + 16 i,
+    // 64 contiguous bytes per row; B: column t % 128 of slice rows t / 128 + 2i.
+    float ra[8], rb[8];
+    auto load_slice = [&](int k0) {
+        const int ka = k0 + (tid & 15);
+        const bool kin = ka < ke;
+        const int kc = kin ? ka : ke - 1;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int m = m0 + (tid >> 4) + 16 * i;
+            const float v = A[(size_t)min(m, M - 1) * K + kc];
+            ra[i] = (kin && m < M) ? v : 0.f;
+        }
+        if (b_trans) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int n = n0 + (tid >> 4) + 16 * i;
+                const float v = B[(size_t)min(n, N - 1) * K + kc];
+                rb[i] = (kin && n < N) ? v : 0.f;
+            }
+        } else {
+            const int n = n0 + (tid & 127);
+            const int ncl = min(n, N - 1);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int k = k0 + (tid >> 7) + 2 * i;
+                const float v = B[(size_t)min(k, ke - 1) * N + ncl];
+                rb[i] = (k < ke && n < N) ? v : 0.f;
             }
         }
-        __syncthreads();
+    };
+    auto store_slice = [&](int buf) {
 #pragma unroll
-        for (int kk = 0; kk < KT; ++kk) {
-            float a[4], b[4];
+        for (int i = 0; i < 8; ++i)
+            As[buf][tid & 15][(tid >> 4) + 16 * i] = ra[i];
+        if (b_trans) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                a[i] = As[kk][ty + 16 * i];
-                b[i] = Bs[kk][tx + 16 * i];
-            }
+            for (int i = 0; i < 8; ++i)
+                Bs[buf][tid & 15][(tid >> 4) + 16 * i] = rb[i];
+        } else {
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    acc[i][j] += a[i] * b[j];
+            for (int i = 0; i < 8; ++i)
+                Bs[buf][(tid >> 7) + 2 * i][tid & 127] = rb[i];
         }
+    };
+
+    floatx16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+                acc[i][j][e] = 0.f;
+
+    load_slice(kb);
+    store_slice(0);
+    __syncthreads();
+    int cur = 0;
+    for (int k0 = kb; k0 < ke; k0 += KT) {
+        const bool more = k0 + KT < ke;
+        if (more)
+            load_slice(k0 + KT);
+#pragma unroll
+        for (int s = 0; s < KT / 2; ++s) {
+            const int k = 2 * s + h;
+            float a[2], b[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+                a[i] = As[cur][k][wm * 64 + 32 * i + r32];
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                b[j] = Bs[cur][k][wn * 64 + 32 * j + r32];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
+        }
+        if (more)
+            store_slice(cur ^ 1); // the other buffer: every wave finished it last slice
         __syncthreads();
+        cur ^= 1;
     }
+
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            int gm = m0 + ty + 16 * i, gn = n0 + tx + 16 * j;
-            if (gm < M && gn < N)
-                C[(size_t)gm * N + gn] = acc[i][j];
-        }
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int m = m0 + wm * 64 + 32 * i + 8 * (v >> 2) + 4 * h + (v & 3);
+                const int n = n0 + wn * 64 + 32 * j + r32;
+                if (m < M && n < N)
+                    out[(size_t)m * N + n] = acc[i][j][v];
+            }
+}
+
+// C = the sum of the ks parts, in split order (deterministic)
+extern "C" __global__ __launch_bounds__(256) void realm_dense_reduce(const float *__restrict__ part,
+                                                                     float *__restrict__ C,
+                                                                     long long n, int ks)
+{
+    const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n)
+        return;
+    float s = part[i];
+    for (int z = 1; z < ks; ++z)
+        s += part[(size_t)z * n + i];
+    C[i] = s;
 }

@@ -579,6 +579,40 @@ def test_dense_random(backend, m, k, n):
     assert rel_l2(got, ref) < 1e-5
 
 
+@pytest.mark.parametrize("transposed", [False, True])
+@pytest.mark.parametrize("m,k,n", [(1, 1, 1), (2, 3, 2), (31, 17, 129), (128, 256, 128),
+                                   (130, 515, 257), (32, 2048, 300), (5, 4099, 70)])
+def test_dense_dev(backend, m, k, n, transposed):
+    """Device-pointer dense product, both B layouts, ragged tile edges in m,
+    n and k, skinny products with K splits (parts summed in split order): f32
+    products and sums, so within f32 rounding of an f64 product; small-integer
+    inputs give exact results."""
+    g = synth.rng(m * 131 + k * 7 + n + transposed)
+    for ints in (False, True):
+        if ints:
+            a = g.integers(-8, 9, (m, k)).astype(np.float32)
+            b = g.integers(-8, 9, (k, n)).astype(np.float32)
+        else:
+            a = g.standard_normal((m, k), dtype=np.float32)
+            b = g.standard_normal((k, n), dtype=np.float32)
+        bs = np.ascontiguousarray(b.T) if transposed else b
+        da, db = backend.alloc(a.nbytes).upload(a), backend.alloc(bs.nbytes).upload(bs)
+        dc = backend.alloc(m * n * 4)
+        try:
+            backend.dense_matmul_dev(da.ptr, db.ptr, dc.ptr, m, k, n, transposed=transposed)
+            backend.synchronize()
+            got = dc.download(np.float32, m * n).reshape(m, n)
+        finally:
+            for d in (da, db, dc):
+                d.close()
+        ref = a.astype(np.float64) @ b.astype(np.float64)
+        if ints:
+            assert np.array_equal(got, ref.astype(np.float32))
+        else:  # f32 sums over k: relative error about 2^-24 sqrt(k)
+            assert rel_l2(got, ref) < 1e-5
+    assert backend.last_kernel() in ("realm_dense_f32", "realm_dense_reduce")
+
+
 def test_candle_matmul_host_function(backend, kat):
     """env.candle_matmul over a linear memory (memory64_host.rs:853-1086)."""
     mem = np.zeros(4096, np.uint8)
