@@ -343,6 +343,35 @@ def test_grouped_launch(backend, oracle, t, m):
         assert rc == 0 and err < REL_TOL
 
 
+def test_grouped_q6k_mixed_wide(backend, oracle):
+    """A grouped Q6_K launch where one matrix has sub-scales over the full
+    int8 range (the split-scale decode) and the others do not: the whole
+    launch takes the wide decode, exact for both kinds."""
+    g = synth.rng(606)
+    k, m = 1536, 37
+    ns = (200, 96, 130)
+    blocks = [synth.blocks(g, GGML_Q6_K, n, k) for n in ns]
+    blocks[1]["scales"] = g.integers(-128, 128, blocks[1]["scales"].shape, dtype=np.int8)
+    x = synth.activations(g, m, k)
+    hs = [backend.register_weights(GGML_Q6_K, b, n, k) for b, n in zip(blocks, ns)]
+    dx = backend.alloc(x.nbytes).upload(x)
+    dys = [backend.alloc(m * n * 4) for n in ns]
+    try:
+        backend.matmul_group_dev(hs, dx.ptr, m, [d.ptr for d in dys])
+        backend.synchronize()
+        kernel = backend.last_kernel()
+        got = [d.download(np.float32, m * n).reshape(m, n) for d, n in zip(dys, ns)]
+    finally:
+        for h in hs:
+            backend.release_weights(h)
+        for d in [dx] + dys:
+            d.close()
+    assert "q6kw_t" in kernel or "tiled_reduce" in kernel, kernel
+    for b, n, gi in zip(blocks, ns, got):
+        rc, ref = oracle.candle_fused(GGML_Q6_K, b, x, m, n, k)
+        assert rc == 0 and rel_l2(gi, ref.reshape(m, n)) < REL_TOL
+
+
 @pytest.mark.parametrize("ks", [2, 3, 6])
 def test_tiled_ksplit_repeat(backend, oracle, monkeypatch, ks):
     """K-split parts summed in split order: results are bit-identical from
