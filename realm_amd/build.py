@@ -19,12 +19,18 @@ KDIR = os.path.join(PKG, "csrc", "kernels")
 HDIR = os.path.join(PKG, "csrc", "host")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
-# code objects: the non-GEMV kernels, the GEMV variants per format and the
-# LDS-tiled GEMM (compiled in parallel; the host library embeds all of them)
+# code objects: the non-GEMV kernels, the GEMV variants per format and token
+# count (1, 2, 4) and the LDS-tiled GEMM (compiled in parallel; the host library embeds all of them)
 HSACO_UNITS = [("realm_kernels", "realm_kernels.hip", ()),
                ("realm_gemv_q4k", "gemv_fmt.hip", ("REALM_GEMV_FMT=0",)),
                ("realm_gemv_q6k", "gemv_fmt.hip", ("REALM_GEMV_FMT=1",)),
                ("realm_gemv_q80", "gemv_fmt.hip", ("REALM_GEMV_FMT=2",)),
+               ("realm_gemv_q4k_t2", "gemv_fmt.hip", ("REALM_GEMV_FMT=0", "REALM_GEMV_NT=2")),
+               ("realm_gemv_q6k_t2", "gemv_fmt.hip", ("REALM_GEMV_FMT=1", "REALM_GEMV_NT=2")),
+               ("realm_gemv_q80_t2", "gemv_fmt.hip", ("REALM_GEMV_FMT=2", "REALM_GEMV_NT=2")),
+               ("realm_gemv_q4k_t4", "gemv_fmt.hip", ("REALM_GEMV_FMT=0", "REALM_GEMV_NT=4")),
+               ("realm_gemv_q6k_t4", "gemv_fmt.hip", ("REALM_GEMV_FMT=1", "REALM_GEMV_NT=4")),
+               ("realm_gemv_q80_t4", "gemv_fmt.hip", ("REALM_GEMV_FMT=2", "REALM_GEMV_NT=4")),
                ("realm_gemm_tiled", "gemm_tiled.hip", ())]
 HSACO = os.path.join(LIB_DIR, "realm_kernels.hsaco")
 LIBSO = os.path.join(LIB_DIR, "librealm_hip.so")

@@ -29,8 +29,8 @@
 #define REALM_STR(x) REALM_STR2(x)
 
 // The code objects (REALM_HSACO_COUNT of them: the non-GEMV kernels, the
-// GEMV variants of each weight format and the LDS-tiled GEMM), embedded at
-// link time.
+// GEMV variants of each weight format and token count, and the LDS-tiled
+// GEMM), embedded at link time.
 #define REALM_EMBED(I, FILE)                                                                   \
     __asm__(".pushsection .rodata.realm_hsaco" #I ",\"a\",@progbits\n"                        \
             ".balign 4096\n"                                                                  \
@@ -46,9 +46,16 @@ REALM_EMBED(1, REALM_HSACO_FILE1)
 REALM_EMBED(2, REALM_HSACO_FILE2)
 REALM_EMBED(3, REALM_HSACO_FILE3)
 REALM_EMBED(4, REALM_HSACO_FILE4)
-static_assert(REALM_HSACO_COUNT == 5, "the build embeds five code objects");
+REALM_EMBED(5, REALM_HSACO_FILE5)
+REALM_EMBED(6, REALM_HSACO_FILE6)
+REALM_EMBED(7, REALM_HSACO_FILE7)
+REALM_EMBED(8, REALM_HSACO_FILE8)
+REALM_EMBED(9, REALM_HSACO_FILE9)
+REALM_EMBED(10, REALM_HSACO_FILE10)
+static_assert(REALM_HSACO_COUNT == 11, "the build embeds eleven code objects");
 static const unsigned char *const realm_hsacos[REALM_HSACO_COUNT] = {
-    realm_hsaco0, realm_hsaco1, realm_hsaco2, realm_hsaco3, realm_hsaco4};
+    realm_hsaco0, realm_hsaco1, realm_hsaco2, realm_hsaco3, realm_hsaco4,  realm_hsaco5,
+    realm_hsaco6, realm_hsaco7, realm_hsaco8, realm_hsaco9, realm_hsaco10};
 
 #define REALM_API extern "C" __attribute__((visibility("default")))
 
@@ -387,11 +394,13 @@ struct LoraCall {
 
 // --------------------------------------------------------------- dispatch
 
-// M = 1, f32 activations: the integer-dot GEMV over 1..4 matrices of one
-// format that share x (rows concatenated).  Returns BACKEND_UNSUPPORTED when
-// the row is too long for the kernel's register budget or LDS (the caller
-// then uses the MFMA path).
-int run_gemv(const Weight *const *ws, int count, const float *d_x, float *const *d_y,
+// M = 1..4 tokens, f32 activations: the integer-dot GEMV over 1..4
+// matrices of one format that share x (rows concatenated); 2 tokens run the
+// 2-token kernels, 3 and 4 the 4-token ones (every weight load serves all of
+// them).  Returns BACKEND_UNSUPPORTED when the row is too long for the
+// kernel's register budget or the quantized x of all tokens does not fit in
+// LDS (the caller then uses the MFMA path).
+int run_gemv(const Weight *const *ws, int count, const float *d_x, int M, float *const *d_y,
              hipStream_t s)
 {
     const Weight &w = *ws[0];
@@ -399,15 +408,18 @@ int run_gemv(const Weight *const *ws, int count, const float *d_x, float *const 
     int lpr = U <= 16 ? 16 : (U <= 32 ? 32 : 64);
     int upl = (U + lpr - 1) / lpr;
     const int rpp = 64 / lpr;
-    size_t lds = (size_t)U * 16 * 10; // 8 x records + up to 2 meta float4 per unit
-    if (upl > 8 || lds > g_dev.max_lds || count < 1 || count > REALM_GEMV_MAX_MATS)
+    const int nt = M <= 1 ? 1 : (M == 2 ? 2 : 4);
+    // per token: 8 x records + up to 2 meta float4 per unit
+    size_t lds = (size_t)U * 16 * 10 * nt;
+    if (M < 1 || M > 4 || upl > 8 || lds > g_dev.max_lds || count < 1 ||
+        count > REALM_GEMV_MAX_MATS)
         return REALM_BACKEND_UNSUPPORTED;
     // A grouped launch needs every matrix to start on a pass boundary;
     // otherwise the matrices go one launch each.
     for (int i = 0; count > 1 && i < count; ++i)
         if (ws[i]->n % rpp) {
             for (int j = 0; j < count; ++j)
-                CHECK(run_gemv(ws + j, 1, d_x, d_y + j, s));
+                CHECK(run_gemv(ws + j, 1, d_x, M, d_y + j, s));
             return REALM_OK;
         }
     realm::GemvArgs a;
@@ -428,6 +440,7 @@ int run_gemv(const Weight *const *ws, int count, const float *d_x, float *const 
     a.K = (int)w.k;
     a.KX = (int)w.kx;
     a.nan_fb = g_nan_fb.load();
+    a.m = M;
     // At most one workgroup per CU (each stages x in its LDS); each wave
     // keeps a ring of D passes in flight, D the smallest variant that holds
     // all of the wave's passes (so the whole weight stream is requested
@@ -436,10 +449,16 @@ int run_gemv(const Weight *const *ws, int count, const float *d_x, float *const 
     static const int d_u1[] = {1, 2, 3, 4, 6, 8, 12}, d_u2[] = {1, 2, 3, 4},
                      d_u3[] = {1, 2, 3, 4, 6}, d_u45[] = {1, 2}, d_big[] = {1};
     const int *ds = upl == 1 ? d_u1 : upl == 2 ? d_u2 : upl == 3 ? d_u3 : upl <= 5 ? d_u45 : d_big;
-    const int nd = upl == 1 ? 7 : upl == 2 ? 4 : upl == 3 ? 5 : upl <= 5 ? 2 : 1;
-    auto threads_of = [&](int d) { // GEMV_TH in gemv.hip
-        return upl == 1 ? (d <= 4 ? 1024 : 512)
-                        : (upl <= 3 ? (d == 1 ? 1024 : (upl == 2 || d == 2 ? 512 : 256)) : 256);
+    int nd = upl == 1 ? 7 : upl == 2 ? 4 : upl == 3 ? 5 : upl <= 5 ? 2 : 1;
+    if (nt > 1) // the multi-token kernels: depths 1-4, 1-2 and 1 (gemv.hip)
+        nd = upl == 1 ? 4 : upl <= 3 ? 2 : 1;
+    auto threads_of = [&](int d) { // GEMV_TH and GEMV_THN in gemv.hip
+        if (nt == 1)
+            return upl == 1 ? (d <= 4 ? 1024 : 512)
+                            : (upl <= 3 ? (d == 1 ? 1024 : (upl == 2 || d == 2 ? 512 : 256)) : 256);
+        if (upl == 1)
+            return nt == 2 || d <= 3 ? 512 : 256;
+        return upl == 2 ? (d == 1 && nt == 2 ? 1024 : 512) : (upl == 3 && d == 1 ? 512 : 256);
     };
     const long cu = g_dev.cu_count;
     const long npass = ((long)rows + rpp - 1) / rpp;
@@ -449,14 +468,21 @@ int run_gemv(const Weight *const *ws, int count, const float *d_x, float *const 
     // the halved workgroup (register budget) leaves each wave two of them.
     // Deeper rings cost more registers than they gain.
     int d = 1;
-    if (upl == 1) {
+    if (upl == 1 && nt > 1) {
+        // multi-token (8 waves per workgroup): all of a wave's passes in
+        // flight up to 3 (measured at 7B shapes: Wo best at 2, Q/K/V and
+        // gate/up at 3)
+        const long t8 = (npass + cu * 8 - 1) / (cu * 8);
+        d = (int)std::min<long>(std::max<long>(t8, 1), 3);
+    } else if (upl == 1) {
         const long t1 = (npass + cu * 16 - 1) / (cu * 16); // passes per wave
         d = t1 <= 3 ? (int)std::max<long>(t1, 1) : 2;
-    } else if ((upl == 2 || upl == 3) && npass >= 2 * cu * 8) {
-        d = 2;
+    } else if ((upl == 2 || upl == 3) && npass >= 2 * cu * 8 && nt == 1) {
+        d = 2; // (multi-token: one pass in flight measured faster)
     }
     if (w.type == GGML_Q8_0 && d > 8) // its 12-deep ring does not fit the registers
         d = 8;
+    d = std::min(d, ds[nd - 1]);
     if (const char *env = getenv("REALM_GEMV_D")) { // tuning override
         int v = atoi(env);
         for (int i = 0; i < nd; ++i)
@@ -473,7 +499,8 @@ int run_gemv(const Weight *const *ws, int count, const float *d_x, float *const 
     }
     std::string name = std::string("realm_gemv_") + fmt_name(w.type) + "_l" +
                        std::to_string(lpr) + "_u" + std::to_string(upl) + "_d" +
-                       std::to_string(d) + "_m" + (count == 1 ? "1" : "4");
+                       std::to_string(d) + "_m" + (count == 1 ? "1" : "4") +
+                       (nt == 1 ? "" : "_t" + std::to_string(nt));
     void *args[] = {&a};
     return launch(name, dim3((unsigned)std::max<long>(wgs, 1)), dim3(threads), lds, s, args);
 }
@@ -816,10 +843,10 @@ int run_gemm(const Weight &w, const void *d_x, bool bf16, size_t M, float *d_y, 
 int run_matmul(const Weight &w, const void *d_x, bool bf16, size_t M, float *d_y,
                hipStream_t s, const LoraCall *lora)
 {
-    if (M == 1 && !bf16 && !lora) {
+    if (M <= 4 && !bf16 && !lora) {
         const Weight *ws[1] = {&w};
         float *ys[1] = {d_y};
-        int rc = run_gemv(ws, 1, (const float *)d_x, ys, s);
+        int rc = run_gemv(ws, 1, (const float *)d_x, (int)M, ys, s);
         if (rc != REALM_BACKEND_UNSUPPORTED)
             return rc;
     }
@@ -1245,8 +1272,8 @@ REALM_API int realm_hip_weights_matmul_group_dev(const uint64_t *handles, size_t
         return fail(REALM_INVALID_ARGUMENT, "batch exceeds 2^31-1");
     hipStream_t s;
     CHECK(pick_stream(stream, &s));
-    if (batch == 1) {
-        int rc = run_gemv(wp, (int)count, d_input, d_outs, s);
+    if (batch >= 1 && batch <= 4) {
+        int rc = run_gemv(wp, (int)count, d_input, (int)batch, d_outs, s);
         if (rc != REALM_BACKEND_UNSUPPORTED)
             return rc;
     }

@@ -283,128 +283,143 @@ REALM_DEV float combine(int ph, int pl, float s)
     return s * ((float)ph + (float)pl * (1.f / 254.f));
 }
 
-// Partial dot products of R rows with one unit of x.
-template <int FMT, int R>
-REALM_DEV void unit_dot(const Unit<FMT> (&w)[R], const int4 *rec, const float4 *meta, int U,
-                        int u, int nan_fb, float (&acc)[R])
+// Partial dot products of one row's unit with NT tokens' x.  xr(t, i) is
+// token t's x record at dword position i (0..7) of the unit, xm(t, j) its
+// metadata float4 j (Q4_K / Q6_K: 0, 1; Q8_0: 0): read from LDS, or from
+// registers that hold them for the whole kernel.  The tokens go one after
+// another with a scheduling barrier between them: left free, the compiler
+// hoists every token's LDS records ahead of the first dot product (32
+// VGPRs per token) and the multi-token kernels spill.
+template <int FMT, int NT, class XR, class XM>
+REALM_DEV void unit_dot(const Unit<FMT> &w, const XR &xr, const XM &xm, int u, int nan_fb,
+                        float (&acc)[NT])
 {
     if constexpr (FMT == FMT_Q4K) {
+        const int g = u & 3;
+        const float d = fix_scale(f16_bits_to_f32(w.hd.x), 0.00000006f, nan_fb);
+        const float dm = fix_scale(f16_bits_to_f32(w.hd.x >> 16), 0.00000024f, nan_fb);
+        const uint32_t pr = q4k_dev_pair(w.hd.y, w.hd.z, w.hd.w, g);
+        const float sa = (float)(pr & 63u), ma = (float)((pr >> 6) & 63u);
+        const float sb = (float)((pr >> 12) & 63u), mb = (float)((pr >> 18) & 63u);
         // low nibbles (sub-block 2g) read as int8 q in 0..15, high nibbles
-        // (sub-block 2g+1, stored XOR 8) masked as int8 16 * (q - 8)
-        int ha[R], la[R], hb[R], lb[R];
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-            ha[r] = la[r] = hb[r] = lb[r] = 0;
+        // (sub-block 2g+1, stored XOR 8) masked as int8 16 (q - 8); unpacked
+        // once for all tokens
+        uint32_t lo[8], hi[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const int4 xq = rec[i * U + u];
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                uint32_t q = word(i < 4 ? w[r].q0 : w[r].q1, i & 3);
-                uint32_t lo = q & 0x0F0F0F0Fu, hi = q & 0xF0F0F0F0u;
-                ha[r] = dot4(lo, (uint32_t)xq.x, ha[r]);
-                la[r] = dot4(lo, (uint32_t)xq.y, la[r]);
-                hb[r] = dot4(hi, (uint32_t)xq.z, hb[r]);
-                lb[r] = dot4(hi, (uint32_t)xq.w, lb[r]);
-            }
+            const uint32_t q = word(i < 4 ? w.q0 : w.q1, i & 3);
+            lo[i] = q & 0x0F0F0F0Fu;
+            hi[i] = q & 0xF0F0F0F0u;
         }
-        // (s_a/254, s_b/(254*16), Sx_a, Sx_b), (8 Sx_b, -, -, -)
-        const float4 m = meta[2 * u], m2 = meta[2 * u + 1];
-        const int g = u & 3;
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const float d = fix_scale(f16_bits_to_f32(w[r].hd.x), 0.00000006f, nan_fb);
-            const float dm = fix_scale(f16_bits_to_f32(w[r].hd.x >> 16), 0.00000024f, nan_fb);
-            const uint32_t pr = q4k_dev_pair(w[r].hd.y, w[r].hd.z, w[r].hd.w, g);
-            const float sa = (float)(pr & 63u), ma = (float)((pr >> 6) & 63u);
-            const float sb = (float)((pr >> 12) & 63u), mb = (float)((pr >> 18) & 63u);
+        for (int t = 0; t < NT; ++t) {
+            if (t > 0)
+                __builtin_amdgcn_sched_barrier(0);
+            int ha = 0, la = 0, hb = 0, lb = 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int4 xq = xr(t, i);
+                ha = dot4(lo[i], (uint32_t)xq.x, ha);
+                la = dot4(lo[i], (uint32_t)xq.y, la);
+                hb = dot4(hi[i], (uint32_t)xq.z, hb);
+                lb = dot4(hi[i], (uint32_t)xq.w, lb);
+            }
+            // (s_a/254, s_b/(254*16), Sx_a, Sx_b), (8 Sx_b, -, -, -)
+            const float4 m = xm(t, 0), m2 = xm(t, 1);
             // exact integers: |ha*254 + la| < 2^24, |hb*254 + lb| < 2^28
-            const float fa = (float)(ha[r] * 254 + la[r]);
-            const float fb = (float)(hb[r] * 254 + lb[r]);
-            const float ta = m.x * fa;          // sum over sub-block a of q * x
+            const float fa = (float)(ha * 254 + la);
+            const float fb = (float)(hb * 254 + lb);
+            const float ta = m.x * fa;            // sum over sub-block a of q * x
             const float tb = fmaf(m.y, fb, m2.x); // sum over b of (q - 8) x + 8 sum x
-            acc[r] += d * fmaf(sa, ta, sb * tb) - dm * fmaf(ma, m.z, mb * m.w);
+            acc[t] += d * fmaf(sa, ta, sb * tb) - dm * fmaf(ma, m.z, mb * m.w);
         }
     } else if constexpr (FMT == FMT_Q6K) {
-        int ph[R][4], pl[R][4];
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-#pragma unroll
-            for (int t = 0; t < 4; ++t)
-                ph[r][t] = pl[r][t] = 0;
+        const float d = fix_scale(f16_bits_to_f32(w.d), 0.00000006f, nan_fb);
+        // the 6-bit quants of the unit's four 16-runs, unpacked once for all
+        // tokens: v[i][r] holds 4 quants of run r
+        uint32_t v[4][4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int4 x01 = rec[(2 * i) * U + u], x23 = rec[(2 * i + 1) * U + u];
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                uint32_t a = word(w[r].qa, i), b = word(w[r].qb, i), h = word(w[r].qh, i);
-                uint32_t v0 = (a & 0x0F0F0F0Fu) | ((h << 4) & 0x30303030u);
-                uint32_t v1 = (b & 0x0F0F0F0Fu) | ((h << 2) & 0x30303030u);
-                uint32_t v2 = ((a >> 4) & 0x0F0F0F0Fu) | (h & 0x30303030u);
-                uint32_t v3 = ((b >> 4) & 0x0F0F0F0Fu) | ((h >> 2) & 0x30303030u);
-                ph[r][0] = dot4(v0, (uint32_t)x01.x, ph[r][0]);
-                pl[r][0] = dot4(v0, (uint32_t)x01.y, pl[r][0]);
-                ph[r][1] = dot4(v1, (uint32_t)x01.z, ph[r][1]);
-                pl[r][1] = dot4(v1, (uint32_t)x01.w, pl[r][1]);
-                ph[r][2] = dot4(v2, (uint32_t)x23.x, ph[r][2]);
-                pl[r][2] = dot4(v2, (uint32_t)x23.y, pl[r][2]);
-                ph[r][3] = dot4(v3, (uint32_t)x23.z, ph[r][3]);
-                pl[r][3] = dot4(v3, (uint32_t)x23.w, pl[r][3]);
-            }
+            const uint32_t a = word(w.qa, i), b = word(w.qb, i), h = word(w.qh, i);
+            v[i][0] = (a & 0x0F0F0F0Fu) | ((h << 4) & 0x30303030u);
+            v[i][1] = (b & 0x0F0F0F0Fu) | ((h << 2) & 0x30303030u);
+            v[i][2] = ((a >> 4) & 0x0F0F0F0Fu) | (h & 0x30303030u);
+            v[i][3] = ((b >> 4) & 0x0F0F0F0Fu) | ((h >> 2) & 0x30303030u);
         }
-        const float4 ms = meta[2 * u], mx = meta[2 * u + 1]; // run scales, run sums
-        const float s[4] = {ms.x, ms.y, ms.z, ms.w}, sx[4] = {mx.x, mx.y, mx.z, mx.w};
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            float d = fix_scale(f16_bits_to_f32(w[r].d), 0.00000006f, nan_fb);
+        for (int t = 0; t < NT; ++t) {
+            if (t > 0)
+                __builtin_amdgcn_sched_barrier(0);
+            int ph[4] = {0, 0, 0, 0}, pl[4] = {0, 0, 0, 0};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int4 x01 = xr(t, 2 * i), x23 = xr(t, 2 * i + 1);
+                ph[0] = dot4(v[i][0], (uint32_t)x01.x, ph[0]);
+                pl[0] = dot4(v[i][0], (uint32_t)x01.y, pl[0]);
+                ph[1] = dot4(v[i][1], (uint32_t)x01.z, ph[1]);
+                pl[1] = dot4(v[i][1], (uint32_t)x01.w, pl[1]);
+                ph[2] = dot4(v[i][2], (uint32_t)x23.x, ph[2]);
+                pl[2] = dot4(v[i][2], (uint32_t)x23.y, pl[2]);
+                ph[3] = dot4(v[i][3], (uint32_t)x23.z, ph[3]);
+                pl[3] = dot4(v[i][3], (uint32_t)x23.w, pl[3]);
+            }
+            // run scales, run sums
+            const float4 ms = xm(t, 0), mx = xm(t, 1);
+            const float sr[4] = {ms.x, ms.y, ms.z, ms.w}, sx[4] = {mx.x, mx.y, mx.z, mx.w};
             float part = 0.f;
 #pragma unroll
-            for (int t = 0; t < 4; ++t)
-                part += (float)(int8_t)(w[r].sc >> (8 * t)) *
-                        (combine(ph[r][t], pl[r][t], s[t]) - 32.f * sx[t]);
-            acc[r] += d * part;
+            for (int r = 0; r < 4; ++r)
+                part += (float)(int8_t)(w.sc >> (8 * r)) *
+                        (combine(ph[r], pl[r], sr[r]) - 32.f * sx[r]);
+            acc[t] += d * part;
         }
     } else {
-        int ha[R], la[R], hb[R], lb[R];
+        const float da = f16_bits_to_f32(w.d), db = f16_bits_to_f32(w.d >> 16);
 #pragma unroll
-        for (int r = 0; r < R; ++r)
-            ha[r] = la[r] = hb[r] = lb[r] = 0;
+        for (int t = 0; t < NT; ++t) {
+            if (t > 0)
+                __builtin_amdgcn_sched_barrier(0);
+            int ha = 0, la = 0, hb = 0, lb = 0;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int4 xq = rec[i * U + u];
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                uint32_t qa = word(w[r].q[i >> 2], i & 3);
-                uint32_t qb = word(w[r].q[2 + (i >> 2)], i & 3);
-                ha[r] = dot4(qa, (uint32_t)xq.x, ha[r]);
-                la[r] = dot4(qa, (uint32_t)xq.y, la[r]);
-                hb[r] = dot4(qb, (uint32_t)xq.z, hb[r]);
-                lb[r] = dot4(qb, (uint32_t)xq.w, lb[r]);
+            for (int i = 0; i < 8; ++i) {
+                const int4 xq = xr(t, i);
+                const uint32_t qa = word(w.q[i >> 2], i & 3);
+                const uint32_t qb = word(w.q[2 + (i >> 2)], i & 3);
+                ha = dot4(qa, (uint32_t)xq.x, ha);
+                la = dot4(qa, (uint32_t)xq.y, la);
+                hb = dot4(qb, (uint32_t)xq.z, hb);
+                lb = dot4(qb, (uint32_t)xq.w, lb);
             }
-        }
-        const float4 m = meta[u];
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            float da = f16_bits_to_f32(w[r].d), db = f16_bits_to_f32(w[r].d >> 16);
-            acc[r] += da * combine(ha[r], la[r], m.x) + db * combine(hb[r], lb[r], m.y);
+            const float4 m = xm(t, 0);
+            acc[t] += da * combine(ha, la, m.x) + db * combine(hb, lb, m.y);
         }
     }
 }
 
 
 // One launch: NM matrices (1, or up to REALM_GEMV_MAX_MATS with NM = 4)
-// that share x, rows concatenated.  LPR lanes share a row (64/LPR row slots
-// per wave and pass), lane l owns units l, l+LPR, ... (UPL of them), and
-// each wave keeps a ring of D passes in flight.
-template <int FMT, int LPR, int UPL, int D, int XR, int TH, int NM>
+// that share x, rows concatenated, and NT tokens (a.m of them live: 1..NT;
+// x is [m][K], each matrix's y is [m][its rows]).  LPR lanes share a row
+// (64/LPR row slots per wave and pass), lane l owns units l, l+LPR, ...
+// (UPL of them), and each wave keeps a ring of D passes in flight.  Every
+// weight a lane loads is used for all NT tokens; token t's quantized x is
+// the LDS region of TS = 10 U int4 starting at t TS (8 U records, then up
+// to 2 U metadata float4).
+template <int FMT, int LPR, int UPL, int D, int XR, int TH, int NM, int NT>
 REALM_DEV void gemv(const GemvArgs &a)
 {
     using W = Unit<FMT>;
     extern __shared__ int4 lds[];
     const int K = a.K, KX = a.KX;
     const int U = KX >> 6;
+    const int TS = 10 * U;
     int4 *rec = lds;
     float4 *meta = reinterpret_cast<float4 *>(lds + 8 * U);
+    const int M = NT == 1 ? 1 : a.m;
+    // x of the lane's unit held in registers (one unit per lane, NT > 1)
+    constexpr bool XREG = UPL == 1 && NT > 1;
+    int4 xreg[XREG ? NT : 1][8];
+    float4 mreg[XREG ? NT : 1][2];
     const int lane = threadIdx.x & 63;
     const int slot = lane / LPR, l = lane % LPR;
     constexpr int wpb = TH / 64;
@@ -427,13 +442,13 @@ REALM_DEV void gemv(const GemvArgs &a)
     // critical path.
     if constexpr (NM == 1)
         asm volatile("" ::"s"(K), "s"(KX), "s"(nw), "s"(rows), "s"(xp), "s"(nan_fb),
-                     "s"(w0[0]), "s"(w1[0]), "s"(w2[0]), "s"(yv[0]), "s"(a.pad));
+                     "s"(w0[0]), "s"(w1[0]), "s"(w2[0]), "s"(yv[0]), "s"(a.m));
     else
         asm volatile("" ::"s"(K), "s"(KX), "s"(nw), "s"(rs1), "s"(rs2), "s"(rs3), "s"(rows),
                      "s"(xp), "s"(nan_fb), "s"(w0[0]), "s"(w0[1]), "s"(w0[2]), "s"(w0[3]),
                      "s"(w1[0]), "s"(w1[1]), "s"(w1[2]), "s"(w1[3]), "s"(w2[0]), "s"(w2[1]),
                      "s"(w2[2]), "s"(w2[3]), "s"(yv[0]), "s"(yv[1]), "s"(yv[2]), "s"(yv[3]),
-                     "s"(a.pad));
+                     "s"(a.m));
     const int npass = (rows + RPP - 1) / RPP;
     // this wave's passes: p = gw + i*nw for i < T
     const int T = gw < npass ? (npass - gw + nw - 1) / nw : 0;
@@ -486,25 +501,52 @@ REALM_DEV void gemv(const GemvArgs &a)
             asm volatile("" : "+v"(zero));
             mt = meta + zero;
         }
-        float acc = 0.f;
+        float acc[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+            acc[t] = 0.f;
 #pragma unroll
         for (int j = 0; j < UPL; ++j) {
-            const int u = l + j * LPR;
-            float part[1] = {0.f};
-            W one[1] = {w[j]};
-            unit_dot<FMT, 1>(one, rec, mt, U, min(u, U - 1), nan_fb, part);
-            acc += u < U ? part[0] : 0.f;
+            const int u = l + j * LPR, uc = min(u, U - 1);
+            float part[NT];
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+                part[t] = 0.f;
+            if constexpr (XREG) {
+                auto xr = [&](int t, int p) { return xreg[t][p]; };
+                auto xm = [&](int t, int q) { return mreg[t][q]; };
+                unit_dot<FMT, NT>(w[j], xr, xm, uc, nan_fb, part);
+            } else {
+                auto xr = [&](int t, int p) { return rec[t * TS + p * U + uc]; };
+                auto xm = [&](int t, int q) {
+                    return mt[t * TS + (FMT == FMT_Q80 ? uc : 2 * uc + q)];
+                };
+                unit_dot<FMT, NT>(w[j], xr, xm, uc, nan_fb, part);
+            }
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+                acc[t] += u < U ? part[t] : 0.f;
         }
-        const float v = group_total<LPR>(acc);
+        float v[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+            v[t] = group_total<LPR>(acc[t]);
         const int row = (gw + i * nw) * RPP + slot;
         if (l == LPR - 1 && row < rows) {
-            if constexpr (NM == 1) {
-                yv[0][row] = v;
-            } else {
+            float *y = yv[0];
+            int lr = row, nrow = rows;
+            if constexpr (NM > 1) {
                 const int m = (row >= rs1 ? 1 : 0) + (row >= rs2 ? 1 : 0) + (row >= rs3 ? 1 : 0);
-                float *y = m == 0 ? yv[0] : (m == 1 ? yv[1] : (m == 2 ? yv[2] : yv[3]));
-                y[row - (m == 0 ? 0 : (m == 1 ? rs1 : (m == 2 ? rs2 : rs3)))] = v;
+                const int r0 = m == 0 ? 0 : (m == 1 ? rs1 : (m == 2 ? rs2 : rs3));
+                const int r1 = m == 0 ? rs1 : (m == 1 ? rs2 : (m == 2 ? rs3 : rows));
+                y = m == 0 ? yv[0] : (m == 1 ? yv[1] : (m == 2 ? yv[2] : yv[3]));
+                lr = row - r0;
+                nrow = r1 - r0;
             }
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+                if (t < M)
+                    y[(size_t)t * nrow + lr] = v[t];
         }
     };
 
@@ -512,10 +554,15 @@ REALM_DEV void gemv(const GemvArgs &a)
     // weights), then the first ring slot, then x is quantized into LDS while
     // those weights are in flight.
     const int rounds = (8 * U + TH - 1) / TH;
-    float4 xv[XR][2];
+    // rounds held in registers per token (the register budget is shared
+    // among the tokens)
+    constexpr int XH = NT == 1 ? XR : (XR / NT > 0 ? XR / NT : 1);
+    float4 xv[NT][XH][2];
 #pragma unroll
-    for (int rd = 0; rd < XR; ++rd)
-        x_round<TH>(xp, K, U, rd, xv[rd]);
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int rd = 0; rd < XH; ++rd)
+            x_round<TH>(xp + (size_t)min(t, M - 1) * K, K, U, rd, xv[t][rd]);
     // Every wave of the workgroup issues its x loads before any wave issues
     // a weight load: the CU's vector memory path returns data in request
     // order, so x requests queued behind other waves' weight requests would
@@ -526,15 +573,36 @@ REALM_DEV void gemv(const GemvArgs &a)
     W w[D][UPL];
     load_pass(w[0], 0);
 #pragma unroll
-    for (int rd = 0; rd < XR; ++rd)
-        if (rd < rounds)
-            quant_round<FMT, TH>(rec, meta, xv[rd], U, rd);
-    for (int rd = XR; rd < rounds; ++rd) {
-        float4 v[2];
-        x_round<TH>(xp, K, U, rd, v);
-        quant_round<FMT, TH>(rec, meta, v, U, rd);
-    }
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int rd = 0; rd < XH; ++rd)
+            if (rd < rounds)
+                quant_round<FMT, TH>(rec + t * TS, meta + t * TS, xv[t][rd], U, rd);
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+        for (int rd = XH; rd < rounds; ++rd) {
+            float4 v[2];
+            x_round<TH>(xp + (size_t)min(t, M - 1) * K, K, U, rd, v);
+            quant_round<FMT, TH>(rec + t * TS, meta + t * TS, v, U, rd);
+        }
     lds_barrier();
+    // One unit per lane, several tokens: the lane's unit is the same in
+    // every pass, so its records and metadata of every token move to
+    // registers once (re-reading them from LDS each pass would take NT x
+    // 160 bytes of LDS bandwidth per lane and pass, more than the CU's LDS
+    // delivers at the weight stream's rate).
+    if constexpr (XREG) {
+        const int uc = min(l, U - 1);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+#pragma unroll
+            for (int p = 0; p < 8; ++p)
+                xreg[t][p] = rec[t * TS + p * U + uc];
+#pragma unroll
+            for (int q = 0; q < 2; ++q)
+                mreg[t][q] = meta[t * TS + (FMT == FMT_Q80 ? uc : 2 * uc + q)];
+        }
+    }
     // The rest of the ring is issued only now: a larger burst ahead of the
     // x staging would delay x (same memory queues) and so the first pass.
 #pragma unroll
@@ -573,24 +641,39 @@ REALM_DEV void gemv(const GemvArgs &a)
     ((UPL) == 1 ? ((D) <= 4 ? 1024 : 512)                                                    \
                 : ((UPL) <= 3 ? ((D) == 1 ? 1024 : ((UPL) == 2 || (D) == 2 ? 512 : 256)) : 256))
 
-// Variant: lanes per row, units per lane, ring depth, matrices (1 or 4).
-#define DEF_GEMV1(NAME, FMT, LPR, UPL, D, NM)                                                 \
-    extern "C" __global__ __launch_bounds__(GEMV_TH(UPL, D)) void                            \
-        realm_gemv_##NAME##_l##LPR##_u##UPL##_d##D##_m##NM(GemvArgs a)                       \
+// Workgroup size of the multi-token kernels: with one unit per lane the x
+// of every token stays in registers (40 VGPRs per token), so 512 or 256
+// threads; beyond, the per-token sums and the longer dot product body need
+// more registers per ring slot, so halved where the one-token size would
+// spill.
+#define GEMV_THN(UPL, D, NT)                                                                  \
+    ((NT) == 1 ? GEMV_TH(UPL, D)                                                              \
+               : ((UPL) == 1 ? ((NT) == 2 || (D) <= 3 ? 512 : 256)                            \
+                             : ((UPL) == 2 ? ((D) == 1 && (NT) == 2 ? 1024 : 512)               \
+                                           : ((UPL) == 3 && (D) == 1 ? 512 : 256))))
+
+// Variant: lanes per row, units per lane, ring depth, matrices (1 or 4),
+// tokens (the one-token kernels carry no token suffix).
+#define DEF_GEMV1(NAME, FMT, LPR, UPL, D, NM, NT, SUF)                                       \
+    extern "C" __global__ __launch_bounds__(GEMV_THN(UPL, D, NT)) void                       \
+        realm_gemv_##NAME##_l##LPR##_u##UPL##_d##D##_m##NM##SUF(GemvArgs a)                  \
     {                                                                                        \
-        gemv<FMT, LPR, UPL, D, GEMV_XR(UPL, GEMV_TH(UPL, D)), GEMV_TH(UPL, D), NM>(a);      \
+        gemv<FMT, LPR, UPL, D, GEMV_XR(UPL, GEMV_THN(UPL, D, NT)), GEMV_THN(UPL, D, NT), NM,  \
+             NT>(a);                                                                          \
     }
 #if REALM_GEMV_FMT == FMT_Q4K
-#define DEF_GEMV2(LPR, UPL, D, NM) DEF_GEMV1(q4k, FMT_Q4K, LPR, UPL, D, NM)
+#define DEF_GEMV2(LPR, UPL, D, NM, NT, SUF) DEF_GEMV1(q4k, FMT_Q4K, LPR, UPL, D, NM, NT, SUF)
 #elif REALM_GEMV_FMT == FMT_Q6K
-#define DEF_GEMV2(LPR, UPL, D, NM) DEF_GEMV1(q6k, FMT_Q6K, LPR, UPL, D, NM)
+#define DEF_GEMV2(LPR, UPL, D, NM, NT, SUF) DEF_GEMV1(q6k, FMT_Q6K, LPR, UPL, D, NM, NT, SUF)
 #else
-#define DEF_GEMV2(LPR, UPL, D, NM) DEF_GEMV1(q80, FMT_Q80, LPR, UPL, D, NM)
+#define DEF_GEMV2(LPR, UPL, D, NM, NT, SUF) DEF_GEMV1(q80, FMT_Q80, LPR, UPL, D, NM, NT, SUF)
 #endif
-#define DEF_GEMV(LPR, UPL, D) DEF_GEMV2(LPR, UPL, D, 1) DEF_GEMV2(LPR, UPL, D, 4)
 
-// The variants the host chooses from (ring depths per units-per-lane must
-// match the host's tables).
+#if !defined(REALM_GEMV_NT) || REALM_GEMV_NT == 1
+#define DEF_GEMV(LPR, UPL, D) DEF_GEMV2(LPR, UPL, D, 1, 1, ) DEF_GEMV2(LPR, UPL, D, 4, 1, )
+
+// The one-token variants the host chooses from (ring depths per
+// units-per-lane must match the host's tables).
 #define DEF_GEMV_ONE_UNIT(LPR)                                                                \
     DEF_GEMV(LPR, 1, 1) DEF_GEMV(LPR, 1, 2) DEF_GEMV(LPR, 1, 3) DEF_GEMV(LPR, 1, 4)           \
         DEF_GEMV(LPR, 1, 6) DEF_GEMV(LPR, 1, 8) DEF_GEMV(LPR, 1, 12)
@@ -613,3 +696,29 @@ DEF_GEMV(64, 5, 2)
 DEF_GEMV(64, 6, 1)
 DEF_GEMV(64, 7, 1)
 DEF_GEMV(64, 8, 1)
+#else
+// Multi-token variants (2 or 4 tokens; 3 tokens run the 4-token kernels):
+// ring depths 1-4 for one unit per lane, 1-2 for two or three, 1 beyond
+// (each pass carries NT times the dot products, so deeper rings gain less).
+#define DEF_GEMV_NT(LPR, UPL, D, NT, SUF)                                                     \
+    DEF_GEMV2(LPR, UPL, D, 1, NT, SUF) DEF_GEMV2(LPR, UPL, D, 4, NT, SUF)
+#define DEF_GEMV_TOKENS(NT, SUF)                                                              \
+    DEF_GEMV_NT(16, 1, 1, NT, SUF) DEF_GEMV_NT(16, 1, 2, NT, SUF)                             \
+    DEF_GEMV_NT(16, 1, 3, NT, SUF) DEF_GEMV_NT(16, 1, 4, NT, SUF)                             \
+    DEF_GEMV_NT(32, 1, 1, NT, SUF) DEF_GEMV_NT(32, 1, 2, NT, SUF)                             \
+    DEF_GEMV_NT(32, 1, 3, NT, SUF) DEF_GEMV_NT(32, 1, 4, NT, SUF)                             \
+    DEF_GEMV_NT(64, 1, 1, NT, SUF) DEF_GEMV_NT(64, 1, 2, NT, SUF)                             \
+    DEF_GEMV_NT(64, 1, 3, NT, SUF) DEF_GEMV_NT(64, 1, 4, NT, SUF)                             \
+    DEF_GEMV_NT(64, 2, 1, NT, SUF) DEF_GEMV_NT(64, 2, 2, NT, SUF)                             \
+    DEF_GEMV_NT(64, 3, 1, NT, SUF) DEF_GEMV_NT(64, 3, 2, NT, SUF)                             \
+    DEF_GEMV_NT(64, 4, 1, NT, SUF) DEF_GEMV_NT(64, 5, 1, NT, SUF)                             \
+    DEF_GEMV_NT(64, 6, 1, NT, SUF) DEF_GEMV_NT(64, 7, 1, NT, SUF)                             \
+    DEF_GEMV_NT(64, 8, 1, NT, SUF)
+#if REALM_GEMV_NT == 2
+DEF_GEMV_TOKENS(2, _t2)
+#elif REALM_GEMV_NT == 4
+DEF_GEMV_TOKENS(4, _t4)
+#else
+#error "REALM_GEMV_NT must be 1, 2 or 4"
+#endif
+#endif

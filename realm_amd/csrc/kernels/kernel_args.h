@@ -68,7 +68,7 @@ struct GemvArgs {
     const float *x;
     int32_t K, KX;
     int32_t nan_fb;
-    int32_t pad;
+    int32_t m; // tokens (rows of x and of each y); 1 for the one-token kernels
 };
 
 #ifdef __cplusplus

@@ -130,7 +130,7 @@ def test_fused_reference_inputs(backend, oracle):
 
 
 @pytest.mark.parametrize("t", FORMATS)
-@pytest.mark.parametrize("m", [1, 2, 5, 16, 17, 33, 64, 100, 130])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 16, 17, 33, 64, 100, 130])
 def test_fused_random(backend, oracle, t, m):
     g = synth.rng(1000 * t + m)
     n, k = 200, 1024 if t != GGML_Q8_0 else 1056
@@ -370,6 +370,58 @@ def test_grouped_q6k_mixed_wide(backend, oracle):
     for b, n, gi in zip(blocks, ns, got):
         rc, ref = oracle.candle_fused(GGML_Q6_K, b, x, m, n, k)
         assert rc == 0 and rel_l2(gi, ref.reshape(m, n)) < REL_TOL
+
+
+@pytest.mark.parametrize("t", FORMATS)
+@pytest.mark.parametrize("m", [2, 3, 4])
+def test_gemv_tokens(backend, oracle, t, m):
+    """The multi-token integer-dot GEMV (2 tokens; 3 and 4 on the 4-token
+    kernels): every lanes-per-row / units-per-lane shape from K = 1024 to
+    28672, ragged row counts, one matrix and a grouped launch.  Each output
+    is checked against the oracle, and each token's row against a one-token
+    launch on that token alone (the same quantized x and the same integer
+    sums, so they agree to f32 rounding)."""
+    g = synth.rng(zlib.crc32(f"tokens{t}{m}".encode()) % 100000)
+    suffix = "_t2" if m == 2 else "_t4"
+    for n, k in ((37, 1024), (50, 2048), (45, 4096), (33, 11008), (19, 28672)):
+        blocks = synth.blocks(g, t, n, k)
+        x = synth.activations(g, m, k)
+        got = _dev_matmul(backend, t, blocks, n, k, x, False)
+        kernel = backend.last_kernel()
+        # 4 tokens of a 28672-long row need more LDS than a workgroup has:
+        # those go to the MFMA path
+        if not (k == 28672 and m > 2):
+            assert kernel.startswith("realm_gemv_") and kernel.endswith(suffix), kernel
+        rc, ref = oracle.candle_fused(t, blocks, x, m, n, k)
+        err = rel_l2(got, ref.reshape(m, n))
+        print(f"{NAMES[t]} m={m} n={n} k={k} {kernel} rel_l2={err:.3e}")
+        assert rc == 0 and err < REL_TOL, (n, k)
+        if kernel.startswith("realm_gemv_"):
+            for i in range(m):
+                one = _dev_matmul(backend, t, blocks, n, k, x[i:i + 1], False)
+                assert np.max(np.abs(one[0] - got[i])) <= 1e-6 * np.max(np.abs(one[0])), (k, i)
+    # grouped: three matrices of one row each per pass (K = 4096)
+    k, ns = 4096, (64, 40, 24)
+    blocks = [synth.blocks(g, t, n, k) for n in ns]
+    x = synth.activations(g, m, k)
+    hs = [backend.register_weights(t, b, n, k) for b, n in zip(blocks, ns)]
+    dx = backend.alloc(x.nbytes).upload(x)
+    dys = [backend.alloc(m * n * 4) for n in ns]
+    try:
+        backend.matmul_group_dev(hs, dx.ptr, m, [d.ptr for d in dys])
+        backend.synchronize()
+        kernel = backend.last_kernel()
+        outs = [d.download(np.float32, m * n).reshape(m, n) for d, n in zip(dys, ns)]
+    finally:
+        for h in hs:
+            backend.release_weights(h)
+        dx.close()
+        for d in dys:
+            d.close()
+    assert "_m4" + suffix in kernel, kernel
+    for b, n, got in zip(blocks, ns, outs):
+        rc, ref = oracle.candle_fused(t, b, x, m, n, k)
+        assert rc == 0 and rel_l2(got, ref.reshape(m, n)) < REL_TOL, n
 
 
 @pytest.mark.parametrize("ks", [2, 3, 6])
