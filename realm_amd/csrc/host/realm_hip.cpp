@@ -731,21 +731,55 @@ LoraU lora_u(const Weight &w, const AdapterSet &set, const XPrep &p)
     return {(int)((w.kx + 511) / 512), (int)(p.Mp * round_up(set.rmax, 8))};
 }
 
-// u = A_a x for every token's adapter a, from the prepared activations
-// (optionally on the side stream, joined again before the expand).
-int lora_shrink_launch(const Weight &w, const LoraCall &lc, const XPrep &p, bool bf16, size_t M,
-                       const GemmTile &tile, void *u, hipStream_t s)
+// Kernel arguments of a LoRA shrink or expand launch over `count`
+// projections that share the prepared input and the token ids; u[i] is
+// projection i's slice of the shrink output, y[i] its output.
+realm::LoraGroupArgs lora_group_args(const Weight *const *w, const LoraCall *lc, int count,
+                                     const XPrep &p, size_t M, void *const *u, float *const *y)
 {
-    const AdapterSet &set = *lc.set;
-    const LoraU lu = lora_u(w, set, p);
-    const void *table = set.table;
-    const int32_t *ids = lc.d_ids;
-    void *xh = p.xh, *xl = p.xl, *ts = p.ts;
-    int iM = (int)M, iK = (int)w.k, iKX = (int)w.kx, irmax = (int)round_up(set.rmax, 8),
-        pstride = lu.pstride;
-    void *args[] = {&xh, &xl, &ts, (void *)&ids, (void *)&table, &u,
-                    &iM, &iK, &iKX, &irmax, &pstride};
-    const std::string name = std::string("realm_lora_shrink_") + fmt_name(w.type) +
+    realm::LoraGroupArgs g;
+    std::memset(&g, 0, sizeof g);
+    g.xh = p.xh;
+    g.xl = p.xl;
+    g.tscale = (const float *)p.ts;
+    g.ids = lc[0].d_ids;
+    g.M = (int)M;
+    g.K = (int)w[0]->k;
+    g.KX = (int)w[0]->kx;
+    g.nparts = lora_u(*w[0], *lc[0].set, p).nparts;
+    int slots = 0;
+    for (int i = 0; i < count; ++i) {
+        const AdapterSet &set = *lc[i].set;
+        g.a_start[i] = slots;
+        slots += (int)set.count;
+        g.table[i] = (const LoraEntry *)set.table;
+        g.u[i] = (float *)u[i];
+        g.y[i] = y ? y[i] : nullptr;
+        g.N[i] = (int)w[i]->n;
+        g.rmax[i] = (int)round_up(set.rmax, 8);
+        g.pstride[i] = lora_u(*w[i], set, p).pstride;
+    }
+    g.a_start[count] = slots;
+    for (int i = count + 1; i <= REALM_GEMM_MAX_SEGS; ++i)
+        g.a_start[i] = INT32_MAX;
+    return g;
+}
+
+// u = A_a x for every token's adapter a, from the prepared activations, for
+// `count` projections in one launch (optionally on the side stream, joined
+// again before the expand).
+int lora_shrink_launch(const Weight *const *w, const LoraCall *lc, int count, const XPrep &p,
+                       bool bf16, size_t M, const GemmTile &tile, void *const *u, hipStream_t s)
+{
+    realm::LoraGroupArgs g = lora_group_args(w, lc, count, p, M, u, nullptr);
+    int rmax = 0;
+    for (int i = 0; i < count; ++i)
+        rmax = std::max(rmax, lc[i].set->rmax);
+    const unsigned slots = (unsigned)g.a_start[count];
+    if (slots == 0)
+        return REALM_OK;
+    void *args[] = {&g};
+    const std::string name = std::string("realm_lora_shrink_") + fmt_name(w[0]->type) +
                              (bf16 ? "_bf16" : "_f32") + (tile.ord ? "_o1" : "");
     const bool use_side = lora_side();
     hipStream_t side = s;
@@ -755,36 +789,36 @@ int lora_shrink_launch(const Weight &w, const LoraCall &lc, const XPrep &p, bool
         HIP_TRY(hipEventRecord(fork, s));
         HIP_TRY(hipStreamWaitEvent(side, fork, 0));
     }
-    CHECK(launch(name,
-                 dim3((unsigned)set.count, (unsigned)((set.rmax + 15) / 16), (unsigned)lu.nparts),
-                 dim3(256), 0, side, args));
+    CHECK(launch(name, dim3(slots, (unsigned)((rmax + 15) / 16), (unsigned)g.nparts), dim3(256),
+                 0, side, args));
     if (use_side)
         HIP_TRY(hipEventRecord(join, side));
     return REALM_OK;
 }
 
-// y += scale_a B_a u per token, one workgroup per (adapter, 512 rows, 16
-// tokens); y already holds the base product.
-int lora_expand_launch(const Weight &w, const LoraCall &lc, const XPrep &p, size_t M, void *u,
-                       float *d_y, hipStream_t s)
+// y += scale_a B_a u per token for `count` projections in one launch, one
+// workgroup per (adapter slot, 512 rows, 16 tokens); y already holds the
+// base product.
+int lora_expand_launch(const Weight *const *w, const LoraCall *lc, int count, const XPrep &p,
+                       size_t M, void *const *u, float *const *d_y, hipStream_t s)
 {
-    const AdapterSet &set = *lc.set;
-    const LoraU lu = lora_u(w, set, p);
-    const void *table = set.table;
-    const int32_t *ids = lc.d_ids;
     if (lora_side()) {
         hipStream_t side;
         hipEvent_t fork, join;
         CHECK(side_stream(&side, &fork, &join));
         HIP_TRY(hipStreamWaitEvent(s, join, 0));
     }
-    int iM = (int)M, iN = (int)w.n, rmax = (int)round_up(set.rmax, 8), np = lu.nparts,
-        pstride = lu.pstride;
-    void *eargs[] = {&u, (void *)&ids, (void *)&table, (void *)&d_y, &iM, &iN, &rmax, &np,
-                     &pstride};
+    realm::LoraGroupArgs g = lora_group_args(w, lc, count, p, M, u, d_y);
+    size_t nmax = 0;
+    for (int i = 0; i < count; ++i)
+        nmax = std::max(nmax, w[i]->n);
+    const unsigned slots = (unsigned)g.a_start[count];
+    if (slots == 0 || nmax == 0)
+        return REALM_OK;
+    void *args[] = {&g};
     return launch("realm_lora_expand",
-                  dim3((unsigned)set.count, (unsigned)((w.n + 511) / 512), (unsigned)((M + 15) / 16)),
-                  dim3(256), 0, s, eargs);
+                  dim3(slots, (unsigned)((nmax + 511) / 512), (unsigned)((M + 15) / 16)),
+                  dim3(256), 0, s, args);
 }
 
 int gemm_launch(const Weight &w, const XPrep &p, bool bf16, size_t M, const GemmTile &tile,
@@ -793,7 +827,8 @@ int gemm_launch(const Weight &w, const XPrep &p, bool bf16, size_t M, const Gemm
     void *u = nullptr;
     if (lora) {
         CHECK(ws_get(s, WS_U, lora_u(w, *lora->set, p).bytes(), &u));
-        CHECK(lora_shrink_launch(w, *lora, p, bf16, M, tile, u, s));
+        const Weight *wp = &w;
+        CHECK(lora_shrink_launch(&wp, lora, 1, p, bf16, M, tile, &u, s));
     }
     if (tile.tiled) {
         const Weight *wp = &w;
@@ -824,8 +859,10 @@ int gemm_launch(const Weight &w, const XPrep &p, bool bf16, size_t M, const Gemm
                         (unsigned)((p.Mp + tile.toks_per_wg - 1) / tile.toks_per_wg));
         CHECK(launch(name, grid, dim3(tile.threads), 0, s, args));
     }
-    if (lora)
-        CHECK(lora_expand_launch(w, *lora, p, M, u, d_y, s));
+    if (lora) {
+        const Weight *wp = &w;
+        CHECK(lora_expand_launch(&wp, lora, 1, p, M, &u, &d_y, s));
+    }
     return REALM_OK;
 }
 
@@ -1532,8 +1569,8 @@ REALM_API int realm_hip_multi_lora_matmul_group_dev(const uint64_t *weight_handl
             CHECK(gemm_launch(w[i], p, false, batch, tile, d_outs[i], s, &lc[i]));
         return REALM_OK;
     }
-    // the shrinks (each into its own slice of the u workspace), one launch of
-    // the base products, then the expands
+    // one shrink launch for every projection (each into its own slice of
+    // the u workspace), one launch of the base products, one expand launch
     size_t uoff[REALM_GEMM_MAX_SEGS], ubytes = 0;
     for (size_t i = 0; i < count; ++i) {
         uoff[i] = ubytes;
@@ -1541,14 +1578,15 @@ REALM_API int realm_hip_multi_lora_matmul_group_dev(const uint64_t *weight_handl
     }
     void *u = nullptr;
     CHECK(ws_get(s, WS_U, ubytes, &u));
-    for (size_t i = 0; i < count; ++i)
-        CHECK(lora_shrink_launch(w[i], lc[i], p, false, batch, tile, (uint8_t *)u + uoff[i], s));
+    void *us[REALM_GEMM_MAX_SEGS];
     const Weight *wp[REALM_GEMM_MAX_SEGS];
-    for (size_t i = 0; i < count; ++i)
+    for (size_t i = 0; i < count; ++i) {
+        us[i] = (uint8_t *)u + uoff[i];
         wp[i] = &w[i];
+    }
+    CHECK(lora_shrink_launch(wp, lc, (int)count, p, false, batch, tile, us, s));
     CHECK(tiled_launch(wp, d_outs, (int)count, p, false, batch, tile, s));
-    for (size_t i = 0; i < count; ++i)
-        CHECK(lora_expand_launch(w[i], lc[i], p, batch, (uint8_t *)u + uoff[i], d_outs[i], s));
+    CHECK(lora_expand_launch(wp, lc, (int)count, p, batch, us, d_outs, s));
     return REALM_OK;
 }
 

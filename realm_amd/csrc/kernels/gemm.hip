@@ -727,24 +727,42 @@ REALM_DEV void shrink_body(const _Float16 *__restrict__ xh, const _Float16 *__re
     }
 }
 
+// Projection p of a grouped LoRA launch that concatenated adapter slot ga
+// falls in, and p's entry of a per-projection field (selects, not an
+// indexed load: an indexed kernel-argument array would go to scratch).
+REALM_DEV int lora_proj(const LoraGroupArgs &g, int ga)
+{
+    return (ga >= g.a_start[1] ? 1 : 0) + (ga >= g.a_start[2] ? 1 : 0) +
+           (ga >= g.a_start[3] ? 1 : 0);
+}
+template <class T, int N>
+REALM_DEV T lora_pick(const T (&v)[N], int p)
+{
+    static_assert(N >= REALM_GEMM_MAX_SEGS, "one entry per projection");
+    return p == 0 ? v[0] : (p == 1 ? v[1] : (p == 2 ? v[2] : v[3]));
+}
+
 template <int FMT, bool LO, int ORD>
-REALM_DEV void lora_shrink(const _Float16 *__restrict__ xh, const _Float16 *__restrict__ xl,
-                           const float *__restrict__ tscale, const int *__restrict__ ids,
-                           const LoraEntry *__restrict__ table, float *__restrict__ part, int M,
-                           int K, int KX, int rmax, int pstride)
+REALM_DEV void lora_shrink(const LoraGroupArgs &g)
 {
     __shared__ int toks[1024];
     __shared__ int count;
     __shared__ int wsum[4];
-    const int a = blockIdx.x;
-    adapter_tokens(ids, M, a, toks, &count, wsum);
-    const LoraEntry e = table[a];
+    const int p = lora_proj(g, blockIdx.x);
+    const int a = blockIdx.x - lora_pick(g.a_start, p);
+    const auto *xh = (const _Float16 *)g.xh, *xl = (const _Float16 *)g.xl;
+    float *part = lora_pick(g.u, p);
+    const int rmax = lora_pick(g.rmax, p), pstride = lora_pick(g.pstride, p);
+    adapter_tokens(g.ids, g.M, a, toks, &count, wsum);
+    const LoraEntry e = lora_pick(g.table, p)[a];
     if ((int)blockIdx.y * 16 >= e.rank || count == 0)
         return;
     if (e.dtype)
-        shrink_body<FMT, LO, ORD, true>(xh, xl, tscale, e, toks, count, part, K, KX, rmax, pstride);
+        shrink_body<FMT, LO, ORD, true>(xh, xl, g.tscale, e, toks, count, part, g.K, g.KX, rmax,
+                                        pstride);
     else
-        shrink_body<FMT, LO, ORD, false>(xh, xl, tscale, e, toks, count, part, K, KX, rmax, pstride);
+        shrink_body<FMT, LO, ORD, false>(xh, xl, g.tscale, e, toks, count, part, g.K, g.KX, rmax,
+                                         pstride);
 }
 
 // ------------------------------------------------------------ LoRA expand
@@ -888,46 +906,47 @@ REALM_DEV void expand_body(const float *__restrict__ u, const LoraEntry &e,
     }
 }
 
-REALM_DEV void lora_expand(const float *__restrict__ u, const int *__restrict__ ids,
-                           const LoraEntry *__restrict__ table, float *__restrict__ y, int M,
-                           int N, int rmax, int nparts, int pstride)
+// Grid: (adapter slots of all projections, groups of 512 rows of the
+// longest projection, 16-token chunks).
+REALM_DEV void lora_expand(const LoraGroupArgs &g)
 {
     __shared__ int toks[1024];
     __shared__ int count;
     __shared__ int wsum[4];
-    const int a = blockIdx.x;
-    adapter_tokens(ids, M, a, toks, &count, wsum);
+    const int p = lora_proj(g, blockIdx.x);
+    const int a = blockIdx.x - lora_pick(g.a_start, p);
+    const int N = lora_pick(g.N, p);
+    if ((int)blockIdx.y * EXPAND_RT * 64 >= N) // a shorter projection of the group
+        return;
+    adapter_tokens(g.ids, g.M, a, toks, &count, wsum);
     const int tc = blockIdx.z * 16; // this workgroup's 16 tokens of the adapter
     if (tc >= count)
         return;
-    const LoraEntry e = table[a];
+    const float *u = lora_pick(g.u, p);
+    float *y = lora_pick(g.y, p);
+    const int rmax = lora_pick(g.rmax, p), pstride = lora_pick(g.pstride, p);
+    const LoraEntry e = lora_pick(g.table, p)[a];
     if (e.dtype && (e.rank & 7) == 0)
-        expand_body<true>(u, e, toks, count, tc, y, N, rmax, nparts, pstride);
+        expand_body<true>(u, e, toks, count, tc, y, N, rmax, g.nparts, pstride);
     else
-        expand_body<false>(u, e, toks, count, tc, y, N, rmax, nparts, pstride);
+        expand_body<false>(u, e, toks, count, tc, y, N, rmax, g.nparts, pstride);
 }
 
-extern "C" __global__ __launch_bounds__(256) void realm_lora_expand(
-    const float *u, const int *ids, const LoraEntry *table, float *y, int M, int N, int rmax,
-    int nparts, int pstride)
+extern "C" __global__ __launch_bounds__(256) void realm_lora_expand(LoraGroupArgs g)
 {
-    lora_expand(u, ids, table, y, M, N, rmax, nparts, pstride);
+    lora_expand(g);
 }
 
 #define DEF_SHRINK1(NAME, FMT, ORD, SUF)                                                   \
     extern "C" __global__ __launch_bounds__(256) void realm_lora_shrink_##NAME##_f32##SUF( \
-        const _Float16 *xh, const _Float16 *xl, const float *tscale, const int *ids,      \
-        const LoraEntry *table, float *part, int M, int K, int KX, int rmax, int pstride) \
+        LoraGroupArgs g)                                                                   \
     {                                                                                      \
-        lora_shrink<FMT, true, ORD>(xh, xl, tscale, ids, table, part, M, K, KX, rmax,      \
-                                    pstride);                                              \
+        lora_shrink<FMT, true, ORD>(g);                                                    \
     }                                                                                      \
     extern "C" __global__ __launch_bounds__(256) void realm_lora_shrink_##NAME##_bf16##SUF(\
-        const _Float16 *xh, const _Float16 *xl, const float *tscale, const int *ids,      \
-        const LoraEntry *table, float *part, int M, int K, int KX, int rmax, int pstride) \
+        LoraGroupArgs g)                                                                   \
     {                                                                                      \
-        lora_shrink<FMT, false, ORD>(xh, xl, tscale, ids, table, part, M, K, KX, rmax,     \
-                                     pstride);                                             \
+        lora_shrink<FMT, false, ORD>(g);                                                   \
     }
 #define DEF_SHRINK(NAME, FMT) DEF_SHRINK1(NAME, FMT, 0, ) DEF_SHRINK1(NAME, FMT, 1, _o1)
 DEF_SHRINK(q4k, FMT_Q4K)

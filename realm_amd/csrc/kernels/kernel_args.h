@@ -21,6 +21,27 @@ struct LoraEntry {
 
 #define REALM_GEMM_MAX_SEGS 4
 
+// Arguments of the LoRA shrink and expand kernels: one launch covers up to
+// REALM_GEMM_MAX_SEGS projections that share the input and the token ids
+// (e.g. q and v), each with its own adapter set.  The adapter slots of the
+// projections are concatenated along grid x: projection p owns slots
+// a_start[p] .. a_start[p + 1] - 1 (unused entries hold INT32_MAX).
+struct LoraGroupArgs {
+    const void *xh;            // shrink: prepared activations (f16 hi)
+    const void *xl;            // shrink: f16 lo part (null for bf16 input)
+    const float *tscale;       // shrink: per-token scales
+    const int32_t *ids;        // adapter slot per token (-1 none)
+    int32_t M, K, KX;
+    int32_t nparts;            // shrink K parts (512 positions each)
+    int32_t a_start[REALM_GEMM_MAX_SEGS + 1];
+    const LoraEntry *table[REALM_GEMM_MAX_SEGS];
+    float *u[REALM_GEMM_MAX_SEGS];        // shrink output [part][token][rmax]
+    float *y[REALM_GEMM_MAX_SEGS];        // expand: outputs [M][N] (hold the base product)
+    int32_t N[REALM_GEMM_MAX_SEGS];
+    int32_t rmax[REALM_GEMM_MAX_SEGS];    // largest rank of the set, rounded up to 8
+    int32_t pstride[REALM_GEMM_MAX_SEGS]; // floats per part of u
+};
+
 // Arguments of the realm_gemm_* kernels.
 struct GemmArgs {
     const void *w0;     // Q4_K hdr | Q6_K d  | Q8_0 d
