@@ -797,7 +797,7 @@ int lora_shrink_launch(const Weight *const *w, const LoraCall *lc, int count, co
 }
 
 // y += scale_a B_a u per token for `count` projections in one launch, one
-// workgroup per (adapter slot, 512 rows, 16 tokens); y already holds the
+// workgroup per (adapter slot, 64 rt rows, 16 tokens); y already holds the
 // base product.
 int lora_expand_launch(const Weight *const *w, const LoraCall *lc, int count, const XPrep &p,
                        size_t M, void *const *u, float *const *d_y, hipStream_t s)
@@ -815,9 +815,20 @@ int lora_expand_launch(const Weight *const *w, const LoraCall *lc, int count, co
     const unsigned slots = (unsigned)g.a_start[count];
     if (slots == 0 || nmax == 0)
         return REALM_OK;
+    // 64-row tiles per workgroup: 8, or 4 (twice the workgroups) when the
+    // adapter slots x row groups of 512 leave fewer than two per CU
+    // (measured: config-4 q/k/v/o 4.8% LoRA overhead at 4 against 10% at 8;
+    // 2 was slower than either for config 3)
+    int rt = (long)slots * (long)((nmax + 511) / 512) < 2L * g_dev.cu_count ? 4 : 8;
+    if (const char *env = getenv("REALM_LORA_EXPAND_RT")) { // tuning override
+        const int v = atoi(env);
+        if (v == 2 || v == 4 || v == 8)
+            rt = v;
+    }
     void *args[] = {&g};
-    return launch("realm_lora_expand",
-                  dim3(slots, (unsigned)((nmax + 511) / 512), (unsigned)((M + 15) / 16)),
+    const std::string name = rt == 8 ? "realm_lora_expand" : "realm_lora_expand_rt" + std::to_string(rt);
+    return launch(name,
+                  dim3(slots, (unsigned)((nmax + 64 * rt - 1) / (64 * rt)), (unsigned)((M + 15) / 16)),
                   dim3(256), 0, s, args);
 }
 

@@ -768,13 +768,13 @@ REALM_DEV void lora_shrink(const LoraGroupArgs &g)
 // ------------------------------------------------------------ LoRA expand
 //
 // y[t][n] += scale_a * sum_j u[t][j] B_a[n][j] for the tokens t of adapter a
-// (y already holds the base product).  Grid (adapter, group of 8 64-row
+// (y already holds the base product).  Grid (adapter, group of RT 64-row
 // tiles, 16-token chunk of the adapter's tokens); a wave sums the shrink's
-// parts for its tokens once and sweeps 16 rows of each tile:
+// parts for its tokens once and sweeps 16 rows of each tile (RT = 8 for
+// large grids; 4 or 2 give small adapter sets more workgroups):
 // MFMA with A = u (token slots x rank, f32 split into f16 hi/lo), B = B_a^T
 // (rank x rows, f16 exact or f32 split).  Every (t, n) belongs to one
 // adapter, so the read-modify-write of y has no conflicts.
-#define EXPAND_RT 8  // 64-row tiles per workgroup
 #define EXPAND_KK 2  // rank steps of 32 held in registers: ranks up to 64
 // One pass of rank steps kk0 .. kk0 + EXPAND_KK - 1 for this wave's 16 rows of
 // each of the workgroup's 8 row tiles.  FAST: f16 B with a rank that is a
@@ -782,7 +782,7 @@ REALM_DEV void lora_shrink(const LoraGroupArgs &g)
 // f16 hi + lo) or f16 B element by element.  All loads of y and B are issued
 // before the u loads, and no loaded value is used before those are issued
 // too (a use right after a load makes the wave wait for it).
-template <bool FAST>
+template <bool FAST, int RT>
 REALM_DEV void expand_body(const float *__restrict__ u, const LoraEntry &e,
                            const int *__restrict__ toks, int count, int tc, float *__restrict__ y,
                            int N, int rmax, int nparts, int pstride)
@@ -802,21 +802,21 @@ REALM_DEV void expand_body(const float *__restrict__ u, const LoraEntry &e,
         toko[v] = toks[tj < count ? tj : 0];
     }
     auto brow = [&](int rt) {
-        return min((int)(blockIdx.y * EXPAND_RT + rt) * 64 + wave * 16 + r16, N - 1);
+        return min((int)(blockIdx.y * RT + rt) * 64 + wave * 16 + r16, N - 1);
     };
     const int ksteps = (e.rank + 31) / 32;
     for (int kk0 = 0; kk0 < ksteps; kk0 += EXPAND_KK) {
         const int nkk = min(EXPAND_KK, ksteps - kk0); // rank steps of this pass (uniform)
-        float yv[EXPAND_RT][4];
-        half8_t bh[EXPAND_RT][EXPAND_KK], bl[EXPAND_RT][EXPAND_KK];
+        float yv[RT][4];
+        half8_t bh[RT][EXPAND_KK], bl[RT][EXPAND_KK];
 #pragma unroll
-        for (int rt = 0; rt < EXPAND_RT; ++rt)
+        for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
             for (int v = 0; v < 4; ++v)
                 yv[rt][v] = y[(size_t)toko[v] * N + brow(rt)];
         if constexpr (FAST) {
 #pragma unroll
-            for (int rt = 0; rt < EXPAND_RT; ++rt)
+            for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
                 for (int q2 = 0; q2 < EXPAND_KK; ++q2) {
                     const int j0 = 32 * (kk0 + q2) + 8 * c;
@@ -864,7 +864,7 @@ REALM_DEV void expand_body(const float *__restrict__ u, const LoraEntry &e,
             }
         }
 #pragma unroll
-        for (int rt = 0; rt < EXPAND_RT; ++rt)
+        for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
             for (int q2 = 0; q2 < EXPAND_KK; ++q2) {
                 const int j0 = 32 * (kk0 + q2) + 8 * c;
@@ -885,8 +885,8 @@ REALM_DEV void expand_body(const float *__restrict__ u, const LoraEntry &e,
                 }
             }
 #pragma unroll
-        for (int rt = 0; rt < EXPAND_RT; ++rt) {
-            const int row = (blockIdx.y * EXPAND_RT + rt) * 64 + wave * 16 + r16;
+        for (int rt = 0; rt < RT; ++rt) {
+            const int row = (blockIdx.y * RT + rt) * 64 + wave * 16 + r16;
             floatx4 P = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int q2 = 0; q2 < EXPAND_KK; ++q2) {
@@ -908,6 +908,7 @@ REALM_DEV void expand_body(const float *__restrict__ u, const LoraEntry &e,
 
 // Grid: (adapter slots of all projections, groups of 512 rows of the
 // longest projection, 16-token chunks).
+template <int RT>
 REALM_DEV void lora_expand(const LoraGroupArgs &g)
 {
     __shared__ int toks[1024];
@@ -916,7 +917,7 @@ REALM_DEV void lora_expand(const LoraGroupArgs &g)
     const int p = lora_proj(g, blockIdx.x);
     const int a = blockIdx.x - lora_pick(g.a_start, p);
     const int N = lora_pick(g.N, p);
-    if ((int)blockIdx.y * EXPAND_RT * 64 >= N) // a shorter projection of the group
+    if ((int)blockIdx.y * RT * 64 >= N) // a shorter projection of the group
         return;
     adapter_tokens(g.ids, g.M, a, toks, &count, wsum);
     const int tc = blockIdx.z * 16; // this workgroup's 16 tokens of the adapter
@@ -927,14 +928,23 @@ REALM_DEV void lora_expand(const LoraGroupArgs &g)
     const int rmax = lora_pick(g.rmax, p), pstride = lora_pick(g.pstride, p);
     const LoraEntry e = lora_pick(g.table, p)[a];
     if (e.dtype && (e.rank & 7) == 0)
-        expand_body<true>(u, e, toks, count, tc, y, N, rmax, g.nparts, pstride);
+        expand_body<true, RT>(u, e, toks, count, tc, y, N, rmax, g.nparts, pstride);
     else
-        expand_body<false>(u, e, toks, count, tc, y, N, rmax, g.nparts, pstride);
+        expand_body<false, RT>(u, e, toks, count, tc, y, N, rmax, g.nparts, pstride);
 }
 
+// Row tiles per workgroup: 8 (realm_lora_expand), 4 or 2.
 extern "C" __global__ __launch_bounds__(256) void realm_lora_expand(LoraGroupArgs g)
 {
-    lora_expand(g);
+    lora_expand<8>(g);
+}
+extern "C" __global__ __launch_bounds__(256) void realm_lora_expand_rt4(LoraGroupArgs g)
+{
+    lora_expand<4>(g);
+}
+extern "C" __global__ __launch_bounds__(256) void realm_lora_expand_rt2(LoraGroupArgs g)
+{
+    lora_expand<2>(g);
 }
 
 #define DEF_SHRINK1(NAME, FMT, ORD, SUF)                                                   \

@@ -540,14 +540,20 @@ def test_multi_lora_small(backend, oracle, t, dtype, shape):
 
 @pytest.mark.parametrize("t", [GGML_Q4_K, GGML_Q6_K])
 @pytest.mark.parametrize("m", [4, 37])
-def test_multi_lora_group(backend, oracle, t, m):
+@pytest.mark.parametrize("rt", ["", "2", "4", "8"])
+def test_multi_lora_group(backend, oracle, monkeypatch, t, m, rt):
     """q/k/v-like projections with their own adapter sets in one grouped
     call (ragged rows; ranks 3 to 100; f16 and f32 factors), against the
     oracle per projection: per-matrix launches at 4 tokens, one tiled base
-    launch for the group at 37."""
+    launch for the group at 37; one shrink and one expand launch for the
+    group, the expand with its default row tile and each of 128, 256 and
+    512 rows per workgroup forced (600 rows: several row groups, the last
+    one partial; shorter projections skip the groups past their rows)."""
+    if rt:
+        monkeypatch.setenv("REALM_LORA_EXPAND_RT", rt)
     g = synth.rng(zlib.crc32(f"lgroup{t}{m}".encode()) % 100000)
     k = 1536
-    specs = [(300, (8, 16, 3), np.float16), (128, (64,), np.float32), (77, (100, 8), np.float16)]
+    specs = [(600, (8, 16, 3), np.float16), (128, (64,), np.float32), (77, (100, 8), np.float16)]
     x = synth.activations(g, m, k)
     ids = synth.adapter_ids(g, m, 3)
     ids[1] = 7  # unknown slot where a projection has fewer adapters: base only
@@ -572,6 +578,7 @@ def test_multi_lora_group(backend, oracle, t, m):
             dys.append(backend.alloc(m * n * 4))
         backend.multi_lora_matmul_group_dev(whs, shs, dx.ptr, m, d_ids.ptr, [d.ptr for d in dys])
         backend.synchronize()
+        kernel = backend.last_kernel()
         got = [d.download(np.float32, m * n).reshape(m, n) for d, n in zip(dys, ns)]
     finally:
         for sh in shs:
@@ -582,9 +589,13 @@ def test_multi_lora_group(backend, oracle, t, m):
             backend.release_weights(wh)
         for d in [dx, d_ids] + dys:
             d.close()
+    if m > 4:  # one expand launch for the group is the last kernel
+        assert kernel.startswith("realm_lora_expand"), kernel
+        if rt:
+            assert kernel.endswith("expand" if rt == "8" else f"_rt{rt}"), kernel
     for i, (gi, ref) in enumerate(zip(got, refs)):
         err = rel_l2(gi, ref)
-        print(f"lora group {NAMES[t]} m={m} proj {i} rel_l2={err:.3e}")
+        print(f"lora group {NAMES[t]} m={m} rt={rt} proj {i} rel_l2={err:.3e}")
         assert err < REL_TOL
 
 
