@@ -181,7 +181,9 @@ int realm_hip_weights_matmul_dev(uint64_t handle, const float *d_input, size_t b
  * input, e.g. the q/k/v projections (or gate/up) that realm_forward_layer
  * issues back to back on the same normed hidden state
  * (crates/realm-runtime/src/memory64_host.rs:2078-2308, 2384-2443):
- * d_outs[i] = x . W_i^T.  Batch 1 runs all of them in one launch. */
+ * d_outs[i] = x . W_i^T.  Batches of 1-4 tokens run all of them in one
+ * integer-dot GEMV launch, larger Q4_K / Q6_K batches in one tiled MFMA
+ * launch. */
 int realm_hip_weights_matmul_group_dev(const uint64_t *handles, size_t count,
                                        const float *d_input, size_t batch,
                                        float *const *d_outs, void *stream);
@@ -228,8 +230,9 @@ int realm_hip_multi_lora_matmul_dev(uint64_t weight_handle, uint64_t set_handle,
  * and the token adapter ids (q/k/v of realm_forward_layer,
  * crates/realm-runtime/src/memory64_host.rs:2078-2308, with LoRA applied per
  * projection as at :625-680): d_outs[i] = multi-LoRA matmul of weight i with
- * adapter set i.  The input is prepared once and the base products run as
- * one launch.  Device pointers, asynchronous on `stream`. */
+ * adapter set i.  The input is prepared once; the base products run as
+ * one launch, the shrinks of all projections as one and their expands as
+ * one.  Device pointers, asynchronous on `stream`. */
 int realm_hip_multi_lora_matmul_group_dev(const uint64_t *weight_handles,
                                           const uint64_t *set_handles, size_t count,
                                           const float *d_input, size_t batch,
