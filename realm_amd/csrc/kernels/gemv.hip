@@ -1,6 +1,6 @@
-// Decode GEMV, one token: y[n] = sum_k W[n,k] x[k] for resident Q4_K / Q6_K /
-// Q8_0 weights in the device layout of common.h, up to 4 matrices that share
-// x per launch (rows concatenated: e.g. Q/K/V, or gate/up).
+// Decode GEMV, 1-4 tokens: y[t][n] = sum_k W[n,k] x[t][k] for resident Q4_K /
+// Q6_K / Q8_0 weights in the device layout of common.h, up to 4 matrices that
+// share x per launch (rows concatenated: e.g. Q/K/V, or gate/up).
 //
 // Arithmetic: integer dot products.  Each workgroup first quantizes x per
 // 32-element block b into two int8 planes, scale s_b = amax_b / 127:
