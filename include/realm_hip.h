@@ -239,6 +239,75 @@ int realm_hip_multi_lora_matmul_group_dev(const uint64_t *weight_handles,
                                           const int32_t *d_adapter_ids,
                                           float *const *d_outs, void *stream);
 
+/* ------------------------------------------------------ GGUF model images */
+
+/* The transformer shape a GGUF image declares: GGUFParser::extract_config
+ * (crates/realm-core/src/formats/gguf.rs:212-280), with its keys
+ * ("<arch>.embedding_length", then "<arch>.hidden_size", ...) and defaults. */
+typedef struct realm_gguf_config {
+    uint32_t vocab_size, hidden_size, num_layers, num_heads, num_kv_heads;
+    uint32_t intermediate_size, max_seq_len;
+    float rms_norm_eps, rope_theta;
+} realm_gguf_config;
+
+/* Parse a GGUF image held in memory (the bytes ModelStorage::store_model
+ * receives, crates/realm-runtime/src/model_storage.rs:386-395): magic,
+ * version 2..3, metadata key/values, tensor table (GGUFParser::parse_header,
+ * gguf.rs:111-160, 300-480).  Host only: no device call.  Errors as the
+ * reference's: bad magic, version or value type -> REALM_MODEL_PARSE_ERROR;
+ * an image that ends inside the header -> REALM_IO_ERROR; an empty shape or
+ * a zero dimension -> REALM_INVALID_ARGUMENT (Shape::validate,
+ * crates/realm-core/src/tensor.rs:102-110).  The data section starts at the
+ * end of the tensor table rounded up to general.alignment (32 when absent,
+ * gguf.rs:165-175).  *model is a handle for the calls below. */
+int realm_hip_gguf_parse(const void *bytes, size_t len, uint64_t *model);
+
+/* Header counts and the data section's byte offset (gguf.rs:120-135, 165-175). */
+int realm_hip_gguf_info(uint64_t model, uint32_t *version, uint64_t *tensor_count,
+                        uint64_t *kv_count, uint64_t *data_offset);
+
+/* Tensor `index` of the table (TensorDesc, gguf.rs:427-455): its name
+ * (NUL-terminated into name[name_cap]), ggml type, number of dimensions,
+ * the dimensions padded with 1 to four (ggml order: dims4[0] is the row
+ * length), its absolute byte offset in the image and its byte size (F32,
+ * F16, Q8_0 as 34-byte blocks, Q4_K, Q6_K; 0 for other types).  Any output
+ * pointer may be NULL. */
+int realm_hip_gguf_tensor(uint64_t model, size_t index, char *name, size_t name_cap,
+                          int *ggml_type, uint32_t *n_dims, uint64_t *dims4,
+                          uint64_t *abs_offset, uint64_t *nbytes);
+
+/* Index of the tensor named `name` (the last one, for a repeated name, as
+ * StoredModel::add_tensor keeps it, model_storage.rs:286-290, 472). */
+int realm_hip_gguf_find(uint64_t model, const char *name, size_t *index);
+
+/* Metadata lookups: MetadataValue::as_u32 (any integer type, truncated) and
+ * as_string (gguf.rs:50-85). */
+int realm_hip_gguf_meta_u32(uint64_t model, const char *key, uint32_t *out);
+int realm_hip_gguf_meta_str(uint64_t model, const char *key, char *buf, size_t cap);
+
+/* GGUFParser::extract_config (gguf.rs:212-280). */
+int realm_hip_gguf_config(uint64_t model, realm_gguf_config *cfg);
+
+/* Upload every 2-D Q4_K / Q6_K / Q8_0 tensor of a parsed image once, as
+ * resident device weights (realm_hip_weights_register with n = dims4[1],
+ * k = dims4[0]), in place of the per-call tensor copies of
+ * ModelStorage / quantized_to_weight_format (model_storage.rs:444-487,
+ * crates/realm-runtime/src/memory64_host.rs:2078-2225).  `bytes` must be
+ * the image that was parsed; it is read during the call only.  A tensor
+ * that extends past the image -> REALM_MODEL_PARSE_ERROR.  Tensors already
+ * registered are skipped; *registered (may be NULL) counts this call's. */
+int realm_hip_gguf_register(uint64_t model, const void *bytes, size_t len,
+                            size_t *registered);
+
+/* The registered weight handle of tensor `name` and its shape (output rows
+ * n, row length k), for realm_hip_weights_matmul* and the multi-LoRA calls.
+ * A tensor that is not a registered weight -> REALM_BACKEND_UNSUPPORTED. */
+int realm_hip_gguf_weight(uint64_t model, const char *name, uint64_t *weight, size_t *n,
+                          size_t *k);
+
+/* Forget a parsed image and release the device weights registered from it. */
+int realm_hip_gguf_release(uint64_t model);
+
 /* -------------------------------------------------------- HIP graphs */
 
 /* Capture the device-pointer calls issued on `stream` (not NULL) between

@@ -74,6 +74,20 @@ SIGNATURES = {
     "realm_hip_event_destroy": (c_int, [c_void_p]),
     "realm_hip_event_record": (c_int, [c_void_p, c_void_p]),
     "realm_hip_event_elapsed_ms": (c_int, [c_void_p, c_void_p, POINTER(c_float)]),
+    "realm_hip_gguf_parse": (c_int, [c_void_p, c_size_t, POINTER(c_uint64)]),
+    "realm_hip_gguf_info": (c_int, [c_uint64, POINTER(c_uint32), POINTER(c_uint64),
+                                    POINTER(c_uint64), POINTER(c_uint64)]),
+    "realm_hip_gguf_tensor": (c_int, [c_uint64, c_size_t, c_char_p, c_size_t, POINTER(c_int),
+                                      POINTER(c_uint32), POINTER(c_uint64), POINTER(c_uint64),
+                                      POINTER(c_uint64)]),
+    "realm_hip_gguf_find": (c_int, [c_uint64, c_char_p, POINTER(c_size_t)]),
+    "realm_hip_gguf_meta_u32": (c_int, [c_uint64, c_char_p, POINTER(c_uint32)]),
+    "realm_hip_gguf_meta_str": (c_int, [c_uint64, c_char_p, c_char_p, c_size_t]),
+    "realm_hip_gguf_config": (c_int, [c_uint64, c_void_p]),
+    "realm_hip_gguf_register": (c_int, [c_uint64, c_void_p, c_size_t, POINTER(c_size_t)]),
+    "realm_hip_gguf_weight": (c_int, [c_uint64, c_char_p, POINTER(c_uint64), POINTER(c_size_t),
+                                      POINTER(c_size_t)]),
+    "realm_hip_gguf_release": (c_int, [c_uint64]),
 }
 
 _lib = None

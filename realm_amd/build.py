@@ -1,7 +1,8 @@
 """Build the gfx950 code object and the C-ABI host library, in-tree.
 
     realm_amd/lib/realm_kernels.hsaco   hipcc --genco --offload-arch=gfx950
-    realm_amd/lib/librealm_hip.so       g++, embeds the code object, links libamdhip64
+    realm_amd/lib/librealm_hip.so       g++ (realm_hip.cpp, gguf.cpp), embeds the code
+                                        objects, links libamdhip64
 
 Run as ``python -m realm_amd.build`` (or through ``__graft_entry__.build()``).
 Builds always recompile; they cross-compile without a GPU.
@@ -82,7 +83,7 @@ def build_host(out: str = LIBSO, hsacos: list | None = None) -> str:
           "-D__HIP_PLATFORM_AMD__", f"-DREALM_HSACO_COUNT={len(hsacos)}", *embeds,
           "-I", os.path.join(ROCM, "include"), "-I", os.path.join(REPO, "include"),
           "-I", KDIR,
-          os.path.join(HDIR, "realm_hip.cpp"), "-o", tmp,
+          os.path.join(HDIR, "realm_hip.cpp"), os.path.join(HDIR, "gguf.cpp"), "-o", tmp,
           "-L", os.path.join(ROCM, "lib"), "-Wl,-rpath," + os.path.join(ROCM, "lib"),
           "-lamdhip64", "-lpthread"])
     os.replace(tmp, out)

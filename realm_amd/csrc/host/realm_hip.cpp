@@ -59,6 +59,10 @@ static const unsigned char *const realm_hsacos[REALM_HSACO_COUNT] = {
 
 #define REALM_API extern "C" __attribute__((visibility("default")))
 
+// Sets the calling thread's last-error message and returns code (for the
+// library's other translation units; not exported).
+int realm_set_error(int code, const std::string &msg);
+
 using realm::GemmArgs;
 using realm::LoraEntry;
 
@@ -1782,3 +1786,5 @@ REALM_API int realm_hip_event_elapsed_ms(void *start, void *stop, float *ms)
     HIP_TRY(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)stop));
     return REALM_OK;
 }
+
+int realm_set_error(int code, const std::string &msg) { return fail(code, msg); }
