@@ -239,6 +239,28 @@ int realm_hip_multi_lora_matmul_group_dev(const uint64_t *weight_handles,
                                           const int32_t *d_adapter_ids,
                                           float *const *d_outs, void *stream);
 
+/* ------------------------------------------- element-wise layer operations */
+
+/* RMSNorm of `rows` rows of `hidden` f32 values on the device, as
+ * CandleNeuralOpsBackend::rms_norm (crates/realm-compute-cpu/src/
+ * candle_neural_ops_backend.rs:32-60; candle-nn ops::rms_norm:
+ * y = x / sqrt(mean(x^2) + eps) * weight) where realm_forward_layer norms
+ * the hidden state (crates/realm-runtime/src/memory64_host.rs:2069, 2337).
+ * With d_residual set, the row is first x + residual (the residual add of
+ * memory64_host.rs:2318-2324), written to d_sum when that is not NULL: the
+ * add and the norm in one pass.  hidden must be a multiple of 4, every
+ * pointer 16-byte aligned; d_sum may not be d_x or d_residual (d_out may be
+ * d_x).  Asynchronous on `stream`. */
+int realm_hip_rms_norm_dev(const float *d_x, const float *d_residual, const float *d_weight,
+                           float eps, size_t rows, size_t hidden, float *d_sum, float *d_out,
+                           void *stream);
+
+/* SwiGLU of realm_forward_layer (memory64_host.rs:2419-2425):
+ * out[i] = (gate[i] * (1 / (1 + exp(-gate[i])))) * up[i].  n a multiple of
+ * 4, pointers 16-byte aligned; d_out may be d_gate or d_up. */
+int realm_hip_swiglu_dev(const float *d_gate, const float *d_up, size_t n, float *d_out,
+                         void *stream);
+
 /* ------------------------------------------------------ GGUF model images */
 
 /* The transformer shape a GGUF image declares: GGUFParser::extract_config

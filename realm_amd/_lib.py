@@ -88,6 +88,9 @@ SIGNATURES = {
     "realm_hip_gguf_weight": (c_int, [c_uint64, c_char_p, POINTER(c_uint64), POINTER(c_size_t),
                                       POINTER(c_size_t)]),
     "realm_hip_gguf_release": (c_int, [c_uint64]),
+    "realm_hip_rms_norm_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_float, c_size_t, c_size_t,
+                                       c_void_p, c_void_p, c_void_p]),
+    "realm_hip_swiglu_dev": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p, c_void_p]),
 }
 
 _lib = None

@@ -322,6 +322,20 @@ class HipGpuBackend:
         self._check(self.lib.realm_hip_multi_lora_matmul_group_dev(
             ws, ss, len(whs), c_void_p(d_x), batch, c_void_p(d_ids), ys, c_void_p(stream or 0)))
 
+    # ------------------------------------------- element-wise layer ops
+    def rms_norm_dev(self, d_x: int, d_weight: int, eps: float, rows: int, hidden: int,
+                     d_out: int, d_residual: int = 0, d_sum: int = 0, stream=None) -> None:
+        """RMSNorm per row (candle_neural_ops_backend.rs:32-60), optionally of
+        x + residual (written to d_sum)."""
+        self._check(self.lib.realm_hip_rms_norm_dev(
+            c_void_p(d_x), c_void_p(d_residual or None), c_void_p(d_weight), eps, rows, hidden,
+            c_void_p(d_sum or None), c_void_p(d_out), c_void_p(stream or 0)))
+
+    def swiglu_dev(self, d_gate: int, d_up: int, n: int, d_out: int, stream=None) -> None:
+        """silu(gate) * up (memory64_host.rs:2419-2425)."""
+        self._check(self.lib.realm_hip_swiglu_dev(c_void_p(d_gate), c_void_p(d_up), n,
+                                                  c_void_p(d_out), c_void_p(stream or 0)))
+
 
 __all__ = ["HipGpuBackend", "RealmError", "InvalidShape", "BackendError", "DeviceBuffer",
            "DTYPE_F32", "DTYPE_F16"]

@@ -1108,6 +1108,55 @@ REALM_API int realm_hip_matmul_dev(const float *d_a, const float *d_b, float *d_
     return dense_launch(d_a, d_b, d_c, m, k, n, b_transposed ? 1 : 0, s);
 }
 
+// ------------------------------------------------ element-wise layer ops
+
+namespace {
+bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+} // namespace
+
+REALM_API int realm_hip_rms_norm_dev(const float *d_x, const float *d_residual,
+                                     const float *d_weight, float eps, size_t rows, size_t hidden,
+                                     float *d_sum, float *d_out, void *stream)
+{
+    if (rows == 0 || hidden == 0)
+        return REALM_OK;
+    if (!d_x || !d_weight || !d_out || (d_sum && !d_residual))
+        return fail(REALM_INVALID_ARGUMENT, "rms_norm: null pointer argument");
+    if (hidden % 4 || hidden > (size_t)INT32_MAX || rows > (size_t)INT32_MAX)
+        return fail(REALM_INVALID_ARGUMENT, "rms_norm: hidden must be a multiple of 4 below 2^31");
+    if (!aligned16(d_x) || !aligned16(d_weight) || !aligned16(d_out) ||
+        (d_residual && !aligned16(d_residual)) || (d_sum && !aligned16(d_sum)))
+        return fail(REALM_INVALID_ARGUMENT, "rms_norm: pointers must be 16-byte aligned");
+    if (d_sum && (d_sum == d_x || d_sum == d_residual))
+        return fail(REALM_INVALID_ARGUMENT, "rms_norm: the sum may not overwrite an input");
+    CHECK(ensure_init());
+    hipStream_t s;
+    CHECK(pick_stream(stream, &s));
+    int ih = (int)hidden;
+    void *args[] = {(void *)&d_x, (void *)&d_residual, (void *)&d_weight, &eps, &ih, &d_sum,
+                    &d_out};
+    return launch("realm_rms_norm", dim3((unsigned)rows), dim3(256), 0, s, args);
+}
+
+REALM_API int realm_hip_swiglu_dev(const float *d_gate, const float *d_up, size_t n, float *d_out,
+                                   void *stream)
+{
+    if (n == 0)
+        return REALM_OK;
+    if (!d_gate || !d_up || !d_out)
+        return fail(REALM_INVALID_ARGUMENT, "swiglu: null pointer argument");
+    if (n % 4 || !aligned16(d_gate) || !aligned16(d_up) || !aligned16(d_out))
+        return fail(REALM_INVALID_ARGUMENT,
+                    "swiglu: n must be a multiple of 4 and pointers 16-byte aligned");
+    CHECK(ensure_init());
+    hipStream_t s;
+    CHECK(pick_stream(stream, &s));
+    size_t n4 = n / 4;
+    const unsigned wgs = (unsigned)std::min<size_t>((n4 + 255) / 256, (size_t)g_dev.cu_count * 8);
+    void *args[] = {(void *)&d_gate, (void *)&d_up, &n4, &d_out};
+    return launch("realm_swiglu", dim3(wgs), dim3(256), 0, s, args);
+}
+
 REALM_API int realm_hip_fused_dequant_matmul_q4k(const void *blocks, size_t n_blocks,
                                                  const float *input, size_t input_len,
                                                  size_t batch_size, size_t n, size_t k,
