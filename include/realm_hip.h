@@ -261,6 +261,35 @@ int realm_hip_rms_norm_dev(const float *d_x, const float *d_residual, const floa
 int realm_hip_swiglu_dev(const float *d_gate, const float *d_up, size_t n, float *d_out,
                          void *stream);
 
+/* RoPE in place on x [seq_len, num_heads, head_dim] (MultiHeadAttention::
+ * apply_rope, crates/realm-models/src/attention.rs:171-235): interleaved
+ * pairs (i, i+1), freq = 1 / theta^(i / head_dim), angle = (start_pos + s)
+ * freq.  head_dim even, x 8-byte aligned. */
+int realm_hip_rope_dev(float *d_x, size_t seq_len, size_t num_heads, size_t head_dim,
+                       size_t start_pos, float theta, void *stream);
+
+/* Causal attention of seq_len query tokens at absolute positions position..
+ * over kv_len cached tokens (MultiHeadAttention::compute_attention,
+ * attention.rs:300-380, with StandardAttention,
+ * crates/realm-runtime/src/attention/standard.rs:36-210): q and out are
+ * [seq_len, num_heads, head_dim], the caches [kv_len, num_kv_heads,
+ * head_dim] (the KVCache layout, crates/realm-models/src/kv_cache.rs:44-70);
+ * query t sees keys j <= position + t, head h reads KV head
+ * h / (num_heads / num_kv_heads) (repeat_kv, attention.rs:272-296), scale
+ * 1/sqrt(head_dim).  head_dim divides 256; kv_len beyond what one
+ * workgroup's LDS holds for the scores -> REALM_BACKEND_UNSUPPORTED. */
+int realm_hip_attention_dev(const float *d_q, const float *d_k_cache, const float *d_v_cache,
+                            size_t seq_len, size_t kv_len, size_t position, size_t num_heads,
+                            size_t num_kv_heads, size_t head_dim, float *d_out, void *stream);
+
+/* KVCache::append (kv_cache.rs:44-70): copy seq_len rows of kv_dim keys and
+ * values into the device caches after the cur_len cached rows; more than
+ * max_len rows -> REALM_MODEL_PARSE_ERROR ("KV cache overflow", as the
+ * reference's Error::ParseError). */
+int realm_hip_kv_append_dev(const float *d_k, const float *d_v, size_t seq_len, size_t kv_dim,
+                            size_t cur_len, size_t max_len, float *d_k_cache, float *d_v_cache,
+                            void *stream);
+
 /* ------------------------------------------------------ GGUF model images */
 
 /* The transformer shape a GGUF image declares: GGUFParser::extract_config

@@ -91,6 +91,13 @@ SIGNATURES = {
     "realm_hip_rms_norm_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_float, c_size_t, c_size_t,
                                        c_void_p, c_void_p, c_void_p]),
     "realm_hip_swiglu_dev": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p, c_void_p]),
+    "realm_hip_rope_dev": (c_int, [c_void_p, c_size_t, c_size_t, c_size_t, c_size_t, c_float,
+                                   c_void_p]),
+    "realm_hip_attention_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_size_t,
+                                        c_size_t, c_size_t, c_size_t, c_size_t, c_void_p,
+                                        c_void_p]),
+    "realm_hip_kv_append_dev": (c_int, [c_void_p, c_void_p, c_size_t, c_size_t, c_size_t,
+                                        c_size_t, c_void_p, c_void_p, c_void_p]),
 }
 
 _lib = None

@@ -336,6 +336,27 @@ class HipGpuBackend:
         self._check(self.lib.realm_hip_swiglu_dev(c_void_p(d_gate), c_void_p(d_up), n,
                                                   c_void_p(d_out), c_void_p(stream or 0)))
 
+    def rope_dev(self, d_x: int, seq_len: int, num_heads: int, head_dim: int, start_pos: int,
+                 theta: float, stream=None) -> None:
+        """MultiHeadAttention::apply_rope in place (attention.rs:171-235)."""
+        self._check(self.lib.realm_hip_rope_dev(c_void_p(d_x), seq_len, num_heads, head_dim,
+                                                start_pos, theta, c_void_p(stream or 0)))
+
+    def attention_dev(self, d_q: int, d_k_cache: int, d_v_cache: int, seq_len: int, kv_len: int,
+                      position: int, num_heads: int, num_kv_heads: int, head_dim: int,
+                      d_out: int, stream=None) -> None:
+        """Causal GQA attention over a device KV cache (attention.rs:300-380)."""
+        self._check(self.lib.realm_hip_attention_dev(
+            c_void_p(d_q), c_void_p(d_k_cache), c_void_p(d_v_cache), seq_len, kv_len, position,
+            num_heads, num_kv_heads, head_dim, c_void_p(d_out), c_void_p(stream or 0)))
+
+    def kv_append_dev(self, d_k: int, d_v: int, seq_len: int, kv_dim: int, cur_len: int,
+                      max_len: int, d_k_cache: int, d_v_cache: int, stream=None) -> None:
+        """KVCache::append (kv_cache.rs:44-70) into device caches."""
+        self._check(self.lib.realm_hip_kv_append_dev(
+            c_void_p(d_k), c_void_p(d_v), seq_len, kv_dim, cur_len, max_len, c_void_p(d_k_cache),
+            c_void_p(d_v_cache), c_void_p(stream or 0)))
+
 
 __all__ = ["HipGpuBackend", "RealmError", "InvalidShape", "BackendError", "DeviceBuffer",
            "DTYPE_F32", "DTYPE_F16"]

@@ -1157,6 +1157,80 @@ REALM_API int realm_hip_swiglu_dev(const float *d_gate, const float *d_up, size_
     return launch("realm_swiglu", dim3(wgs), dim3(256), 0, s, args);
 }
 
+REALM_API int realm_hip_rope_dev(float *d_x, size_t seq_len, size_t num_heads, size_t head_dim,
+                                size_t start_pos, float theta, void *stream)
+{
+    if (seq_len == 0 || num_heads == 0)
+        return REALM_OK;
+    if (!d_x || head_dim == 0 || head_dim % 2 || ((uintptr_t)d_x & 7))
+        return fail(REALM_INVALID_ARGUMENT, "rope: head_dim must be even, x 8-byte aligned");
+    const size_t pairs = seq_len * num_heads * (head_dim / 2);
+    if (start_pos + seq_len > (size_t)INT32_MAX || pairs / 256 >= (size_t)UINT32_MAX ||
+        head_dim > (size_t)INT32_MAX || num_heads > (size_t)INT32_MAX)
+        return fail(REALM_INVALID_ARGUMENT, "rope: sizes exceed 2^31-1");
+    CHECK(ensure_init());
+    hipStream_t s;
+    CHECK(pick_stream(stream, &s));
+    int is = (int)seq_len, ih = (int)num_heads, id = (int)head_dim, ip = (int)start_pos;
+    void *args[] = {&d_x, &is, &ih, &id, &ip, &theta};
+    return launch("realm_rope", dim3((unsigned)((pairs + 255) / 256)), dim3(256), 0, s, args);
+}
+
+REALM_API int realm_hip_attention_dev(const float *d_q, const float *d_k_cache,
+                                      const float *d_v_cache, size_t seq_len, size_t kv_len,
+                                      size_t position, size_t num_heads, size_t num_kv_heads,
+                                      size_t head_dim, float *d_out, void *stream)
+{
+    if (seq_len == 0 || num_heads == 0)
+        return REALM_OK;
+    if (!d_q || !d_out || (kv_len && (!d_k_cache || !d_v_cache)))
+        return fail(REALM_INVALID_ARGUMENT, "attention: null pointer argument");
+    if (head_dim < 4 || head_dim > 256 || 256 % head_dim || num_kv_heads == 0 ||
+        num_heads % num_kv_heads)
+        return fail(REALM_INVALID_ARGUMENT,
+                    "attention: head_dim must divide 256 (4..256) and kv heads divide heads");
+    if (!aligned16(d_k_cache) || !aligned16(d_v_cache))
+        return fail(REALM_INVALID_ARGUMENT, "attention: caches must be 16-byte aligned");
+    if (seq_len * num_heads > (size_t)UINT32_MAX || position + seq_len > (size_t)INT32_MAX ||
+        kv_len > (size_t)INT32_MAX || num_heads > (size_t)INT32_MAX)
+        return fail(REALM_INVALID_ARGUMENT, "attention: sizes exceed 2^31-1");
+    CHECK(ensure_init());
+    const size_t lds = (head_dim + kv_len + 256) * sizeof(float);
+    if (lds + 64 > g_dev.max_lds)
+        return fail(REALM_BACKEND_UNSUPPORTED,
+                    "attention: " + std::to_string(kv_len) + " cached keys exceed the LDS");
+    hipStream_t s;
+    CHECK(pick_stream(stream, &s));
+    int ikv = (int)kv_len, ipos = (int)position, ih = (int)num_heads, ikh = (int)num_kv_heads,
+        id = (int)head_dim;
+    float scale = 1.0f / std::sqrt((float)head_dim);
+    void *args[] = {(void *)&d_q, (void *)&d_k_cache, (void *)&d_v_cache, &ikv, &ipos, &ih, &ikh,
+                    &id, &scale, &d_out};
+    return launch("realm_attention", dim3((unsigned)(seq_len * num_heads)), dim3(256), lds, s,
+                  args);
+}
+
+REALM_API int realm_hip_kv_append_dev(const float *d_k, const float *d_v, size_t seq_len,
+                                      size_t kv_dim, size_t cur_len, size_t max_len,
+                                      float *d_k_cache, float *d_v_cache, void *stream)
+{
+    if (cur_len + seq_len > max_len)
+        return fail(REALM_MODEL_PARSE_ERROR, "KV cache overflow: " + std::to_string(cur_len) +
+                                                 " + " + std::to_string(seq_len) + " > " +
+                                                 std::to_string(max_len));
+    if (seq_len == 0 || kv_dim == 0)
+        return REALM_OK;
+    if (!d_k || !d_v || !d_k_cache || !d_v_cache)
+        return fail(REALM_INVALID_ARGUMENT, "kv_append: null pointer argument");
+    CHECK(ensure_init());
+    hipStream_t s;
+    CHECK(pick_stream(stream, &s));
+    const size_t off = cur_len * kv_dim, bytes = seq_len * kv_dim * sizeof(float);
+    HIP_TRY(hipMemcpyAsync(d_k_cache + off, d_k, bytes, hipMemcpyDeviceToDevice, s));
+    HIP_TRY(hipMemcpyAsync(d_v_cache + off, d_v, bytes, hipMemcpyDeviceToDevice, s));
+    return REALM_OK;
+}
+
 REALM_API int realm_hip_fused_dequant_matmul_q4k(const void *blocks, size_t n_blocks,
                                                  const float *input, size_t input_len,
                                                  size_t batch_size, size_t n, size_t k,

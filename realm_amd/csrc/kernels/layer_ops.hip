@@ -89,3 +89,111 @@ extern "C" __global__ __launch_bounds__(256) void realm_swiglu(const float4 *gat
         out[i] = o;
     }
 }
+
+// RoPE of realm's MultiHeadAttention::apply_rope (crates/realm-models/src/
+// attention.rs:171-235), in place on x [seq][heads][head_dim]: interleaved
+// pairs (i, i + 1), freq = 1 / theta^(i / head_dim), angle = (start + s) *
+// freq, in the reference's f32 operation order.  One thread per pair.
+extern "C" __global__ __launch_bounds__(256) void realm_rope(float *x, int seq, int heads,
+                                                             int head_dim, int start, float theta)
+{
+    const int half = head_dim >> 1;
+    const size_t pairs = (size_t)seq * heads * half;
+    const size_t p = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (p >= pairs)
+        return;
+    const int i = 2 * (int)(p % half);
+    const int s = (int)(p / ((size_t)heads * half));
+    const float freq = 1.0f / powf(theta, (float)i / (float)head_dim);
+    const float angle = (float)(start + s) * freq;
+    const float c = cosf(angle), sn = sinf(angle);
+    float2 *v = reinterpret_cast<float2 *>(x) + p;
+    const float2 a = *v;
+    *v = make_float2(a.x * c - a.y * sn, a.x * sn + a.y * c);
+}
+
+namespace {
+
+REALM_DEV float wave_max(float v)
+{
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1)
+        v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+} // namespace
+
+// Causal attention over a KV cache (MultiHeadAttention::compute_attention,
+// attention.rs:300-380, with StandardAttention, crates/realm-runtime/src/
+// attention/standard.rs:36-210): query token t (absolute position
+// position + t) of head h attends to cached keys j <= position + t of KV
+// head h / (heads / kv_heads); scores (q . k_j) / sqrt(head_dim), softmax
+// with the maximum subtracted, weights normalized by their sum, output
+// sum_j p_j v_j.  One workgroup of 256 threads per (token, head); the
+// scores of the visible keys live in dynamic LDS after q.  head_dim divides
+// 256 (the host checks); the output sums run over head_dim x (256 /
+// head_dim) threads, key slices summed in slice order.
+extern "C" __global__ __launch_bounds__(256) void realm_attention(
+    const float *q, const float *kc, const float *vc, int kv_len, int position, int heads,
+    int kv_heads, int head_dim, float scale, float *out)
+{
+    extern __shared__ float smem[];
+    __shared__ float red[8];
+    float *qs = smem;              // head_dim
+    float *sc = smem + head_dim;   // visible keys
+    float *acc = sc + kv_len;      // 256 partial outputs
+    const int t = blockIdx.x / heads, h = blockIdx.x % heads;
+    const int kvh = h / (heads / kv_heads);
+    const int kv_dim = kv_heads * head_dim;
+    const int vis = min(kv_len, position + t + 1);
+    const float *qr = q + ((size_t)t * heads + h) * head_dim;
+    for (int d = threadIdx.x; d < head_dim; d += 256)
+        qs[d] = qr[d];
+    __syncthreads();
+    float mx = -INFINITY;
+    for (int j = threadIdx.x; j < vis; j += 256) {
+        const float *kr = kc + (size_t)j * kv_dim + (size_t)kvh * head_dim;
+        float dot = 0.f;
+        for (int d = 0; d < head_dim; d += 4) {
+            const float4 k4 = *reinterpret_cast<const float4 *>(kr + d);
+            dot += qs[d] * k4.x;
+            dot += qs[d + 1] * k4.y;
+            dot += qs[d + 2] * k4.z;
+            dot += qs[d + 3] * k4.w;
+        }
+        const float s = dot * scale;
+        sc[j] = s;
+        mx = fmaxf(mx, s);
+    }
+    mx = wave_max(mx);
+    if ((threadIdx.x & 63) == 0)
+        red[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float sum = 0.f;
+    for (int j = threadIdx.x; j < vis; j += 256) {
+        const float e = expf(sc[j] - mx);
+        sc[j] = e;
+        sum += e;
+    }
+    sum = wave_sum(sum);
+    if ((threadIdx.x & 63) == 0)
+        red[4 + (threadIdx.x >> 6)] = sum;
+    __syncthreads();
+    sum = red[4] + red[5] + red[6] + red[7];
+    const float inv = sum > 0.f ? 1.f / sum : 1.f;
+    const int parts = 256 / head_dim;
+    const int d = threadIdx.x % head_dim, part = threadIdx.x / head_dim;
+    float a = 0.f;
+    for (int j = part; j < vis; j += parts)
+        a += (sc[j] * inv) * vc[(size_t)j * kv_dim + (size_t)kvh * head_dim + d];
+    acc[threadIdx.x] = a;
+    __syncthreads();
+    if (part == 0) {
+        float o = acc[d];
+        for (int p = 1; p < parts; ++p)
+            o += acc[p * head_dim + d];
+        out[((size_t)t * heads + h) * head_dim + d] = o;
+    }
+}

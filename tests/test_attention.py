@@ -1,0 +1,152 @@
+"""RoPE, the KV-cache append and causal GQA attention: the oracle's numpy
+restatement pinned by closed forms and an fp64 brute force (CPU), the HIP
+kernels through the C ABI against it (GPU)."""
+import numpy as np
+import pytest
+
+from conftest import rel_l2
+from oracle import attention as oa
+
+
+def _fp64_attention(q, k, v, seq_len, kv_len, position, heads, kv_heads, hd):
+    q = q.reshape(seq_len, heads, hd).astype(np.float64)
+    k = k.reshape(kv_len, kv_heads, hd).astype(np.float64)
+    v = v.reshape(kv_len, kv_heads, hd).astype(np.float64)
+    out = np.zeros((seq_len, heads, hd))
+    for i in range(seq_len):
+        for h in range(heads):
+            kh = h // (heads // kv_heads)
+            vis = min(kv_len, position + i + 1)
+            s = k[:vis, kh] @ q[i, h] / np.sqrt(hd)
+            p = np.exp(s - s.max())
+            out[i, h] = (p / p.sum()) @ v[:vis, kh]
+    return out.reshape(-1)
+
+
+# --------------------------------------------------------------- oracle
+
+def test_oracle_rope_closed_forms():
+    g = np.random.default_rng(0)
+    x = g.standard_normal(2 * 4 * 64).astype(np.float32)
+    assert np.array_equal(oa.rope(x[:256], 0, 1, 4, 64, 10000.0), x[:256])  # position 0
+    y = oa.rope(x, 5, 2, 4, 64, 10000.0).reshape(-1, 2)
+    assert np.allclose(np.hypot(y[:, 0], y[:, 1]), np.hypot(*x.reshape(-1, 2).T), rtol=1e-5)
+    # pair 0 (freq 1) of position p rotates by p radians
+    z = oa.rope(np.array([1.0, 0.0] * 32, np.float32), 3, 1, 1, 64, 10000.0)
+    assert np.allclose(z[:2], [np.cos(3.0), np.sin(3.0)], atol=1e-6)
+
+
+def test_oracle_attention_closed_forms_and_fp64():
+    g = np.random.default_rng(1)
+    hd, heads, kvh = 64, 8, 2
+    q = g.standard_normal(heads * hd).astype(np.float32)
+    k = g.standard_normal(kvh * hd).astype(np.float32)
+    v = g.standard_normal(kvh * hd).astype(np.float32)
+    out = oa.attention(q, k, v, 1, 1, 0, heads, kvh, hd).reshape(heads, hd)
+    assert np.array_equal(out, np.repeat(v.reshape(kvh, hd), heads // kvh, axis=0))  # one key
+    kk = np.tile(k, 5)                      # five equal keys: uniform weights
+    vv = g.standard_normal(5 * kvh * hd).astype(np.float32)
+    out = oa.attention(q, kk, vv, 1, 5, 4, heads, kvh, hd).reshape(heads, hd)
+    want = np.repeat(vv.reshape(5, kvh, hd).mean(0), heads // kvh, axis=0)
+    assert np.allclose(out, want, rtol=1e-5, atol=1e-6)
+    for seq, kv, pos in ((3, 10, 7), (4, 4, 0), (1, 33, 32)):
+        q = g.standard_normal(seq * heads * hd).astype(np.float32)
+        k = g.standard_normal(kv * kvh * hd).astype(np.float32)
+        v = g.standard_normal(kv * kvh * hd).astype(np.float32)
+        got = oa.attention(q, k, v, seq, kv, pos, heads, kvh, hd)
+        assert rel_l2(got, _fp64_attention(q, k, v, seq, kv, pos, heads, kvh, hd)) < 1e-5
+
+
+def test_oracle_kv_append_overflow():
+    kc, vc = np.zeros(4 * 8, np.float32), np.zeros(4 * 8, np.float32)
+    n = oa.kv_append(kc, vc, 0, 4, np.ones(24, np.float32), np.ones(24, np.float32), 8)
+    assert n == 3 and kc[:24].sum() == 24 and kc[24:].sum() == 0
+    with pytest.raises(oa.KVCacheError):
+        oa.kv_append(kc, vc, 3, 4, np.ones(16, np.float32), np.ones(16, np.float32), 8)
+
+
+# ------------------------------------------------------------------ GPU
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seq,heads,hd,start", [(1, 32, 128, 0), (1, 32, 128, 4095),
+                                                (5, 8, 64, 17), (3, 64, 128, 100)])
+def test_rope(backend, seq, heads, hd, start):
+    g = np.random.default_rng(seq * 100 + start)
+    x = g.standard_normal(seq * heads * hd).astype(np.float32)
+    d = backend.alloc(x.nbytes).upload(x)
+    try:
+        backend.rope_dev(d.ptr, seq, heads, hd, start, 10000.0)
+        backend.synchronize()
+        got = d.download(np.float32, x.size)
+    finally:
+        d.close()
+    want = oa.rope(x, start, seq, heads, hd, 10000.0)
+    # a 1-ulp difference between two libms' powf in freq moves the f32 angle
+    # by position x 2^-23 relative: the bound is 2 such ulps at the largest
+    # position (the reference's Rust powf has the same freedom)
+    tol = 1e-5 + 2.4e-7 * (start + seq)
+    assert np.allclose(got, want, rtol=0, atol=tol * np.abs(x).max())
+    assert rel_l2(got, want) < tol
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seq,kv,pos,heads,kvh,hd", [
+    (1, 1, 0, 32, 32, 128),        # first decode token
+    (1, 300, 299, 32, 8, 128),     # decode with GQA (LLaMA-70B head ratio)
+    (1, 2048, 2047, 32, 32, 128),  # long context
+    (7, 7, 0, 8, 2, 64),           # prefill chunk from empty
+    (5, 20, 15, 16, 4, 64),        # prefill chunk after 15 cached tokens
+    (3, 40, 10, 4, 4, 256),        # cache longer than the visible keys
+])
+def test_attention(backend, seq, kv, pos, heads, kvh, hd):
+    g = np.random.default_rng(seq * 7 + kv)
+    q = g.standard_normal(seq * heads * hd).astype(np.float32)
+    k = g.standard_normal(kv * kvh * hd).astype(np.float32)
+    v = g.standard_normal(kv * kvh * hd).astype(np.float32)
+    dq, dk, dv = (backend.alloc(a.nbytes).upload(a) for a in (q, k, v))
+    do = backend.alloc(q.nbytes)
+    try:
+        backend.attention_dev(dq.ptr, dk.ptr, dv.ptr, seq, kv, pos, heads, kvh, hd, do.ptr)
+        backend.synchronize()
+        got = do.download(np.float32, q.size)
+    finally:
+        for b in (dq, dk, dv, do):
+            b.close()
+    want = oa.attention(q, k, v, seq, kv, pos, heads, kvh, hd)
+    assert rel_l2(got, want) < 1e-5
+
+
+@pytest.mark.gpu
+def test_kv_append_then_attention(backend):
+    """Decode three steps into a device cache (append, then attend) against
+    the oracle's cache; the overflowing append fails with ParseError (4)."""
+    from realm_amd.backend import RealmError
+    heads, kvh, hd, max_len = 8, 2, 64, 6
+    kv_dim = kvh * hd
+    g = np.random.default_rng(3)
+    kc_ref, vc_ref = np.zeros(max_len * kv_dim, np.float32), np.zeros(max_len * kv_dim, np.float32)
+    dkc, dvc = backend.alloc(kc_ref.nbytes), backend.alloc(vc_ref.nbytes)
+    cur = 0
+    try:
+        for step, n in enumerate((3, 1, 2)):
+            k = g.standard_normal(n * kv_dim).astype(np.float32)
+            v = g.standard_normal(n * kv_dim).astype(np.float32)
+            q = g.standard_normal(n * heads * hd).astype(np.float32)
+            dk, dv, dq = (backend.alloc(a.nbytes).upload(a) for a in (k, v, q))
+            do = backend.alloc(q.nbytes)
+            backend.kv_append_dev(dk.ptr, dv.ptr, n, kv_dim, cur, max_len, dkc.ptr, dvc.ptr)
+            new = oa.kv_append(kc_ref, vc_ref, cur, max_len, k, v, kv_dim)
+            backend.attention_dev(dq.ptr, dkc.ptr, dvc.ptr, n, new, cur, heads, kvh, hd, do.ptr)
+            backend.synchronize()
+            want = oa.attention(q, kc_ref[:new * kv_dim], vc_ref[:new * kv_dim], n, new, cur,
+                                heads, kvh, hd)
+            assert rel_l2(do.download(np.float32, q.size), want) < 1e-5, step
+            cur = new
+            for b in (dk, dv, dq, do):
+                b.close()
+        with pytest.raises(RealmError) as e:
+            backend.kv_append_dev(dkc.ptr, dvc.ptr, 1, kv_dim, cur, max_len, dkc.ptr, dvc.ptr)
+        assert e.value.code == 4
+    finally:
+        dkc.close()
+        dvc.close()
