@@ -290,6 +290,37 @@ int realm_hip_kv_append_dev(const float *d_k, const float *d_v, size_t seq_len, 
                             size_t cur_len, size_t max_len, float *d_k_cache, float *d_v_cache,
                             void *stream);
 
+/* Residual add out = a + b (CandleCpuBackend::add where realm_forward_layer
+ * adds the attention and FFN outputs, memory64_host.rs:2318-2324,
+ * 2452-2458).  n a multiple of 4, pointers 16-byte aligned. */
+int realm_hip_add_dev(const float *d_a, const float *d_b, size_t n, float *d_out, void *stream);
+
+/* One decoder layer's weights and shape for realm_hip_forward_layer_dev:
+ * registered weight handles (Wq, Wo [hidden x hidden], Wk, Wv [kv_heads *
+ * head_dim x hidden], W_gate, W_up [intermediate x hidden], W_down
+ * [hidden x intermediate]), the two norm weight vectors on the device, and
+ * the TransformerConfig fields the layer reads (gguf.rs:212-280). */
+typedef struct realm_layer {
+    uint64_t wq, wk, wv, wo, w_gate, w_up, w_down;
+    const float *attn_norm, *ffn_norm;
+    uint32_t hidden, num_heads, num_kv_heads, head_dim, intermediate;
+    float rms_norm_eps, rope_theta;
+} realm_layer;
+
+/* realm_forward_layer (crates/realm-runtime/src/memory64_host.rs:1915-2472)
+ * on the device for seq_len tokens at absolute positions position.. :
+ * RMSNorm, Q/K/V, RoPE, KV-cache append (K and V rows written at row
+ * `position` of the [max_seq_len, kv_heads * head_dim] caches), causal
+ * attention over the position + seq_len cached rows, Wo, residual, FFN
+ * RMSNorm, gate/up, SwiGLU, W_down, residual.  d_hidden and d_out are
+ * [seq_len, hidden] f32 (they may not overlap).  Asynchronous on `stream`;
+ * every step is a kernel or a library product on that stream, so a decode
+ * step can be captured in a HIP graph after one eager call.  Overflowing the
+ * cache -> REALM_MODEL_PARSE_ERROR, as KVCache::append. */
+int realm_hip_forward_layer_dev(const realm_layer *layer, const float *d_hidden, size_t seq_len,
+                                size_t position, float *d_k_cache, float *d_v_cache,
+                                size_t max_seq_len, float *d_out, void *stream);
+
 /* ------------------------------------------------------ GGUF model images */
 
 /* The transformer shape a GGUF image declares: GGUFParser::extract_config

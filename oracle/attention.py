@@ -67,3 +67,33 @@ def attention(q, k, v, seq_len: int, kv_len: int, position: int, num_heads: int,
                 e = (e / s).astype(np.float32)
             out[i, h, :] = (e @ vr[:, h, :]).astype(np.float32)
     return out.reshape(-1)
+
+
+def forward_layer(matmul, x, w, norms, cfg, k_cache, v_cache, position: int, seq_len: int):
+    """realm_forward_layer's decoder layer (crates/realm-runtime/src/
+    memory64_host.rs:2059-2458) composed from the restated steps:
+    matmul(name, x, m) -> [m, n] is the caller's fused dequant x matmul
+    (the oracle's candle_fused); w names the seven projections; norms holds
+    the two norm vectors; the caches are [max_len * kv_dim] arrays whose
+    rows position.. are written (KVCache::append).  Returns [seq_len, hidden]."""
+    from oracle import layer_ops as lo
+    H, heads, kvh, hd = cfg["hidden"], cfg["heads"], cfg["kv_heads"], cfg["head_dim"]
+    kv_dim = kvh * hd
+    eps, theta = cfg["eps"], cfg["theta"]
+    x = np.asarray(x, np.float32).reshape(seq_len, H)
+    normed, _ = lo.rms_norm(x, norms["attn"], eps)
+    q = matmul("wq", normed, seq_len).reshape(-1)
+    k = matmul("wk", normed, seq_len).reshape(-1)
+    v = matmul("wv", normed, seq_len).reshape(-1)
+    q = rope(q, position, seq_len, heads, hd, theta)
+    k = rope(k, position, seq_len, kvh, hd, theta)
+    kv_len = kv_append(k_cache, v_cache, position, len(k_cache) // kv_dim, k, v, kv_dim)
+    att = attention(q, k_cache[:kv_len * kv_dim], v_cache[:kv_len * kv_dim], seq_len, kv_len,
+                    position, heads, kvh, hd)
+    o = matmul("wo", att.reshape(seq_len, H), seq_len)
+    ffn_normed, h2 = lo.rms_norm(x, norms["ffn"], eps, residual=o)
+    gate = matmul("w_gate", ffn_normed, seq_len)
+    up = matmul("w_up", ffn_normed, seq_len)
+    act = lo.swiglu(gate, up)
+    down = matmul("w_down", act, seq_len)
+    return (h2 + down).astype(np.float32)

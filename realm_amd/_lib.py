@@ -98,6 +98,9 @@ SIGNATURES = {
                                         c_void_p]),
     "realm_hip_kv_append_dev": (c_int, [c_void_p, c_void_p, c_size_t, c_size_t, c_size_t,
                                         c_size_t, c_void_p, c_void_p, c_void_p]),
+    "realm_hip_add_dev": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p, c_void_p]),
+    "realm_hip_forward_layer_dev": (c_int, [c_void_p, c_void_p, c_size_t, c_size_t, c_void_p,
+                                            c_void_p, c_size_t, c_void_p, c_void_p]),
 }
 
 _lib = None

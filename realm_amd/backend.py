@@ -14,6 +14,7 @@ LoRA, the candle_matmul host-function surface, and device-buffer plumbing.
 """
 from __future__ import annotations
 
+import ctypes
 from ctypes import byref, c_float, c_int, c_size_t, c_uint64, c_void_p
 
 import numpy as np
@@ -357,6 +358,29 @@ class HipGpuBackend:
             c_void_p(d_k), c_void_p(d_v), seq_len, kv_dim, cur_len, max_len, c_void_p(d_k_cache),
             c_void_p(d_v_cache), c_void_p(stream or 0)))
 
+    def add_dev(self, d_a: int, d_b: int, n: int, d_out: int, stream=None) -> None:
+        self._check(self.lib.realm_hip_add_dev(c_void_p(d_a), c_void_p(d_b), n,
+                                               c_void_p(d_out), c_void_p(stream or 0)))
 
-__all__ = ["HipGpuBackend", "RealmError", "InvalidShape", "BackendError", "DeviceBuffer",
-           "DTYPE_F32", "DTYPE_F16"]
+    def forward_layer_dev(self, layer: "RealmLayer", d_hidden: int, seq_len: int, position: int,
+                          d_k_cache: int, d_v_cache: int, max_seq_len: int, d_out: int,
+                          stream=None) -> None:
+        """realm_forward_layer on the device (memory64_host.rs:1915-2472)."""
+        self._check(self.lib.realm_hip_forward_layer_dev(
+            ctypes.byref(layer), c_void_p(d_hidden), seq_len, position, c_void_p(d_k_cache),
+            c_void_p(d_v_cache), max_seq_len, c_void_p(d_out), c_void_p(stream or 0)))
+
+
+class RealmLayer(ctypes.Structure):
+    """struct realm_layer of include/realm_hip.h."""
+    _fields_ = [("wq", c_uint64), ("wk", c_uint64), ("wv", c_uint64), ("wo", c_uint64),
+                ("w_gate", c_uint64), ("w_up", c_uint64), ("w_down", c_uint64),
+                ("attn_norm", c_void_p), ("ffn_norm", c_void_p),
+                ("hidden", ctypes.c_uint32), ("num_heads", ctypes.c_uint32),
+                ("num_kv_heads", ctypes.c_uint32), ("head_dim", ctypes.c_uint32),
+                ("intermediate", ctypes.c_uint32), ("rms_norm_eps", ctypes.c_float),
+                ("rope_theta", ctypes.c_float)]
+
+
+__all__ = ["HipGpuBackend", "RealmLayer", "RealmError", "InvalidShape", "BackendError",
+           "DeviceBuffer", "DTYPE_F32", "DTYPE_F16"]

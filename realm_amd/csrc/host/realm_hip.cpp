@@ -236,7 +236,8 @@ int pick_stream(void *user, hipStream_t *s)
 
 // Per-stream scratch buffers (grow-only).  Work on one stream is ordered, so
 // reusing a stream's buffers for its next call is safe.
-enum Slot { WS_RAW, WS_WEIGHT, WS_X, WS_Y, WS_XH, WS_XL, WS_XM, WS_TS, WS_U, WS_IDS, WS_PART, WS_N };
+enum Slot { WS_RAW, WS_WEIGHT, WS_X, WS_Y, WS_XH, WS_XL, WS_XM, WS_TS, WS_U, WS_IDS, WS_PART,
+            WS_LAYER, WS_N };
 
 struct Workspace {
     void *buf[WS_N] = {};
@@ -1229,6 +1230,119 @@ REALM_API int realm_hip_kv_append_dev(const float *d_k, const float *d_v, size_t
     HIP_TRY(hipMemcpyAsync(d_k_cache + off, d_k, bytes, hipMemcpyDeviceToDevice, s));
     HIP_TRY(hipMemcpyAsync(d_v_cache + off, d_v, bytes, hipMemcpyDeviceToDevice, s));
     return REALM_OK;
+}
+
+REALM_API int realm_hip_add_dev(const float *d_a, const float *d_b, size_t n, float *d_out,
+                               void *stream)
+{
+    if (n == 0)
+        return REALM_OK;
+    if (!d_a || !d_b || !d_out)
+        return fail(REALM_INVALID_ARGUMENT, "add: null pointer argument");
+    if (n % 4 || !aligned16(d_a) || !aligned16(d_b) || !aligned16(d_out))
+        return fail(REALM_INVALID_ARGUMENT,
+                    "add: n must be a multiple of 4 and pointers 16-byte aligned");
+    CHECK(ensure_init());
+    hipStream_t s;
+    CHECK(pick_stream(stream, &s));
+    size_t n4 = n / 4;
+    const unsigned wgs = (unsigned)std::min<size_t>((n4 + 255) / 256, (size_t)g_dev.cu_count * 8);
+    void *args[] = {(void *)&d_a, (void *)&d_b, &n4, &d_out};
+    return launch("realm_add", dim3(wgs), dim3(256), 0, s, args);
+}
+
+// One decoder layer of realm_forward_layer (memory64_host.rs:2059-2458) on
+// the device, every step on `stream`: RMSNorm, Q/K/V in one grouped product
+// with K and V written straight into the cache rows of this call's tokens,
+// RoPE on Q and on those K rows, attention over the cache, Wo, the residual
+// add fused with the FFN norm, gate/up in one grouped product, SwiGLU,
+// W_down, the final residual add.
+REALM_API int realm_hip_forward_layer_dev(const realm_layer *L, const float *d_hidden,
+                                          size_t seq_len, size_t position, float *d_k_cache,
+                                          float *d_v_cache, size_t max_seq_len, float *d_out,
+                                          void *stream)
+{
+    if (!L || !d_hidden || !d_out || !d_k_cache || !d_v_cache || !L->attn_norm || !L->ffn_norm)
+        return fail(REALM_INVALID_ARGUMENT, "forward_layer: null pointer argument");
+    if (seq_len == 0)
+        return REALM_OK;
+    const size_t H = L->hidden, heads = L->num_heads, kvh = L->num_kv_heads, hd = L->head_dim,
+                 I = L->intermediate, kv_dim = kvh * hd;
+    if (H == 0 || heads * hd != H || kvh == 0 || heads % kvh || I == 0 || I % 4 || H % 4)
+        return fail(REALM_INVALID_ARGUMENT,
+                    "forward_layer: hidden must be heads x head_dim, kv heads divide heads, "
+                    "hidden and intermediate multiples of 4");
+    if (position + seq_len > max_seq_len)
+        return fail(REALM_MODEL_PARSE_ERROR, "KV cache overflow: " + std::to_string(position) +
+                                                 " + " + std::to_string(seq_len) + " > " +
+                                                 std::to_string(max_seq_len));
+    struct Want {
+        uint64_t h;
+        size_t n, k;
+    } want[7] = {{L->wq, H, H},     {L->wk, kv_dim, H}, {L->wv, kv_dim, H}, {L->wo, H, H},
+                 {L->w_gate, I, H}, {L->w_up, I, H},    {L->w_down, H, I}};
+    int type[7];
+    for (int i = 0; i < 7; ++i) {
+        const Want &x = want[i];
+        Weight w;
+        CHECK(get_weight(x.h, &w));
+        type[i] = w.type;
+        if (w.n != x.n || w.k != x.k)
+            return fail(REALM_INVALID_ARGUMENT,
+                        "forward_layer: weight " + std::to_string(x.h) + " is " +
+                            std::to_string(w.n) + " x " + std::to_string(w.k) + ", the layer needs " +
+                            std::to_string(x.n) + " x " + std::to_string(x.k));
+    }
+    auto weight_type = [&](uint64_t h) {
+        for (int i = 0; i < 7; ++i)
+            if (want[i].h == h)
+                return type[i];
+        return -1;
+    };
+    CHECK(ensure_init());
+    hipStream_t s;
+    CHECK(pick_stream(stream, &s));
+    // intermediates: normed / attention out / h2 / down [seq][H], q [seq][H],
+    // gate and up [seq][I], o [seq][H]
+    const size_t sh = align256(seq_len * H * 4), si = align256(seq_len * I * 4);
+    void *ws = nullptr;
+    CHECK(ws_get(s, WS_LAYER, 5 * sh + 2 * si, &ws));
+    uint8_t *base = static_cast<uint8_t *>(ws);
+    float *normed = (float *)base, *q = (float *)(base + sh), *att = (float *)(base + 2 * sh),
+          *h2 = (float *)(base + 3 * sh), *o = (float *)(base + 4 * sh),
+          *gate = (float *)(base + 5 * sh), *up = (float *)(base + 5 * sh + si);
+    float *k_rows = d_k_cache + position * kv_dim, *v_rows = d_v_cache + position * kv_dim;
+    CHECK(realm_hip_rms_norm_dev(d_hidden, nullptr, L->attn_norm, L->rms_norm_eps, seq_len, H,
+                                 nullptr, normed, s));
+    // matrices of one format share a grouped product (GGUF quant mixes
+    // often keep V or up in Q6_K: then separate products)
+    auto products = [&](const uint64_t *h, float *const *out, int n) {
+        bool same = true;
+        for (int i = 1; i < n; ++i)
+            same = same && weight_type(h[i]) == weight_type(h[0]);
+        if (same)
+            return realm_hip_weights_matmul_group_dev(h, n, normed, seq_len, out, s);
+        for (int i = 0; i < n; ++i)
+            if (int rc = realm_hip_weights_matmul_dev(h[i], normed, seq_len, out[i], s))
+                return rc;
+        return (int)REALM_OK;
+    };
+    const uint64_t qkv[3] = {L->wq, L->wk, L->wv};
+    float *const qkv_out[3] = {q, k_rows, v_rows};
+    CHECK(products(qkv, qkv_out, 3));
+    CHECK(realm_hip_rope_dev(q, seq_len, heads, hd, position, L->rope_theta, s));
+    CHECK(realm_hip_rope_dev(k_rows, seq_len, kvh, hd, position, L->rope_theta, s));
+    CHECK(realm_hip_attention_dev(q, d_k_cache, d_v_cache, seq_len, position + seq_len, position,
+                                  heads, kvh, hd, att, s));
+    CHECK(realm_hip_weights_matmul_dev(L->wo, att, seq_len, o, s));
+    CHECK(realm_hip_rms_norm_dev(d_hidden, o, L->ffn_norm, L->rms_norm_eps, seq_len, H, h2,
+                                 normed, s));
+    const uint64_t gu[2] = {L->w_gate, L->w_up};
+    float *const gu_out[2] = {gate, up};
+    CHECK(products(gu, gu_out, 2));
+    CHECK(realm_hip_swiglu_dev(gate, up, seq_len * I, gate, s));
+    CHECK(realm_hip_weights_matmul_dev(L->w_down, gate, seq_len, att, s));
+    return realm_hip_add_dev(h2, att, seq_len * H, d_out, s);
 }
 
 REALM_API int realm_hip_fused_dequant_matmul_q4k(const void *blocks, size_t n_blocks,

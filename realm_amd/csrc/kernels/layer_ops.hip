@@ -197,3 +197,16 @@ extern "C" __global__ __launch_bounds__(256) void realm_attention(
         out[((size_t)t * heads + h) * head_dim + d] = o;
     }
 }
+
+// Residual add out[i] = a[i] + b[i] (CandleCpuBackend::add as
+// realm_forward_layer uses it, memory64_host.rs:2452-2458), float4 per
+// thread over n4 vectors.
+extern "C" __global__ __launch_bounds__(256) void realm_add(const float4 *a, const float4 *b,
+                                                            size_t n4, float4 *out)
+{
+    const size_t stride = (size_t)gridDim.x * 256;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += stride) {
+        const float4 x = a[i], y = b[i];
+        out[i] = make_float4(x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w);
+    }
+}

@@ -150,3 +150,82 @@ def test_kv_append_then_attention(backend):
     finally:
         dkc.close()
         dvc.close()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mixed", [False, True])
+def test_forward_layer(backend, oracle, mixed):
+    """realm_hip_forward_layer_dev against the oracle's composition of the
+    reference's steps: a 5-token prefill from an empty cache, a 1-token and
+    a 3-token decode after it (the GEMV and MFMA product paths), and a call
+    that would overflow the cache.  mixed: V and up in Q6_K (separate
+    products), otherwise every projection in Q4_K (grouped products)."""
+    from realm_amd import synth
+    from realm_amd.backend import RealmError, RealmLayer
+    from realm_amd.formats import GGML_Q4_K, GGML_Q6_K
+    H, heads, kvh, hd, inter, max_len = 256, 4, 2, 64, 512, 12
+    kv_dim = kvh * hd
+    cfg = {"hidden": H, "heads": heads, "kv_heads": kvh, "head_dim": hd, "eps": 1e-5,
+           "theta": 10000.0}
+    g = synth.rng(40 + mixed)
+    shapes = {"wq": (H, H), "wk": (kv_dim, H), "wv": (kv_dim, H), "wo": (H, H),
+              "w_gate": (inter, H), "w_up": (inter, H), "w_down": (H, inter)}
+    types = {name: GGML_Q4_K for name in shapes}
+    if mixed:
+        types["wv"] = types["w_up"] = GGML_Q6_K
+    blocks = {name: synth.blocks(g, types[name], n, k) for name, (n, k) in shapes.items()}
+    # larger scales than the synthetic 1e-3 so that every step matters
+    for b in blocks.values():
+        b["d"] = (b["d"].view(np.float16) * np.float16(40)).view(np.uint16)
+    handles = {name: backend.register_weights(types[name], blocks[name], *shapes[name])
+               for name in shapes}
+    norms = {"attn": (1 + 0.1 * g.standard_normal(H)).astype(np.float32),
+             "ffn": (1 + 0.1 * g.standard_normal(H)).astype(np.float32)}
+    dn = {key: backend.alloc(v.nbytes).upload(v) for key, v in norms.items()}
+    layer = RealmLayer(wq=handles["wq"], wk=handles["wk"], wv=handles["wv"], wo=handles["wo"],
+                       w_gate=handles["w_gate"], w_up=handles["w_up"], w_down=handles["w_down"],
+                       attn_norm=dn["attn"].ptr, ffn_norm=dn["ffn"].ptr, hidden=H,
+                       num_heads=heads, num_kv_heads=kvh, head_dim=hd, intermediate=inter,
+                       rms_norm_eps=1e-5, rope_theta=10000.0)
+
+    def matmul(name, x, m):
+        n, k = shapes[name]
+        rc, y = oracle.candle_fused(types[name], blocks[name], np.ascontiguousarray(x), m, n, k)
+        assert rc == 0
+        return y.reshape(m, n)
+
+    kc_ref = np.zeros(max_len * kv_dim, np.float32)
+    vc_ref = np.zeros(max_len * kv_dim, np.float32)
+    dkc, dvc = backend.alloc(kc_ref.nbytes), backend.alloc(vc_ref.nbytes)
+    pos = 0
+    try:
+        for seq in (5, 1, 3):
+            x = g.standard_normal((seq, H)).astype(np.float32)
+            dx, dy = backend.alloc(x.nbytes).upload(x), backend.alloc(x.nbytes)
+            backend.forward_layer_dev(layer, dx.ptr, seq, pos, dkc.ptr, dvc.ptr, max_len, dy.ptr)
+            backend.synchronize()
+            got = dy.download(np.float32, x.size).reshape(seq, H)
+            want = forward = oa.forward_layer(matmul, x, blocks, norms, cfg, kc_ref, vc_ref, pos,
+                                              seq)
+            err = rel_l2(got, want)
+            delta = rel_l2(got - x, forward - x)  # the layer's own contribution
+            print(f"forward_layer mixed={mixed} seq={seq} pos={pos} rel_l2={err:.3e} "
+                  f"delta={delta:.3e}")
+            assert err < 1e-3 and delta < 1e-3, (seq, pos)
+            kc = dkc.download(np.float32, kc_ref.size)
+            assert rel_l2(kc[:(pos + seq) * kv_dim], kc_ref[:(pos + seq) * kv_dim]) < 1e-3
+            pos += seq
+            dx.close()
+            dy.close()
+        x = np.zeros((4, H), np.float32)
+        dx, dy = backend.alloc(x.nbytes).upload(x), backend.alloc(x.nbytes)
+        with pytest.raises(RealmError) as e:
+            backend.forward_layer_dev(layer, dx.ptr, 4, pos, dkc.ptr, dvc.ptr, max_len, dy.ptr)
+        assert e.value.code == 4
+        dx.close()
+        dy.close()
+    finally:
+        for h in handles.values():
+            backend.release_weights(h)
+        for b in list(dn.values()) + [dkc, dvc]:
+            b.close()
