@@ -161,6 +161,52 @@ def decode_roofline(be, model: Model7B, stream: int, reps: int) -> dict:
             "shape": "grouped W_gate + W_up, 2 x (11008 x 4096) Q4_K, batch 1"}
 
 
+def full_layers(be, model: Model7B, stream: int, reps: int, context: int = 512) -> dict:
+    """The whole decoder layer on the device (realm_hip_forward_layer_dev:
+    norm, Q/K/V, RoPE, KV append, attention, Wo, residual + norm, gate/up,
+    SwiGLU, W_down, residual) for all of the model's layers, each with its own
+    weights and KV cache (LLaMA-7B has 32 KV heads of 128, no GQA): a
+    prefill of `context - 1` tokens, then the decode step of the
+    next token captured in one HIP graph and replayed (every replay writes the
+    same cache row and attends over `context` keys)."""
+    from realm_amd.backend import RealmLayer
+    H, heads, kvh, hd, inter = 4096, 32, 32, 128, 11008
+    g = synth.rng(5)
+    norms = [(be.alloc(H * 4).upload((1 + 0.1 * g.standard_normal(H)).astype(np.float32)),
+              be.alloc(H * 4).upload((1 + 0.1 * g.standard_normal(H)).astype(np.float32)))
+             for _ in model.layers]
+    caches = [(be.alloc(context * kvh * hd * 4), be.alloc(context * kvh * hd * 4))
+              for _ in model.layers]
+    layers = []
+    for lw, (an, fn) in zip(model.layers, norms):
+        h = {name: handle for name, _, _, _, handle in lw}
+        layers.append(RealmLayer(wq=h["wq"], wk=h["wk"], wv=h["wv"], wo=h["wo"],
+                                 w_gate=h["w_gate"], w_up=h["w_up"], w_down=h["w_down"],
+                                 attn_norm=an.ptr, ffn_norm=fn.ptr, hidden=H, num_heads=heads,
+                                 num_kv_heads=kvh, head_dim=hd, intermediate=inter,
+                                 rms_norm_eps=1e-5, rope_theta=10000.0))
+    pre = context - 1
+    bufs = [be.alloc(pre * H * 4), be.alloc(pre * H * 4)]
+    bufs[0].upload(synth.activations(g, pre, H))
+
+    def run(seq, pos):
+        for i, L in enumerate(layers):
+            be.forward_layer_dev(L, bufs[i % 2].ptr, seq, pos, caches[i][0].ptr, caches[i][1].ptr,
+                                 context, bufs[(i + 1) % 2].ptr, stream=stream)
+
+    run(pre, 0)  # prefill fills rows 0 .. context - 2 of every cache
+    be.synchronize()
+    gr = capture(be, stream, lambda: run(1, pre))
+    time_graph(be, gr, stream, 3)
+    ms = time_graph(be, gr, stream, reps)
+    be.graph_release(gr)
+    for b in bufs + [x for pair in norms + caches for x in pair]:
+        b.close()
+    return {"ms_per_token": round(ms, 4), "tok_per_s": round(1e3 / ms, 1), "context": context,
+            "layers": len(model.layers),
+            "note": "all layer steps on the device; embedding, final norm and logits excluded"}
+
+
 def lora_overhead(be, stream: int, reps: int) -> dict:
     """Config 3: q_proj and v_proj (Q4_K 4096x4096) for 64 tokens, 16 adapters
     with ranks from {8,16,64}, Zipf(1.1) tenant ids, 10% without adapter.
@@ -422,7 +468,8 @@ def main() -> int:
     ap.add_argument("--traffic-probe", action="store_true",
                     help="no timing: one 256 MiB device copy (the counter reference) then "
                          "one gate/up GEMV launch per layer, for rocprofv3 --pmc runs")
-    ap.add_argument("--extra-only", choices=("batched", "lora", "prefill", "config4", "dense"),
+    ap.add_argument("--extra-only",
+                    choices=("batched", "lora", "prefill", "config4", "dense", "layer"),
                     help="run one of the extra measurements alone (for kernel profiles) and "
                          "print its result; no decode step, no JSON line")
     args = ap.parse_args()
@@ -487,9 +534,15 @@ def main() -> int:
                                "gb_per_s": round(value, 1)}}}
     roof = decode_roofline(be, model, stream, max(5, args.steps))
     log(f"roofline: {roof['achieved']} GB/s ({roof['frac'] * 100:.1f}% of peak)")
-    if args.extra_only == "batched":
+    if args.extra_only in ("batched", "layer"):
         args.skip_extra = False
+    if args.extra_only == "layer":
+        log(f"full layers: {full_layers(be, model, stream, max(5, args.steps))}")
+        model.close()
+        return 0
     if not args.skip_extra:
+        extra["full_layer_decode_7b"] = full_layers(be, model, stream, max(5, args.steps))
+        log(f"full layers: {extra['full_layer_decode_7b']}")
         for mb in (4, 16):
             gr = capture(be, stream, lambda: model.step(mb, stream))
             time_graph(be, gr, stream, 2)

@@ -133,7 +133,9 @@ REALM_DEV float wave_max(float v)
 // sum_j p_j v_j.  One workgroup of 256 threads per (token, head); the
 // scores of the visible keys live in dynamic LDS after q.  head_dim divides
 // 256 (the host checks); the output sums run over head_dim x (256 /
-// head_dim) threads, key slices summed in slice order.
+// head_dim) threads, key slices summed in slice order.  The shuffle
+// reduction of a key's partial dots stays inside its lpk-lane group
+// (xor offsets below lpk), so groups never mix.
 extern "C" __global__ __launch_bounds__(256) void realm_attention(
     const float *q, const float *kc, const float *vc, int kv_len, int position, int heads,
     int kv_heads, int head_dim, float scale, float *out)
@@ -151,21 +153,38 @@ extern "C" __global__ __launch_bounds__(256) void realm_attention(
     for (int d = threadIdx.x; d < head_dim; d += 256)
         qs[d] = qr[d];
     __syncthreads();
+    // Scores: a key row is read by head_dim / 4 adjacent lanes, one float4
+    // each (coalesced), and their partial dots meet by shuffles; a wave
+    // covers 256 / head_dim keys per step, the workgroup 1024 / head_dim.
+    const int lpk = head_dim >> 2, kpw = 64 / lpk;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int c = lane % lpk, sub = lane / lpk;
+    const float4 q4 = reinterpret_cast<const float4 *>(qs)[c];
+    // 8 steps per round, every key load of the round issued before the
+    // first is used (one memory round trip per round, not per step)
     float mx = -INFINITY;
-    for (int j = threadIdx.x; j < vis; j += 256) {
-        const float *kr = kc + (size_t)j * kv_dim + (size_t)kvh * head_dim;
-        float dot = 0.f;
-        for (int d = 0; d < head_dim; d += 4) {
-            const float4 k4 = *reinterpret_cast<const float4 *>(kr + d);
-            dot += qs[d] * k4.x;
-            dot += qs[d + 1] * k4.y;
-            dot += qs[d + 2] * k4.z;
-            dot += qs[d + 3] * k4.w;
+    for (int base = wave * kpw; base < vis; base += 32 * kpw) {
+        float4 k4[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int jc = min(base + u * 4 * kpw + sub, vis - 1);
+            k4[u] = *reinterpret_cast<const float4 *>(kc + (size_t)jc * kv_dim +
+                                                      (size_t)kvh * head_dim + 4 * c);
         }
-        const float s = dot * scale;
-        sc[j] = s;
-        mx = fmaxf(mx, s);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int j = base + u * 4 * kpw + sub;
+            float dot = q4.x * k4[u].x + q4.y * k4[u].y + q4.z * k4[u].z + q4.w * k4[u].w;
+            for (int off = lpk >> 1; off > 0; off >>= 1)
+                dot += __shfl_xor(dot, off, 64);
+            const float sv = dot * scale;
+            if (c == 0 && j < vis) {
+                sc[j] = sv;
+                mx = fmaxf(mx, sv);
+            }
+        }
     }
+    __syncthreads(); // the exp pass below reads scores other waves wrote
     mx = wave_max(mx);
     if ((threadIdx.x & 63) == 0)
         red[threadIdx.x >> 6] = mx;
@@ -185,9 +204,21 @@ extern "C" __global__ __launch_bounds__(256) void realm_attention(
     const float inv = sum > 0.f ? 1.f / sum : 1.f;
     const int parts = 256 / head_dim;
     const int d = threadIdx.x % head_dim, part = threadIdx.x / head_dim;
+    // weighted sum of V in key order (per slice), 8 keys per round with
+    // their loads issued first; keys past the visible ones add zero
     float a = 0.f;
-    for (int j = part; j < vis; j += parts)
-        a += (sc[j] * inv) * vc[(size_t)j * kv_dim + (size_t)kvh * head_dim + d];
+    for (int j0 = part; j0 < vis; j0 += 8 * parts) {
+        float vv[8], pw[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int j = j0 + u * parts, jc = min(j, vis - 1);
+            vv[u] = vc[(size_t)jc * kv_dim + (size_t)kvh * head_dim + d];
+            pw[u] = j < vis ? sc[jc] * inv : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            a += pw[u] * vv[u];
+    }
     acc[threadIdx.x] = a;
     __syncthreads();
     if (part == 0) {
