@@ -1196,7 +1196,8 @@ REALM_API int realm_hip_attention_dev(const float *d_q, const float *d_k_cache,
         kv_len > (size_t)INT32_MAX || num_heads > (size_t)INT32_MAX)
         return fail(REALM_INVALID_ARGUMENT, "attention: sizes exceed 2^31-1");
     CHECK(ensure_init());
-    const size_t lds = (head_dim + kv_len + 256) * sizeof(float);
+    const size_t att_threads = 1024; // ATT_TH in layer_ops.hip
+    const size_t lds = (head_dim + kv_len + att_threads) * sizeof(float);
     if (lds + 64 > g_dev.max_lds)
         return fail(REALM_BACKEND_UNSUPPORTED,
                     "attention: " + std::to_string(kv_len) + " cached keys exceed the LDS");
@@ -1207,8 +1208,8 @@ REALM_API int realm_hip_attention_dev(const float *d_q, const float *d_k_cache,
     float scale = 1.0f / std::sqrt((float)head_dim);
     void *args[] = {(void *)&d_q, (void *)&d_k_cache, (void *)&d_v_cache, &ikv, &ipos, &ih, &ikh,
                     &id, &scale, &d_out};
-    return launch("realm_attention", dim3((unsigned)(seq_len * num_heads)), dim3(256), lds, s,
-                  args);
+    return launch("realm_attention", dim3((unsigned)(seq_len * num_heads)),
+                  dim3((unsigned)att_threads), lds, s, args);
 }
 
 REALM_API int realm_hip_kv_append_dev(const float *d_k, const float *d_v, size_t seq_len,

@@ -130,32 +130,36 @@ REALM_DEV float wave_max(float v)
 // position + t) of head h attends to cached keys j <= position + t of KV
 // head h / (heads / kv_heads); scores (q . k_j) / sqrt(head_dim), softmax
 // with the maximum subtracted, weights normalized by their sum, output
-// sum_j p_j v_j.  One workgroup of 256 threads per (token, head); the
+// sum_j p_j v_j.  One workgroup of ATT_TH threads per (token, head); the
 // scores of the visible keys live in dynamic LDS after q.  head_dim divides
-// 256 (the host checks); the output sums run over head_dim x (256 /
+// 256 (the host checks); the output sums run over head_dim x (ATT_TH /
 // head_dim) threads, key slices summed in slice order.  The shuffle
 // reduction of a key's partial dots stays inside its lpk-lane group
 // (xor offsets below lpk), so groups never mix.
-extern "C" __global__ __launch_bounds__(256) void realm_attention(
+// Workgroup of the attention kernel: 16 waves, so that a (token, head)
+// workgroup keeps 16 waves' key and value loads in flight.
+#define ATT_TH 1024
+#define ATT_NW (ATT_TH / 64)
+extern "C" __global__ __launch_bounds__(ATT_TH) void realm_attention(
     const float *q, const float *kc, const float *vc, int kv_len, int position, int heads,
     int kv_heads, int head_dim, float scale, float *out)
 {
     extern __shared__ float smem[];
-    __shared__ float red[8];
+    __shared__ float red[2 * ATT_NW];
     float *qs = smem;              // head_dim
     float *sc = smem + head_dim;   // visible keys
-    float *acc = sc + kv_len;      // 256 partial outputs
+    float *acc = sc + kv_len;      // ATT_TH partial outputs
     const int t = blockIdx.x / heads, h = blockIdx.x % heads;
     const int kvh = h / (heads / kv_heads);
     const int kv_dim = kv_heads * head_dim;
     const int vis = min(kv_len, position + t + 1);
     const float *qr = q + ((size_t)t * heads + h) * head_dim;
-    for (int d = threadIdx.x; d < head_dim; d += 256)
+    for (int d = threadIdx.x; d < head_dim; d += ATT_TH)
         qs[d] = qr[d];
     __syncthreads();
     // Scores: a key row is read by head_dim / 4 adjacent lanes, one float4
     // each (coalesced), and their partial dots meet by shuffles; a wave
-    // covers 256 / head_dim keys per step, the workgroup 1024 / head_dim.
+    // covers 256 / head_dim keys per step, the workgroup ATT_NW times that.
     const int lpk = head_dim >> 2, kpw = 64 / lpk;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int c = lane % lpk, sub = lane / lpk;
@@ -163,17 +167,17 @@ extern "C" __global__ __launch_bounds__(256) void realm_attention(
     // 8 steps per round, every key load of the round issued before the
     // first is used (one memory round trip per round, not per step)
     float mx = -INFINITY;
-    for (int base = wave * kpw; base < vis; base += 32 * kpw) {
+    for (int base = wave * kpw; base < vis; base += 8 * ATT_NW * kpw) {
         float4 k4[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-            const int jc = min(base + u * 4 * kpw + sub, vis - 1);
+            const int jc = min(base + u * ATT_NW * kpw + sub, vis - 1);
             k4[u] = *reinterpret_cast<const float4 *>(kc + (size_t)jc * kv_dim +
                                                       (size_t)kvh * head_dim + 4 * c);
         }
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-            const int j = base + u * 4 * kpw + sub;
+            const int j = base + u * ATT_NW * kpw + sub;
             float dot = q4.x * k4[u].x + q4.y * k4[u].y + q4.z * k4[u].z + q4.w * k4[u].w;
             for (int off = lpk >> 1; off > 0; off >>= 1)
                 dot += __shfl_xor(dot, off, 64);
@@ -189,20 +193,24 @@ extern "C" __global__ __launch_bounds__(256) void realm_attention(
     if ((threadIdx.x & 63) == 0)
         red[threadIdx.x >> 6] = mx;
     __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    mx = red[0];
+    for (int w = 1; w < ATT_NW; ++w)
+        mx = fmaxf(mx, red[w]);
     float sum = 0.f;
-    for (int j = threadIdx.x; j < vis; j += 256) {
+    for (int j = threadIdx.x; j < vis; j += ATT_TH) {
         const float e = expf(sc[j] - mx);
         sc[j] = e;
         sum += e;
     }
     sum = wave_sum(sum);
     if ((threadIdx.x & 63) == 0)
-        red[4 + (threadIdx.x >> 6)] = sum;
+        red[ATT_NW + (threadIdx.x >> 6)] = sum;
     __syncthreads();
-    sum = red[4] + red[5] + red[6] + red[7];
+    sum = red[ATT_NW];
+    for (int w = 1; w < ATT_NW; ++w)
+        sum += red[ATT_NW + w];
     const float inv = sum > 0.f ? 1.f / sum : 1.f;
-    const int parts = 256 / head_dim;
+    const int parts = ATT_TH / head_dim;
     const int d = threadIdx.x % head_dim, part = threadIdx.x / head_dim;
     // weighted sum of V in key order (per slice), 8 keys per round with
     // their loads issued first; keys past the visible ones add zero
