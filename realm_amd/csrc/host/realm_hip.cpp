@@ -1269,7 +1269,8 @@ REALM_API int realm_hip_forward_layer_dev(const realm_layer *L, const float *d_h
         return REALM_OK;
     const size_t H = L->hidden, heads = L->num_heads, kvh = L->num_kv_heads, hd = L->head_dim,
                  I = L->intermediate, kv_dim = kvh * hd;
-    if (H == 0 || heads * hd != H || kvh == 0 || heads % kvh || I == 0 || I % 4 || H % 4)
+    if (H == 0 || heads * hd != H || kvh == 0 || heads % kvh || I == 0 || I % 4 || H % 4 ||
+        hd % 4 || 256 % hd || seq_len * (heads + kvh) * (hd / 2) / 256 >= (size_t)UINT32_MAX)
         return fail(REALM_INVALID_ARGUMENT,
                     "forward_layer: hidden must be heads x head_dim, kv heads divide heads, "
                     "hidden and intermediate multiples of 4");
@@ -1331,8 +1332,14 @@ REALM_API int realm_hip_forward_layer_dev(const realm_layer *L, const float *d_h
     const uint64_t qkv[3] = {L->wq, L->wk, L->wv};
     float *const qkv_out[3] = {q, k_rows, v_rows};
     CHECK(products(qkv, qkv_out, 3));
-    CHECK(realm_hip_rope_dev(q, seq_len, heads, hd, position, L->rope_theta, s));
-    CHECK(realm_hip_rope_dev(k_rows, seq_len, kvh, hd, position, L->rope_theta, s));
+    { // RoPE of Q and of this call's K rows in one launch
+        int iq = (int)heads, ik = (int)kvh, is = (int)seq_len, id = (int)hd, ip = (int)position;
+        float theta = L->rope_theta;
+        const size_t pairs = seq_len * (heads + kvh) * (hd / 2);
+        void *args[] = {&q, &iq, &k_rows, &ik, &is, &id, &ip, &theta};
+        CHECK(launch("realm_rope_qk", dim3((unsigned)((pairs + 255) / 256)), dim3(256), 0, s,
+                     args));
+    }
     CHECK(realm_hip_attention_dev(q, d_k_cache, d_v_cache, seq_len, position + seq_len, position,
                                   heads, kvh, hd, att, s));
     CHECK(realm_hip_weights_matmul_dev(L->wo, att, seq_len, o, s));

@@ -94,14 +94,13 @@ extern "C" __global__ __launch_bounds__(256) void realm_swiglu(const float4 *gat
 // attention.rs:171-235), in place on x [seq][heads][head_dim]: interleaved
 // pairs (i, i + 1), freq = 1 / theta^(i / head_dim), angle = (start + s) *
 // freq, in the reference's f32 operation order.  One thread per pair.
-extern "C" __global__ __launch_bounds__(256) void realm_rope(float *x, int seq, int heads,
-                                                             int head_dim, int start, float theta)
+namespace {
+
+// Pair p of x [seq][heads][head_dim] rotated in place.
+__device__ __forceinline__ void rope_pair(float *x, size_t p, int heads, int head_dim, int start,
+                                          float theta)
 {
     const int half = head_dim >> 1;
-    const size_t pairs = (size_t)seq * heads * half;
-    const size_t p = (size_t)blockIdx.x * 256 + threadIdx.x;
-    if (p >= pairs)
-        return;
     const int i = 2 * (int)(p % half);
     const int s = (int)(p / ((size_t)heads * half));
     const float freq = 1.0f / powf(theta, (float)i / (float)head_dim);
@@ -110,6 +109,31 @@ extern "C" __global__ __launch_bounds__(256) void realm_rope(float *x, int seq, 
     float2 *v = reinterpret_cast<float2 *>(x) + p;
     const float2 a = *v;
     *v = make_float2(a.x * c - a.y * sn, a.x * sn + a.y * c);
+}
+
+} // namespace
+
+extern "C" __global__ __launch_bounds__(256) void realm_rope(float *x, int seq, int heads,
+                                                             int head_dim, int start, float theta)
+{
+    const size_t pairs = (size_t)seq * heads * (head_dim >> 1);
+    const size_t p = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (p < pairs)
+        rope_pair(x, p, heads, head_dim, start, theta);
+}
+
+// Q and K of one layer in one launch: pairs of q first, then of k.
+extern "C" __global__ __launch_bounds__(256) void realm_rope_qk(float *q, int q_heads, float *k,
+                                                                int k_heads, int seq, int head_dim,
+                                                                int start, float theta)
+{
+    const size_t pq = (size_t)seq * q_heads * (head_dim >> 1);
+    const size_t pk = (size_t)seq * k_heads * (head_dim >> 1);
+    const size_t p = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (p < pq)
+        rope_pair(q, p, q_heads, head_dim, start, theta);
+    else if (p < pq + pk)
+        rope_pair(k, p - pq, k_heads, head_dim, start, theta);
 }
 
 namespace {
