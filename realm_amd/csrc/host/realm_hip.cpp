@@ -237,7 +237,7 @@ int pick_stream(void *user, hipStream_t *s)
 // Per-stream scratch buffers (grow-only).  Work on one stream is ordered, so
 // reusing a stream's buffers for its next call is safe.
 enum Slot { WS_RAW, WS_WEIGHT, WS_X, WS_Y, WS_XH, WS_XL, WS_XM, WS_TS, WS_U, WS_IDS, WS_PART,
-            WS_LAYER, WS_N };
+            WS_LAYER, WS_ATT, WS_N };
 
 struct Workspace {
     void *buf[WS_N] = {};
@@ -1196,6 +1196,40 @@ REALM_API int realm_hip_attention_dev(const float *d_q, const float *d_k_cache,
         kv_len > (size_t)INT32_MAX || num_heads > (size_t)INT32_MAX)
         return fail(REALM_INVALID_ARGUMENT, "attention: sizes exceed 2^31-1");
     CHECK(ensure_init());
+    // Small grids (decode): split the keys of each (token, head) over up to
+    // 16 workgroups of at least 64 keys, then combine the partials.
+    size_t splits = 1;
+    if (seq_len * num_heads < 2 * (size_t)g_dev.cu_count && kv_len >= 256)
+        splits = std::min<size_t>({16, (2 * (size_t)g_dev.cu_count + seq_len * num_heads - 1) /
+                                           (seq_len * num_heads),
+                                   (kv_len + 63) / 64});
+    if (const char *env = getenv("REALM_ATT_SPLITS")) { // tuning / test override
+        const long v = atol(env);
+        if (v >= 1 && v <= 64)
+            splits = (size_t)v;
+    }
+    if (splits > 1) {
+        const size_t chunk = (kv_len + splits - 1) / splits;
+        const size_t lds = (head_dim + chunk + 256) * sizeof(float);
+        if (lds + 64 > g_dev.max_lds)
+            return fail(REALM_BACKEND_UNSUPPORTED,
+                        "attention: " + std::to_string(chunk) + " keys per split exceed the LDS");
+        hipStream_t s;
+        CHECK(pick_stream(stream, &s));
+        void *part = nullptr;
+        CHECK(ws_get(s, WS_ATT, seq_len * num_heads * splits * (head_dim + 2) * sizeof(float),
+                     &part));
+        int ikv = (int)kv_len, ipos = (int)position, ih = (int)num_heads,
+            ikh = (int)num_kv_heads, id = (int)head_dim, isp = (int)splits, ich = (int)chunk;
+        float scale = 1.0f / std::sqrt((float)head_dim);
+        void *args[] = {(void *)&d_q, (void *)&d_k_cache, (void *)&d_v_cache, &ikv, &ipos, &ih,
+                        &ikh, &id, &scale, &isp, &ich, &part};
+        CHECK(launch("realm_attention_split", dim3((unsigned)(seq_len * num_heads * splits)),
+                     dim3(256), lds, s, args));
+        void *cargs[] = {&part, &isp, &id, &d_out};
+        return launch("realm_attention_combine", dim3((unsigned)(seq_len * num_heads)),
+                      dim3(256), 0, s, cargs);
+    }
     const size_t att_threads = 1024; // ATT_TH in layer_ops.hip
     const size_t lds = (head_dim + kv_len + att_threads) * sizeof(float);
     if (lds + 64 > g_dev.max_lds)

@@ -273,3 +273,122 @@ extern "C" __global__ __launch_bounds__(256) void realm_add(const float4 *a, con
         out[i] = make_float4(x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w);
     }
 }
+
+// Split-K form of the attention for small grids (decode): workgroup
+// (token, head, split s) takes the visible keys [s chunk, (s+1) chunk) and
+// writes its partial max m_s, exp-sum l_s = sum exp(score - m_s) and
+// unnormalized output acc_s = sum exp(score - m_s) v into
+// part[((t * heads + h) * splits + s) * (head_dim + 2)]: (m, l, acc...).
+// realm_attention_combine then forms m = max m_s, l = sum l_s e^(m_s - m),
+// out = sum acc_s e^(m_s - m) / l, splits in order.  256 threads; the
+// chunk's scores live in LDS.
+extern "C" __global__ __launch_bounds__(256) void realm_attention_split(
+    const float *q, const float *kc, const float *vc, int kv_len, int position, int heads,
+    int kv_heads, int head_dim, float scale, int splits, int chunk, float *part)
+{
+    extern __shared__ float smem[];
+    __shared__ float red[8];
+    float *qs = smem, *sc = smem + head_dim, *acc = sc + chunk;
+    const int s = blockIdx.x % splits, th = blockIdx.x / splits;
+    const int t = th / heads, h = th % heads;
+    const int kvh = h / (heads / kv_heads), kv_dim = kv_heads * head_dim;
+    const int vis = min(kv_len, position + t + 1);
+    const int j0 = s * chunk, j1 = min(vis, j0 + chunk);
+    const int n = max(j1 - j0, 0);
+    const float *qr = q + ((size_t)t * heads + h) * head_dim;
+    for (int d = threadIdx.x; d < head_dim; d += 256)
+        qs[d] = qr[d];
+    __syncthreads();
+    const int lpk = head_dim >> 2, kpw = 64 / lpk;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int c = lane % lpk, sub = lane / lpk;
+    const float4 q4 = reinterpret_cast<const float4 *>(qs)[c];
+    float mx = -INFINITY;
+    for (int base = wave * kpw; base < n; base += 32 * kpw) {
+        float4 k4[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int jc = j0 + min(base + u * 4 * kpw + sub, n - 1);
+            k4[u] = *reinterpret_cast<const float4 *>(kc + (size_t)jc * kv_dim +
+                                                      (size_t)kvh * head_dim + 4 * c);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int jl = base + u * 4 * kpw + sub;
+            float dot = q4.x * k4[u].x + q4.y * k4[u].y + q4.z * k4[u].z + q4.w * k4[u].w;
+            for (int off = lpk >> 1; off > 0; off >>= 1)
+                dot += __shfl_xor(dot, off, 64);
+            const float sv = dot * scale;
+            if (c == 0 && jl < n) {
+                sc[jl] = sv;
+                mx = fmaxf(mx, sv);
+            }
+        }
+    }
+    __syncthreads();
+    mx = wave_max(mx);
+    if ((threadIdx.x & 63) == 0)
+        red[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float sum = 0.f;
+    for (int j = threadIdx.x; j < n; j += 256) {
+        const float e = expf(sc[j] - mx);
+        sc[j] = e;
+        sum += e;
+    }
+    sum = wave_sum(sum);
+    if ((threadIdx.x & 63) == 0)
+        red[4 + (threadIdx.x >> 6)] = sum;
+    __syncthreads();
+    sum = red[4] + red[5] + red[6] + red[7];
+    const int parts = 256 / head_dim;
+    const int d = threadIdx.x % head_dim, pp = threadIdx.x / head_dim;
+    float a = 0.f;
+    for (int jb = pp; jb < n; jb += 8 * parts) {
+        float vv[8], pw[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int jl = jb + u * parts, jc = j0 + min(jl, n - 1);
+            vv[u] = vc[(size_t)jc * kv_dim + (size_t)kvh * head_dim + d];
+            pw[u] = jl < n ? sc[min(jl, n - 1)] : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            a += pw[u] * vv[u];
+    }
+    acc[threadIdx.x] = a;
+    __syncthreads();
+    float *pr = part + ((size_t)th * splits + s) * (head_dim + 2);
+    if (pp == 0) {
+        float o = acc[d];
+        for (int p = 1; p < parts; ++p)
+            o += acc[p * head_dim + d];
+        pr[2 + d] = o;
+    }
+    if (threadIdx.x == 0) {
+        pr[0] = n > 0 ? mx : -INFINITY;
+        pr[1] = n > 0 ? sum : 0.f;
+    }
+}
+
+// One workgroup of head_dim threads per (token, head).
+extern "C" __global__ __launch_bounds__(256) void realm_attention_combine(
+    const float *part, int splits, int head_dim, float *out)
+{
+    const int th = blockIdx.x, d = threadIdx.x;
+    if (d >= head_dim)
+        return;
+    const float *pr = part + (size_t)th * splits * (head_dim + 2);
+    float m = -INFINITY;
+    for (int s = 0; s < splits; ++s)
+        m = fmaxf(m, pr[(size_t)s * (head_dim + 2)]);
+    float l = 0.f, o = 0.f;
+    for (int s = 0; s < splits; ++s) {
+        const float *p = pr + (size_t)s * (head_dim + 2);
+        const float w = p[1] > 0.f ? expf(p[0] - m) : 0.f;
+        l += p[1] * w;
+        o += p[2 + d] * w;
+    }
+    out[(size_t)th * head_dim + d] = l > 0.f ? o / l : 0.f;
+}

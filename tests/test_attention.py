@@ -98,7 +98,13 @@ def test_rope(backend, seq, heads, hd, start):
     (5, 20, 15, 16, 4, 64),        # prefill chunk after 15 cached tokens
     (3, 40, 10, 4, 4, 256),        # cache longer than the visible keys
 ])
-def test_attention(backend, seq, kv, pos, heads, kvh, hd):
+@pytest.mark.parametrize("splits", ["", "1", "3", "16"])
+def test_attention(backend, monkeypatch, seq, kv, pos, heads, kvh, hd, splits):
+    """The one-workgroup form and the split-K form (partials, then a
+    combine) with its default and forced split counts, including splits
+    with no visible keys (3 and 16 splits of short caches)."""
+    if splits:
+        monkeypatch.setenv("REALM_ATT_SPLITS", splits)
     g = np.random.default_rng(seq * 7 + kv)
     q = g.standard_normal(seq * heads * hd).astype(np.float32)
     k = g.standard_normal(kv * kvh * hd).astype(np.float32)
