@@ -162,9 +162,10 @@ def decode_roofline(be, model: Model7B, stream: int, reps: int) -> dict:
 
 
 def full_layers(be, model: Model7B, stream: int, reps: int, context: int = 512) -> dict:
-    """The whole decoder layer on the device (realm_hip_forward_layer_dev:
+    """The whole decoder layer on the device (realm_hip_forward_layers_dev:
     norm, Q/K/V, RoPE, KV append, attention, Wo, residual + norm, gate/up,
-    SwiGLU, W_down, residual) for all of the model's layers, each with its own
+    SwiGLU, W_down, residual; the residual add fused into the next layer's
+    first norm) for all of the model's layers in one call, each with its own
     weights and KV cache (LLaMA-7B has 32 KV heads of 128, no GQA): a
     prefill of `context - 1` tokens, then the decode step of the
     next token captured in one HIP graph and replayed (every replay writes the
@@ -190,9 +191,8 @@ def full_layers(be, model: Model7B, stream: int, reps: int, context: int = 512) 
     bufs[0].upload(synth.activations(g, pre, H))
 
     def run(seq, pos):
-        for i, L in enumerate(layers):
-            be.forward_layer_dev(L, bufs[i % 2].ptr, seq, pos, caches[i][0].ptr, caches[i][1].ptr,
-                                 context, bufs[(i + 1) % 2].ptr, stream=stream)
+        be.forward_layers_dev(layers, bufs[0].ptr, seq, pos, [c[0].ptr for c in caches],
+                              [c[1].ptr for c in caches], context, bufs[1].ptr, stream=stream)
 
     run(pre, 0)  # prefill fills rows 0 .. context - 2 of every cache
     be.synchronize()

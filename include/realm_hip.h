@@ -321,6 +321,17 @@ int realm_hip_forward_layer_dev(const realm_layer *layer, const float *d_hidden,
                                 size_t position, float *d_k_cache, float *d_v_cache,
                                 size_t max_seq_len, float *d_out, void *stream);
 
+/* n_layers such layers back to back (the layer loop around realm_forward_layer,
+ * Model::forward, crates/realm-models/src/model.rs:598-601): layer l reads
+ * d_k_caches[l] / d_v_caches[l]; between layers the residual add is fused
+ * into the next layer's first RMSNorm (one launch fewer per layer), and
+ * d_out receives the last layer's output.  Same contract as
+ * realm_hip_forward_layer_dev otherwise. */
+int realm_hip_forward_layers_dev(const realm_layer *layers, size_t n_layers,
+                                 const float *d_hidden, size_t seq_len, size_t position,
+                                 float *const *d_k_caches, float *const *d_v_caches,
+                                 size_t max_seq_len, float *d_out, void *stream);
+
 /* ------------------------------------------------------ GGUF model images */
 
 /* The transformer shape a GGUF image declares: GGUFParser::extract_config

@@ -101,6 +101,8 @@ SIGNATURES = {
     "realm_hip_add_dev": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p, c_void_p]),
     "realm_hip_forward_layer_dev": (c_int, [c_void_p, c_void_p, c_size_t, c_size_t, c_void_p,
                                             c_void_p, c_size_t, c_void_p, c_void_p]),
+    "realm_hip_forward_layers_dev": (c_int, [c_void_p, c_size_t, c_void_p, c_size_t, c_size_t,
+                                             c_void_p, c_void_p, c_size_t, c_void_p, c_void_p]),
 }
 
 _lib = None

@@ -370,6 +370,17 @@ class HipGpuBackend:
             ctypes.byref(layer), c_void_p(d_hidden), seq_len, position, c_void_p(d_k_cache),
             c_void_p(d_v_cache), max_seq_len, c_void_p(d_out), c_void_p(stream or 0)))
 
+    def forward_layers_dev(self, layers, d_hidden: int, seq_len: int, position: int,
+                           d_k_caches, d_v_caches, max_seq_len: int, d_out: int,
+                           stream=None) -> None:
+        """Several device layers back to back, residual adds fused between them."""
+        arr = (RealmLayer * len(layers))(*layers)
+        kc = (c_void_p * len(layers))(*d_k_caches)
+        vc = (c_void_p * len(layers))(*d_v_caches)
+        self._check(self.lib.realm_hip_forward_layers_dev(
+            arr, len(layers), c_void_p(d_hidden), seq_len, position, kc, vc, max_seq_len,
+            c_void_p(d_out), c_void_p(stream or 0)))
+
 
 class RealmLayer(ctypes.Structure):
     """struct realm_layer of include/realm_hip.h."""

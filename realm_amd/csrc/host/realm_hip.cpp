@@ -1286,21 +1286,15 @@ REALM_API int realm_hip_add_dev(const float *d_a, const float *d_b, size_t n, fl
     return launch("realm_add", dim3(wgs), dim3(256), 0, s, args);
 }
 
-// One decoder layer of realm_forward_layer (memory64_host.rs:2059-2458) on
-// the device, every step on `stream`: RMSNorm, Q/K/V in one grouped product
-// with K and V written straight into the cache rows of this call's tokens,
-// RoPE on Q and on those K rows, attention over the cache, Wo, the residual
-// add fused with the FFN norm, gate/up in one grouped product, SwiGLU,
-// W_down, the final residual add.
-REALM_API int realm_hip_forward_layer_dev(const realm_layer *L, const float *d_hidden,
-                                          size_t seq_len, size_t position, float *d_k_cache,
-                                          float *d_v_cache, size_t max_seq_len, float *d_out,
-                                          void *stream)
+namespace {
+
+// Checks one layer's shape, cache room and weights; type[] gets the seven
+// weights' formats (Wq, Wk, Wv, Wo, W_gate, W_up, W_down).
+int check_layer(const realm_layer *L, size_t seq_len, size_t position, size_t max_seq_len,
+                int type[7])
 {
-    if (!L || !d_hidden || !d_out || !d_k_cache || !d_v_cache || !L->attn_norm || !L->ffn_norm)
-        return fail(REALM_INVALID_ARGUMENT, "forward_layer: null pointer argument");
-    if (seq_len == 0)
-        return REALM_OK;
+    if (!L->attn_norm || !L->ffn_norm)
+        return fail(REALM_INVALID_ARGUMENT, "forward_layer: null norm weights");
     const size_t H = L->hidden, heads = L->num_heads, kvh = L->num_kv_heads, hd = L->head_dim,
                  I = L->intermediate, kv_dim = kvh * hd;
     if (H == 0 || heads * hd != H || kvh == 0 || heads % kvh || I == 0 || I % 4 || H % 4 ||
@@ -1312,60 +1306,62 @@ REALM_API int realm_hip_forward_layer_dev(const realm_layer *L, const float *d_h
         return fail(REALM_MODEL_PARSE_ERROR, "KV cache overflow: " + std::to_string(position) +
                                                  " + " + std::to_string(seq_len) + " > " +
                                                  std::to_string(max_seq_len));
-    struct Want {
-        uint64_t h;
-        size_t n, k;
-    } want[7] = {{L->wq, H, H},     {L->wk, kv_dim, H}, {L->wv, kv_dim, H}, {L->wo, H, H},
-                 {L->w_gate, I, H}, {L->w_up, I, H},    {L->w_down, H, I}};
-    int type[7];
+    const uint64_t h[7] = {L->wq, L->wk, L->wv, L->wo, L->w_gate, L->w_up, L->w_down};
+    const size_t n[7] = {H, kv_dim, kv_dim, H, I, I, H}, k[7] = {H, H, H, H, H, H, I};
     for (int i = 0; i < 7; ++i) {
-        const Want &x = want[i];
         Weight w;
-        CHECK(get_weight(x.h, &w));
+        CHECK(get_weight(h[i], &w));
         type[i] = w.type;
-        if (w.n != x.n || w.k != x.k)
+        if (w.n != n[i] || w.k != k[i])
             return fail(REALM_INVALID_ARGUMENT,
-                        "forward_layer: weight " + std::to_string(x.h) + " is " +
+                        "forward_layer: weight " + std::to_string(h[i]) + " is " +
                             std::to_string(w.n) + " x " + std::to_string(w.k) + ", the layer needs " +
-                            std::to_string(x.n) + " x " + std::to_string(x.k));
+                            std::to_string(n[i]) + " x " + std::to_string(k[i]));
     }
-    auto weight_type = [&](uint64_t h) {
-        for (int i = 0; i < 7; ++i)
-            if (want[i].h == h)
-                return type[i];
-        return -1;
-    };
-    CHECK(ensure_init());
-    hipStream_t s;
-    CHECK(pick_stream(stream, &s));
-    // intermediates: normed / attention out / h2 / down [seq][H], q [seq][H],
-    // gate and up [seq][I], o [seq][H]
-    const size_t sh = align256(seq_len * H * 4), si = align256(seq_len * I * 4);
-    void *ws = nullptr;
-    CHECK(ws_get(s, WS_LAYER, 5 * sh + 2 * si, &ws));
-    uint8_t *base = static_cast<uint8_t *>(ws);
-    float *normed = (float *)base, *q = (float *)(base + sh), *att = (float *)(base + 2 * sh),
-          *h2 = (float *)(base + 3 * sh), *o = (float *)(base + 4 * sh),
-          *gate = (float *)(base + 5 * sh), *up = (float *)(base + 5 * sh + si);
-    float *k_rows = d_k_cache + position * kv_dim, *v_rows = d_v_cache + position * kv_dim;
-    CHECK(realm_hip_rms_norm_dev(d_hidden, nullptr, L->attn_norm, L->rms_norm_eps, seq_len, H,
-                                 nullptr, normed, s));
+    return REALM_OK;
+}
+
+// The steps of one layer up to (not including) the final residual add.  The
+// layer's input is x, or x + x_res when x_res is set (the previous layer's
+// output left as its two addends: the add is fused into this layer's first
+// norm, the sum going to h_in).  Leaves h2 = input + attention output and
+// down = the FFN output, whose sum is the layer's output.  h2 and down may be
+// the buffers x and x_res came in (both are consumed by the first norm).
+int layer_steps(const realm_layer *L, const int type[7], const float *x, const float *x_res,
+                size_t seq_len, size_t position, float *kc, float *vc, float *ws, float *h_in,
+                float *h2, float *down, hipStream_t s)
+{
+    const size_t H = L->hidden, heads = L->num_heads, kvh = L->num_kv_heads, hd = L->head_dim,
+                 I = L->intermediate, kv_dim = kvh * hd;
+    const size_t sh = align256(seq_len * H * 4) / 4, si = align256(seq_len * I * 4) / 4;
+    float *normed = ws, *q = ws + sh, *att = ws + 2 * sh, *o = ws + 3 * sh, *gate = ws + 4 * sh,
+          *up = ws + 4 * sh + si;
+    float *k_rows = kc + position * kv_dim, *v_rows = vc + position * kv_dim;
+    const float *h = x;
+    if (x_res) {
+        CHECK(realm_hip_rms_norm_dev(x, x_res, L->attn_norm, L->rms_norm_eps, seq_len, H, h_in,
+                                     normed, s));
+        h = h_in;
+    } else {
+        CHECK(realm_hip_rms_norm_dev(x, nullptr, L->attn_norm, L->rms_norm_eps, seq_len, H,
+                                     nullptr, normed, s));
+    }
     // matrices of one format share a grouped product (GGUF quant mixes
     // often keep V or up in Q6_K: then separate products)
-    auto products = [&](const uint64_t *h, float *const *out, int n) {
+    auto products = [&](const uint64_t *hs, const int *ts, float *const *out, int n) {
         bool same = true;
         for (int i = 1; i < n; ++i)
-            same = same && weight_type(h[i]) == weight_type(h[0]);
+            same = same && ts[i] == ts[0];
         if (same)
-            return realm_hip_weights_matmul_group_dev(h, n, normed, seq_len, out, s);
+            return realm_hip_weights_matmul_group_dev(hs, n, normed, seq_len, out, s);
         for (int i = 0; i < n; ++i)
-            if (int rc = realm_hip_weights_matmul_dev(h[i], normed, seq_len, out[i], s))
+            if (int rc = realm_hip_weights_matmul_dev(hs[i], normed, seq_len, out[i], s))
                 return rc;
         return (int)REALM_OK;
     };
     const uint64_t qkv[3] = {L->wq, L->wk, L->wv};
     float *const qkv_out[3] = {q, k_rows, v_rows};
-    CHECK(products(qkv, qkv_out, 3));
+    CHECK(products(qkv, type, qkv_out, 3));
     { // RoPE of Q and of this call's K rows in one launch
         int iq = (int)heads, ik = (int)kvh, is = (int)seq_len, id = (int)hd, ip = (int)position;
         float theta = L->rope_theta;
@@ -1374,17 +1370,73 @@ REALM_API int realm_hip_forward_layer_dev(const realm_layer *L, const float *d_h
         CHECK(launch("realm_rope_qk", dim3((unsigned)((pairs + 255) / 256)), dim3(256), 0, s,
                      args));
     }
-    CHECK(realm_hip_attention_dev(q, d_k_cache, d_v_cache, seq_len, position + seq_len, position,
-                                  heads, kvh, hd, att, s));
+    CHECK(realm_hip_attention_dev(q, kc, vc, seq_len, position + seq_len, position, heads, kvh,
+                                  hd, att, s));
     CHECK(realm_hip_weights_matmul_dev(L->wo, att, seq_len, o, s));
-    CHECK(realm_hip_rms_norm_dev(d_hidden, o, L->ffn_norm, L->rms_norm_eps, seq_len, H, h2,
-                                 normed, s));
+    CHECK(realm_hip_rms_norm_dev(h, o, L->ffn_norm, L->rms_norm_eps, seq_len, H, h2, normed, s));
     const uint64_t gu[2] = {L->w_gate, L->w_up};
     float *const gu_out[2] = {gate, up};
-    CHECK(products(gu, gu_out, 2));
+    CHECK(products(gu, type + 4, gu_out, 2));
     CHECK(realm_hip_swiglu_dev(gate, up, seq_len * I, gate, s));
-    CHECK(realm_hip_weights_matmul_dev(L->w_down, gate, seq_len, att, s));
-    return realm_hip_add_dev(h2, att, seq_len * H, d_out, s);
+    return realm_hip_weights_matmul_dev(L->w_down, gate, seq_len, down, s);
+}
+
+} // namespace
+
+// n_layers decoder layers of realm_forward_layer (memory64_host.rs:
+// 2059-2458) on the device, every step on `stream`: per layer RMSNorm, Q/K/V
+// in one grouped product with K and V written straight into the cache rows
+// of this call's tokens, RoPE on Q and on those K rows, attention over the
+// cache, Wo, the residual add fused with the FFN norm, gate/up in one grouped
+// product, SwiGLU, W_down; between layers the residual add is fused into the
+// next layer's first norm, and only the last layer's output is summed.
+REALM_API int realm_hip_forward_layers_dev(const realm_layer *layers, size_t n_layers,
+                                           const float *d_hidden, size_t seq_len,
+                                           size_t position, float *const *d_k_caches,
+                                           float *const *d_v_caches, size_t max_seq_len,
+                                           float *d_out, void *stream)
+{
+    if (!layers || !d_hidden || !d_out || (n_layers && (!d_k_caches || !d_v_caches)))
+        return fail(REALM_INVALID_ARGUMENT, "forward_layers: null pointer argument");
+    if (seq_len == 0 || n_layers == 0)
+        return REALM_OK;
+    std::vector<int> types(7 * n_layers);
+    size_t wsize = 0;
+    for (size_t l = 0; l < n_layers; ++l) {
+        if (!d_k_caches[l] || !d_v_caches[l])
+            return fail(REALM_INVALID_ARGUMENT, "forward_layers: null KV cache");
+        if (layers[l].hidden != layers[0].hidden)
+            return fail(REALM_INVALID_ARGUMENT, "forward_layers: layers of different widths");
+        CHECK(check_layer(&layers[l], seq_len, position, max_seq_len, &types[7 * l]));
+        wsize = std::max(wsize, 4 * align256(seq_len * layers[l].hidden * 4) +
+                                    2 * align256(seq_len * layers[l].intermediate * 4));
+    }
+    CHECK(ensure_init());
+    hipStream_t s;
+    CHECK(pick_stream(stream, &s));
+    // per-layer intermediates, then the chained h_in, h2 and down [seq][H]
+    const size_t sh = align256(seq_len * layers[0].hidden * 4);
+    void *ws = nullptr;
+    CHECK(ws_get(s, WS_LAYER, wsize + 3 * sh, &ws));
+    uint8_t *base = static_cast<uint8_t *>(ws);
+    float *h_in = (float *)(base + wsize), *h2 = (float *)(base + wsize + sh),
+          *down = (float *)(base + wsize + 2 * sh);
+    for (size_t l = 0; l < n_layers; ++l)
+        CHECK(layer_steps(&layers[l], &types[7 * l], l ? h2 : d_hidden, l ? down : nullptr,
+                          seq_len, position, d_k_caches[l], d_v_caches[l], (float *)base, h_in,
+                          h2, down, s));
+    return realm_hip_add_dev(h2, down, seq_len * layers[0].hidden, d_out, s);
+}
+
+REALM_API int realm_hip_forward_layer_dev(const realm_layer *L, const float *d_hidden,
+                                          size_t seq_len, size_t position, float *d_k_cache,
+                                          float *d_v_cache, size_t max_seq_len, float *d_out,
+                                          void *stream)
+{
+    if (!L || !d_k_cache || !d_v_cache)
+        return fail(REALM_INVALID_ARGUMENT, "forward_layer: null pointer argument");
+    return realm_hip_forward_layers_dev(L, 1, d_hidden, seq_len, position, &d_k_cache,
+                                        &d_v_cache, max_seq_len, d_out, stream);
 }
 
 REALM_API int realm_hip_fused_dequant_matmul_q4k(const void *blocks, size_t n_blocks,

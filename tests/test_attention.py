@@ -235,3 +235,69 @@ def test_forward_layer(backend, oracle, mixed):
             backend.release_weights(h)
         for b in list(dn.values()) + [dkc, dvc]:
             b.close()
+
+
+@pytest.mark.gpu
+def test_forward_layers_chain(backend, oracle):
+    """Three layers in one realm_hip_forward_layers_dev call (the residual add
+    fused into the next layer's first norm) against three oracle layers
+    applied in turn, for a 4-token prefill and a 1-token decode after it."""
+    from realm_amd import synth
+    from realm_amd.backend import RealmLayer
+    from realm_amd.formats import GGML_Q4_K, GGML_Q6_K
+    H, heads, kvh, hd, inter, max_len, nl = 256, 4, 2, 64, 512, 8, 3
+    kv_dim = kvh * hd
+    cfg = {"hidden": H, "heads": heads, "kv_heads": kvh, "head_dim": hd, "eps": 1e-5,
+           "theta": 10000.0}
+    shapes = {"wq": (H, H), "wk": (kv_dim, H), "wv": (kv_dim, H), "wo": (H, H),
+              "w_gate": (inter, H), "w_up": (inter, H), "w_down": (H, inter)}
+    g = synth.rng(77)
+    per, layers, bufs, handles = [], [], [], []
+    for li in range(nl):
+        types = {n: (GGML_Q6_K if n == "w_down" else GGML_Q4_K) for n in shapes}
+        blocks = {n: synth.blocks(g, types[n], *shapes[n]) for n in shapes}
+        for b in blocks.values():
+            b["d"] = (b["d"].view(np.float16) * np.float16(40)).view(np.uint16)
+        hs = {n: backend.register_weights(types[n], blocks[n], *shapes[n]) for n in shapes}
+        handles += hs.values()
+        norms = {"attn": (1 + 0.1 * g.standard_normal(H)).astype(np.float32),
+                 "ffn": (1 + 0.1 * g.standard_normal(H)).astype(np.float32)}
+        dn = {k: backend.alloc(v.nbytes).upload(v) for k, v in norms.items()}
+        kc, vc = backend.alloc(max_len * kv_dim * 4), backend.alloc(max_len * kv_dim * 4)
+        bufs += list(dn.values()) + [kc, vc]
+        layers.append(RealmLayer(wq=hs["wq"], wk=hs["wk"], wv=hs["wv"], wo=hs["wo"],
+                                 w_gate=hs["w_gate"], w_up=hs["w_up"], w_down=hs["w_down"],
+                                 attn_norm=dn["attn"].ptr, ffn_norm=dn["ffn"].ptr, hidden=H,
+                                 num_heads=heads, num_kv_heads=kvh, head_dim=hd,
+                                 intermediate=inter, rms_norm_eps=1e-5, rope_theta=10000.0))
+        per.append((types, blocks, norms, np.zeros(max_len * kv_dim, np.float32),
+                    np.zeros(max_len * kv_dim, np.float32), kc, vc))
+    try:
+        pos = 0
+        for seq in (4, 1):
+            x = g.standard_normal((seq, H)).astype(np.float32)
+            dx, dy = backend.alloc(x.nbytes).upload(x), backend.alloc(x.nbytes)
+            backend.forward_layers_dev(layers, dx.ptr, seq, pos, [p[5].ptr for p in per],
+                                       [p[6].ptr for p in per], max_len, dy.ptr)
+            backend.synchronize()
+            got = dy.download(np.float32, x.size).reshape(seq, H)
+            want = x
+            for types, blocks, norms, kr, vr, _, _ in per:
+                def matmul(name, a, m, types=types, blocks=blocks):
+                    n, k = shapes[name]
+                    rc, y = oracle.candle_fused(types[name], blocks[name],
+                                                np.ascontiguousarray(a), m, n, k)
+                    assert rc == 0
+                    return y.reshape(m, n)
+                want = oa.forward_layer(matmul, want, blocks, norms, cfg, kr, vr, pos, seq)
+            err = rel_l2(got, want)
+            print(f"forward_layers seq={seq} pos={pos} rel_l2={err:.3e}")
+            assert err < 1e-3, (seq, pos)
+            pos += seq
+            dx.close()
+            dy.close()
+    finally:
+        for h in handles:
+            backend.release_weights(h)
+        for b in bufs:
+            b.close()
