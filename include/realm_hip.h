@@ -49,7 +49,12 @@ typedef enum realm_status {
 
 /* ggml tensor type ids (crates/realm-core/src/formats/gguf.rs:458-480). */
 #define REALM_GGML_F32 0
+#define REALM_GGML_Q4_0 2
+#define REALM_GGML_Q4_1 3
+#define REALM_GGML_Q5_0 6
+#define REALM_GGML_Q5_1 7
 #define REALM_GGML_Q8_0 8
+#define REALM_GGML_Q8_1 9
 #define REALM_GGML_Q4_K 12
 #define REALM_GGML_Q6_K 14
 
@@ -119,8 +124,31 @@ int realm_hip_fused_dequant_matmul_q80(const void *blocks, size_t n_blocks,
                                        size_t batch_size, size_t n, size_t k,
                                        float *out);
 
-/* Format-generic form of the three above (ggml_type 8, 12 or 14).  Every
- * other fused_dequant_matmul_* of the trait (Q2_K..Q8_1, Q5_K, Q8_K) returns
+/* GpuBackendTrait::fused_dequant_matmul_q40 / _q41 / _q50 / _q51 / _q81
+ * (gpu_backend_trait.rs:82-119, 132-139) on the reference's 32-element block
+ * layouts (crates/realm-core/src/quant.rs:10-70: Q4_0 18 B, Q4_1 20 B, Q5_0
+ * 22 B, Q5_1 24 B, Q8_1 36 B per block), as CandleGpuBackend computes them
+ * (candle_backend.rs:837-1103): validation k % 32 == 0, n_blocks == n*k/32,
+ * input_len == batch_size*k; the blocks dequantized bit-exactly on the
+ * device (quant.rs:226-370), then y = x W^T on the f32 MFMA GEMM. */
+int realm_hip_fused_dequant_matmul_q40(const void *blocks, size_t n_blocks,
+                                       const float *input, size_t input_len,
+                                       size_t batch_size, size_t n, size_t k, float *out);
+int realm_hip_fused_dequant_matmul_q41(const void *blocks, size_t n_blocks,
+                                       const float *input, size_t input_len,
+                                       size_t batch_size, size_t n, size_t k, float *out);
+int realm_hip_fused_dequant_matmul_q50(const void *blocks, size_t n_blocks,
+                                       const float *input, size_t input_len,
+                                       size_t batch_size, size_t n, size_t k, float *out);
+int realm_hip_fused_dequant_matmul_q51(const void *blocks, size_t n_blocks,
+                                       const float *input, size_t input_len,
+                                       size_t batch_size, size_t n, size_t k, float *out);
+int realm_hip_fused_dequant_matmul_q81(const void *blocks, size_t n_blocks,
+                                       const float *input, size_t input_len,
+                                       size_t batch_size, size_t n, size_t k, float *out);
+
+/* Format-generic form of the eight above (ggml_type 2, 3, 6, 7, 8, 9, 12 or
+ * 14).  The trait's Q2_K, Q3_K, Q5_K and Q8_K forms return
  * REALM_BACKEND_UNSUPPORTED so that dispatch_matmul falls back to the CPU
  * (crates/realm-models/src/matmul_dispatch.rs:72-88). */
 int realm_hip_fused_dequant_matmul(int ggml_type, const void *blocks, size_t n_blocks,

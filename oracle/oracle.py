@@ -18,6 +18,11 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "build", "librealm_oracle.so")
 
 GGML_Q8_0, GGML_Q4_K, GGML_Q6_K = 8, 12, 14
+GGML_Q4_0, GGML_Q4_1, GGML_Q5_0, GGML_Q5_1, GGML_Q8_1 = 2, 3, 6, 7, 9
+# bytes per block and elements per block of every format restated here
+BLOCK_BYTES = {GGML_Q4_K: 144, GGML_Q6_K: 210, GGML_Q8_0: 34, GGML_Q4_0: 18, GGML_Q4_1: 20,
+               GGML_Q5_0: 22, GGML_Q5_1: 24, GGML_Q8_1: 36}
+BLOCK_ELEMS = {t: (256 if t in (GGML_Q4_K, GGML_Q6_K) else 32) for t in BLOCK_BYTES}
 OK, INVALID_ARGUMENT, MODEL_PARSE_ERROR, PANIC = 0, 3, 4, -1
 
 _lib = None
@@ -91,8 +96,7 @@ def dequantize_tensor(ggml_type: int, data, element_count: int):
 
 def dequantize(ggml_type: int, blocks) -> np.ndarray:
     raw = np.ascontiguousarray(blocks).view(np.uint8).reshape(-1)
-    per = 32 if ggml_type == GGML_Q8_0 else 256
-    bb = {GGML_Q4_K: 144, GGML_Q6_K: 210, GGML_Q8_0: 34}[ggml_type]
+    per, bb = BLOCK_ELEMS[ggml_type], BLOCK_BYTES[ggml_type]
     rc, out = dequantize_tensor(ggml_type, raw, (raw.size // bb) * per)
     assert rc == OK, rc
     return out
@@ -118,7 +122,7 @@ def fused(ggml_type: int, blocks, x, batch: int, n: int, k: int, nan_fallback: b
 def candle_fused(ggml_type: int, blocks, x, batch: int, n: int, k: int):
     """CandleCpuBackend semantics; returns (status, out)."""
     raw = np.ascontiguousarray(blocks).view(np.uint8).reshape(-1)
-    bb = {GGML_Q4_K: 144, GGML_Q6_K: 210, GGML_Q8_0: 34}[ggml_type]
+    bb = BLOCK_BYTES[ggml_type]
     x = np.ascontiguousarray(x, np.float32).reshape(-1)
     out = np.zeros(max(batch * n, 1), np.float32)
     rc = lib().ro_candle_fused(ggml_type, _p(raw), raw.size // bb, _p(x), x.size, _p(out),

@@ -161,6 +161,66 @@ int ro_dequantize_q8_0(const ro_block_q8_0 *b, float *y)
  * element count (InvalidShape).  Q6_K and Q8_0 validate nothing: a trailing
  * partial block is ignored, elements beyond the last block stay 0, and an
  * element_count smaller than the blocks' output makes the reference panic. */
+/* The 32-element block formats, as the reference lays them out and
+ * dequantizes them (crates/realm-core/src/quant.rs:10-70, 226-370):
+ *   Q4_0 (18 B): f16 scale, 16 B nibbles; y[i] = (lo(b[i]) - 8) s,
+ *                y[i + 16] = (hi(b[i]) - 8) s
+ *   Q4_1 (20 B): f16 scale, f16 delta, nibbles as Q4_0, then + delta
+ *   Q5_0 (22 B): f16 scale, qh[4], ql[16]; element i: nibble i%2 of ql[i/2],
+ *                high bit (qh[i/8] >> (4 ((i%4) >= 2) + 2 ((i/4)%2))) & 1,
+ *                y = (q - 16) s
+ *   Q5_1 (24 B): f16 scale, f16 delta, qh[4], ql[16]; high bit
+ *                (qh[i/8] >> 4 ((i%4) >= 2)) & 1, y = (q - 16) s + delta
+ *   Q8_1 (36 B): f16 scale, f16 delta, 32 int8; y = q s + delta
+ * Each product and sum rounds to f32 on its own (no fused multiply-add). */
+int ro_block32_bytes(int type)
+{
+    switch (type) {
+    case RO_GGML_Q4_0: return 18;
+    case RO_GGML_Q4_1: return 20;
+    case RO_GGML_Q5_0: return 22;
+    case RO_GGML_Q5_1: return 24;
+    case RO_GGML_Q8_1: return 36;
+    default: return 0;
+    }
+}
+
+static uint16_t rd16(const uint8_t *p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+
+static void dequantize_block32(int type, const uint8_t *b, float *y)
+{
+    volatile float t; /* keeps each rounding step separate */
+    const float s = ro_f16_to_f32(rd16(b));
+    if (type == RO_GGML_Q4_0 || type == RO_GGML_Q4_1) {
+        const int q1 = type == RO_GGML_Q4_1;
+        const float d = q1 ? ro_f16_to_f32(rd16(b + 2)) : 0.0f;
+        const uint8_t *qs = b + (q1 ? 4 : 2);
+        for (int i = 0; i < 16; ++i) {
+            t = (float)((int)(qs[i] & 0x0F) - 8) * s;
+            y[i] = q1 ? (float)(t + d) : t;
+            t = (float)((int)(qs[i] >> 4) - 8) * s;
+            y[i + 16] = q1 ? (float)(t + d) : t;
+        }
+    } else if (type == RO_GGML_Q5_0 || type == RO_GGML_Q5_1) {
+        const int q1 = type == RO_GGML_Q5_1;
+        const float d = q1 ? ro_f16_to_f32(rd16(b + 2)) : 0.0f;
+        const uint8_t *qh = b + (q1 ? 4 : 2), *ql = qh + 4;
+        for (int i = 0; i < 32; ++i) {
+            const int lo = (i % 2 == 0) ? (ql[i / 2] & 0x0F) : (ql[i / 2] >> 4);
+            const int sh = 4 * ((i % 4) >= 2) + (q1 ? 0 : 2 * ((i / 4) % 2));
+            const int hi = (qh[i / 8] >> sh) & 1;
+            t = (float)((lo | (hi << 4)) - 16) * s;
+            y[i] = q1 ? (float)(t + d) : t;
+        }
+    } else { /* Q8_1 */
+        const float d = ro_f16_to_f32(rd16(b + 2));
+        for (int i = 0; i < 32; ++i) {
+            t = (float)(int8_t)b[4 + i] * s;
+            y[i] = (float)(t + d);
+        }
+    }
+}
+
 int ro_dequantize_tensor(const uint8_t *data, size_t nbytes, int type,
                          size_t element_count, float *out)
 {
@@ -198,6 +258,14 @@ int ro_dequantize_tensor(const uint8_t *data, size_t nbytes, int type,
             memcpy(&b, data + i * sizeof b, sizeof b);
             ro_dequantize_q8_0(&b, out + i * RO_QK8_0);
         }
+        return RO_OK;
+    }
+    if (ro_block32_bytes(type)) { /* quant.rs:773-856: no size validation */
+        const size_t bb = (size_t)ro_block32_bytes(type), nb = nbytes / bb;
+        if (nb * 32 > element_count)
+            return RO_PANIC;
+        for (size_t i = 0; i < nb; ++i)
+            dequantize_block32(type, data + i * bb, out + i * 32);
         return RO_OK;
     }
     return RO_GENERIC_FAILURE; /* format not restated here */
@@ -373,7 +441,7 @@ int ro_candle_fused(int type, const void *blocks, size_t nblocks,
                     const float *input, size_t input_len, float *out,
                     size_t batch, size_t n, size_t k)
 {
-    size_t per = type == RO_GGML_Q8_0 ? RO_QK8_0 : RO_QK_K;
+    size_t per = (type == RO_GGML_Q8_0 || ro_block32_bytes(type)) ? RO_QK8_0 : RO_QK_K;
     size_t total = nblocks * per;
     float *w = (float *)malloc((total ? total : 1) * sizeof(float));
     if (!w)
@@ -385,6 +453,9 @@ int ro_candle_fused(int type, const void *blocks, size_t nblocks,
             ro_dequantize_q6_k((const ro_block_q6_k *)blocks + i, w + i * per);
         else if (type == RO_GGML_Q8_0)
             ro_dequantize_q8_0((const ro_block_q8_0 *)blocks + i, w + i * per);
+        else if (ro_block32_bytes(type))
+            dequantize_block32(type, (const uint8_t *)blocks + i * ro_block32_bytes(type),
+                               w + i * per);
         else {
             free(w);
             return RO_GENERIC_FAILURE;

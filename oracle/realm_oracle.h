@@ -37,7 +37,12 @@ extern "C" {
 #define RO_PANIC (-1)
 
 /* ggml type ids (crates/realm-core/src/formats/gguf.rs:458-480) */
+#define RO_GGML_Q4_0 2
+#define RO_GGML_Q4_1 3
+#define RO_GGML_Q5_0 6
+#define RO_GGML_Q5_1 7
 #define RO_GGML_Q8_0 8
+#define RO_GGML_Q8_1 9
 #define RO_GGML_Q4_K 12
 #define RO_GGML_Q6_K 14
 
@@ -67,6 +72,9 @@ typedef struct {
 
 /* IEEE binary16 <-> binary32 (the `half` crate's f16::to_f32 / from_f32). */
 float ro_f16_to_f32(uint16_t h);
+/* Bytes per block of the 32-element formats Q4_0/Q4_1/Q5_0/Q5_1/Q8_1 (0 for
+ * others). */
+int ro_block32_bytes(int type);
 uint16_t ro_f32_to_f16(float f);
 
 void ro_get_scale_min_k4(int j, const uint8_t *scales, uint8_t *sc, uint8_t *m);

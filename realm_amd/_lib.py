@@ -103,6 +103,16 @@ SIGNATURES = {
                                             c_void_p, c_size_t, c_void_p, c_void_p]),
     "realm_hip_forward_layers_dev": (c_int, [c_void_p, c_size_t, c_void_p, c_size_t, c_size_t,
                                              c_void_p, c_void_p, c_size_t, c_void_p, c_void_p]),
+    "realm_hip_fused_dequant_matmul_q40": (c_int, [c_void_p, c_size_t, c_void_p, c_size_t,
+                                                   c_size_t, c_size_t, c_size_t, c_void_p]),
+    "realm_hip_fused_dequant_matmul_q41": (c_int, [c_void_p, c_size_t, c_void_p, c_size_t,
+                                                   c_size_t, c_size_t, c_size_t, c_void_p]),
+    "realm_hip_fused_dequant_matmul_q50": (c_int, [c_void_p, c_size_t, c_void_p, c_size_t,
+                                                   c_size_t, c_size_t, c_size_t, c_void_p]),
+    "realm_hip_fused_dequant_matmul_q51": (c_int, [c_void_p, c_size_t, c_void_p, c_size_t,
+                                                   c_size_t, c_size_t, c_size_t, c_void_p]),
+    "realm_hip_fused_dequant_matmul_q81": (c_int, [c_void_p, c_size_t, c_void_p, c_size_t,
+                                                   c_size_t, c_size_t, c_size_t, c_void_p]),
 }
 
 _lib = None

@@ -142,6 +142,19 @@ class HipGpuBackend:
     def fused_dequant_matmul_q80(self, blocks, input, batch_size, n, k):
         return self._fused(GGML_Q8_0, blocks, input, batch_size, n, k)
 
+    # the reference's 32-element formats: bytes per block (quant.rs:10-70)
+    BLOCK32_BYTES = {"q40": 18, "q41": 20, "q50": 22, "q51": 24, "q81": 36}
+
+    def _fused_raw(self, fmt: str, blocks, input, batch_size: int, n: int, k: int):
+        """Q4_0/Q4_1/Q5_0/Q5_1/Q8_1 blocks as raw bytes (or a record array)."""
+        raw = np.ascontiguousarray(blocks).view(np.uint8).reshape(-1)
+        x = np.ascontiguousarray(input, np.float32)
+        out = np.empty(batch_size * n, np.float32)
+        fn = getattr(self.lib, f"realm_hip_fused_dequant_matmul_{fmt}")
+        self._check(fn(_ptr(raw), raw.size // self.BLOCK32_BYTES[fmt], _ptr(x), x.size,
+                       batch_size, n, k, _ptr(out)))
+        return out
+
     def _unsupported(self, fmt: str):
         raise BackendError(BACKEND_UNSUPPORTED, f"{fmt} is not supported by the HIP backend")
 
@@ -157,20 +170,20 @@ class HipGpuBackend:
     def fused_dequant_matmul_q3k(self, *a):
         self._unsupported("Q3_K")
 
-    def fused_dequant_matmul_q40(self, *a):
-        self._unsupported("Q4_0")
+    def fused_dequant_matmul_q40(self, blocks, input, batch_size, n, k):
+        return self._fused_raw("q40", blocks, input, batch_size, n, k)
 
-    def fused_dequant_matmul_q41(self, *a):
-        self._unsupported("Q4_1")
+    def fused_dequant_matmul_q41(self, blocks, input, batch_size, n, k):
+        return self._fused_raw("q41", blocks, input, batch_size, n, k)
 
-    def fused_dequant_matmul_q50(self, *a):
-        self._unsupported("Q5_0")
+    def fused_dequant_matmul_q50(self, blocks, input, batch_size, n, k):
+        return self._fused_raw("q50", blocks, input, batch_size, n, k)
 
-    def fused_dequant_matmul_q51(self, *a):
-        self._unsupported("Q5_1")
+    def fused_dequant_matmul_q51(self, blocks, input, batch_size, n, k):
+        return self._fused_raw("q51", blocks, input, batch_size, n, k)
 
-    def fused_dequant_matmul_q81(self, *a):
-        self._unsupported("Q8_1")
+    def fused_dequant_matmul_q81(self, blocks, input, batch_size, n, k):
+        return self._fused_raw("q81", blocks, input, batch_size, n, k)
 
     # ------------------------------------------------------------ extras
     def set_nan_fallback(self, enable: bool) -> None:

@@ -100,8 +100,19 @@ int hip_code(hipError_t e)
 constexpr int GGML_Q8_0 = REALM_GGML_Q8_0, GGML_Q4_K = REALM_GGML_Q4_K,
               GGML_Q6_K = REALM_GGML_Q6_K;
 
-size_t block_bytes(int t) { return t == GGML_Q4_K ? 144 : t == GGML_Q6_K ? 210 : 34; }
-size_t block_elems(int t) { return t == GGML_Q8_0 ? 32 : 256; }
+// The reference's 32-element formats Q4_0, Q4_1, Q5_0, Q5_1, Q8_1
+// (quant.rs:10-70): dequantized on the device, products through the dense
+// f32 GEMM (as CandleGpuBackend's fused_dequant_matmul_q40 etc.).
+bool is_block32(int t) { return t == 2 || t == 3 || t == 6 || t == 7 || t == 9; }
+size_t block32_bytes(int t)
+{
+    return t == 2 ? 18 : t == 3 ? 20 : t == 6 ? 22 : t == 7 ? 24 : t == 9 ? 36 : 0;
+}
+size_t block_bytes(int t)
+{
+    return t == GGML_Q4_K ? 144 : t == GGML_Q6_K ? 210 : is_block32(t) ? block32_bytes(t) : 34;
+}
+size_t block_elems(int t) { return (t == GGML_Q4_K || t == GGML_Q6_K) ? 256 : 32; }
 size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 size_t round_up(size_t v, size_t m) { return (v + m - 1) / m * m; }
 const char *fmt_name(int t) { return t == GGML_Q4_K ? "q4k" : t == GGML_Q6_K ? "q6k" : "q80"; }
@@ -941,9 +952,62 @@ int validate_fused(int type, size_t n_blocks, size_t input_len, size_t batch, si
     return REALM_OK;
 }
 
+int dense_launch(const float *da, const float *db, float *dc, size_t m, size_t k, size_t n,
+                 int bt, hipStream_t s);
+
+// Q4_0 / Q4_1 / Q5_0 / Q5_1 / Q8_1 (candle_backend.rs:837-1103): validated
+// as the reference does, dequantized on the device into f32 W [n][k], then
+// y = x W^T on the f32 MFMA GEMM.
+int fused_block32(int type, const void *blocks, size_t n_blocks, const float *input,
+                  size_t input_len, size_t batch, size_t n, size_t k, float *out)
+{
+    if (k % 32)
+        return fail(REALM_INVALID_ARGUMENT, "K dimension " + std::to_string(k) +
+                                                " must be multiple of 32");
+    if (n_blocks != n * (k / 32))
+        return fail(REALM_INVALID_ARGUMENT, "Expected " + std::to_string(n * (k / 32)) +
+                                                " blocks, got " + std::to_string(n_blocks));
+    if (input_len != batch * k)
+        return fail(REALM_INVALID_ARGUMENT, "Input length " + std::to_string(input_len) +
+                                                " does not match batch_size * k = " +
+                                                std::to_string(batch * k));
+    if (!out || (n_blocks && !blocks) || (input_len && !input))
+        return fail(REALM_INVALID_ARGUMENT, "null pointer argument");
+    if (n > (size_t)INT32_MAX || k > (size_t)INT32_MAX || batch > (size_t)INT32_MAX)
+        return fail(REALM_INVALID_ARGUMENT, "dimension exceeds 2^31-1");
+    CHECK(ensure_init());
+    if (batch == 0 || n == 0)
+        return REALM_OK;
+    if (k == 0) {
+        std::memset(out, 0, batch * n * sizeof(float));
+        return REALM_OK;
+    }
+    hipStream_t s;
+    CHECK(thread_stream(&s));
+    void *raw, *w, *dx, *dy;
+    const size_t bb = block32_bytes(type);
+    CHECK(ws_get(s, WS_RAW, n_blocks * bb, &raw));
+    CHECK(ws_get(s, WS_WEIGHT, n * k * 4, &w));
+    CHECK(ws_get(s, WS_X, batch * k * 4, &dx));
+    CHECK(ws_get(s, WS_Y, batch * n * 4, &dy));
+    HIP_TRY(hipMemcpyAsync(raw, blocks, n_blocks * bb, hipMemcpyHostToDevice, s));
+    HIP_TRY(hipMemcpyAsync(dx, input, batch * k * 4, hipMemcpyHostToDevice, s));
+    long long lnb = (long long)n_blocks;
+    int it = type;
+    void *args[] = {&raw, &w, &lnb, &it};
+    CHECK(launch("realm_dequant_q32", dim3((unsigned)((n_blocks * 32 + 255) / 256)), dim3(256),
+                 0, s, args));
+    CHECK(dense_launch((const float *)dx, (const float *)w, (float *)dy, batch, k, n, 1, s));
+    HIP_TRY(hipMemcpyAsync(out, dy, batch * n * 4, hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipStreamSynchronize(s));
+    return REALM_OK;
+}
+
 int fused_host(int type, const void *blocks, size_t n_blocks, const float *input,
                size_t input_len, size_t batch, size_t n, size_t k, float *out)
 {
+    if (is_block32(type))
+        return fused_block32(type, blocks, n_blocks, input, input_len, batch, n, k, out);
     if (type != GGML_Q4_K && type != GGML_Q6_K && type != GGML_Q8_0)
         return fail(REALM_BACKEND_UNSUPPORTED,
                     "ggml type " + std::to_string(type) + " is not supported by the HIP backend");
@@ -1439,6 +1503,46 @@ REALM_API int realm_hip_forward_layer_dev(const realm_layer *L, const float *d_h
                                         &d_v_cache, max_seq_len, d_out, stream);
 }
 
+REALM_API int realm_hip_fused_dequant_matmul_q40(const void *blocks, size_t n_blocks,
+                                                 const float *input, size_t input_len,
+                                                 size_t batch_size, size_t n, size_t k,
+                                                 float *out)
+{
+    return fused_host(2, blocks, n_blocks, input, input_len, batch_size, n, k, out);
+}
+
+REALM_API int realm_hip_fused_dequant_matmul_q41(const void *blocks, size_t n_blocks,
+                                                 const float *input, size_t input_len,
+                                                 size_t batch_size, size_t n, size_t k,
+                                                 float *out)
+{
+    return fused_host(3, blocks, n_blocks, input, input_len, batch_size, n, k, out);
+}
+
+REALM_API int realm_hip_fused_dequant_matmul_q50(const void *blocks, size_t n_blocks,
+                                                 const float *input, size_t input_len,
+                                                 size_t batch_size, size_t n, size_t k,
+                                                 float *out)
+{
+    return fused_host(6, blocks, n_blocks, input, input_len, batch_size, n, k, out);
+}
+
+REALM_API int realm_hip_fused_dequant_matmul_q51(const void *blocks, size_t n_blocks,
+                                                 const float *input, size_t input_len,
+                                                 size_t batch_size, size_t n, size_t k,
+                                                 float *out)
+{
+    return fused_host(7, blocks, n_blocks, input, input_len, batch_size, n, k, out);
+}
+
+REALM_API int realm_hip_fused_dequant_matmul_q81(const void *blocks, size_t n_blocks,
+                                                 const float *input, size_t input_len,
+                                                 size_t batch_size, size_t n, size_t k,
+                                                 float *out)
+{
+    return fused_host(9, blocks, n_blocks, input, input_len, batch_size, n, k, out);
+}
+
 REALM_API int realm_hip_fused_dequant_matmul_q4k(const void *blocks, size_t n_blocks,
                                                  const float *input, size_t input_len,
                                                  size_t batch_size, size_t n, size_t k,
@@ -1488,7 +1592,7 @@ REALM_API int32_t realm_hip_candle_matmul_transposed(uint8_t *mem, size_t mem_le
 REALM_API int realm_hip_dequantize(int type, const void *data, size_t nbytes,
                                    size_t element_count, float *out)
 {
-    if (type != GGML_Q4_K && type != GGML_Q6_K && type != GGML_Q8_0)
+    if (type != GGML_Q4_K && type != GGML_Q6_K && type != GGML_Q8_0 && !is_block32(type))
         return fail(REALM_BACKEND_UNSUPPORTED,
                     "ggml type " + std::to_string(type) + " is not supported by the HIP backend");
     size_t bb = block_bytes(type), qk = block_elems(type);
@@ -1518,10 +1622,17 @@ REALM_API int realm_hip_dequantize(int type, const void *data, size_t nbytes,
     CHECK(ws_get(s, WS_Y, nb * qk * 4, &dy));
     HIP_TRY(hipMemcpyAsync(raw, data, nb * bb, hipMemcpyHostToDevice, s));
     long long lnb = (long long)nb;
-    void *args[] = {&raw, &dy, &lnb};
-    size_t threads = nb * (type == GGML_Q4_K ? 128 : type == GGML_Q6_K ? 64 : 32);
-    CHECK(launch(std::string("realm_dequant_") + fmt_name(type),
-                 dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, args));
+    if (is_block32(type)) {
+        int it = type;
+        void *args[] = {&raw, &dy, &lnb, &it};
+        CHECK(launch("realm_dequant_q32", dim3((unsigned)((nb * 32 + 255) / 256)), dim3(256), 0, s,
+                     args));
+    } else {
+        void *args[] = {&raw, &dy, &lnb};
+        size_t threads = nb * (type == GGML_Q4_K ? 128 : type == GGML_Q6_K ? 64 : 32);
+        CHECK(launch(std::string("realm_dequant_") + fmt_name(type),
+                     dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, args));
+    }
     HIP_TRY(hipMemcpyAsync(out, dy, nb * qk * 4, hipMemcpyDeviceToHost, s));
     HIP_TRY(hipStreamSynchronize(s));
     return REALM_OK;

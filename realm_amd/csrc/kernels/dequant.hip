@@ -193,3 +193,36 @@ extern "C" __global__ __launch_bounds__(256) void realm_repack_q80(
     if (i < 2)
         dq[(n * (kp / 32) + kb) * 2 + i] = blk[i];
 }
+
+// The 32-element block formats of the reference (crates/realm-core/src/
+// quant.rs:10-70, 226-370), one thread per output element: Q4_0 (type 2,
+// 18 B), Q4_1 (3, 20 B), Q5_0 (6, 22 B), Q5_1 (7, 24 B), Q8_1 (9, 36 B).
+// Products and sums are separate f32 roundings (__fmul_rn / __fadd_rn), as
+// the reference's mul-then-add, so the output is bit-exact.
+extern "C" __global__ __launch_bounds__(256) void realm_dequant_q32(const uint8_t *raw, float *y,
+                                                                   long long nb, int type)
+{
+    const long long e = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (e >= nb * 32)
+        return;
+    const int i = (int)(e & 31);
+    const int bb = type == 2 ? 18 : type == 3 ? 20 : type == 6 ? 22 : type == 7 ? 24 : 36;
+    const uint8_t *b = raw + (e >> 5) * bb;
+    const float s = realm::f16_bits_to_f32(b[0] | (b[1] << 8));
+    const bool delta = type == 3 || type == 7 || type == 9;
+    const float d = delta ? realm::f16_bits_to_f32(b[2] | (b[3] << 8)) : 0.f;
+    int q;
+    if (type == 2 || type == 3) {
+        const uint8_t byte = b[(delta ? 4 : 2) + (i & 15)];
+        q = (i < 16 ? (byte & 0x0F) : (byte >> 4)) - 8;
+    } else if (type == 6 || type == 7) {
+        const uint8_t *qh = b + (delta ? 4 : 2), *ql = qh + 4;
+        const int lo = (i & 1) ? (ql[i >> 1] >> 4) : (ql[i >> 1] & 0x0F);
+        const int sh = 4 * ((i & 3) >= 2) + (type == 6 ? 2 * ((i >> 2) & 1) : 0);
+        q = (lo | (((qh[i >> 3] >> sh) & 1) << 4)) - 16;
+    } else {
+        q = (int8_t)b[4 + i];
+    }
+    const float t = __fmul_rn((float)q, s);
+    y[e] = delta ? __fadd_rn(t, d) : t;
+}
