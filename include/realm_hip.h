@@ -189,7 +189,10 @@ int realm_hip_dequantize(int ggml_type, const void *data, size_t nbytes,
  * layout (repacked on the GPU).  Replaces the per-call f32 upload of
  * CandleGpuBackend (candle_backend.rs:484-490) for the weights that
  * realm_forward_layer reads every call (memory64_host.rs:1958-2225).
- * ggml_type is 12 (Q4_K), 14 (Q6_K) or 8 (Q8_0). */
+ * ggml_type is 12 (Q4_K), 14 (Q6_K) or 8 (Q8_0); the 32-element formats 2
+ * (Q4_0), 3 (Q4_1), 6 (Q5_0), 7 (Q5_1) and 9 (Q8_1) are kept dequantized
+ * (f32, 4 bytes per weight) and multiply on the f32 GEMM; they take no bf16
+ * input and no LoRA (REALM_BACKEND_UNSUPPORTED). */
 int realm_hip_weights_register(int ggml_type, const void *blocks, size_t nbytes,
                                size_t n, size_t k, uint64_t *handle);
 int realm_hip_weights_release(uint64_t handle);
@@ -409,7 +412,8 @@ int realm_hip_gguf_meta_str(uint64_t model, const char *key, char *buf, size_t c
 /* GGUFParser::extract_config (gguf.rs:212-280). */
 int realm_hip_gguf_config(uint64_t model, realm_gguf_config *cfg);
 
-/* Upload every 2-D Q4_K / Q6_K / Q8_0 tensor of a parsed image once, as
+/* Upload every 2-D Q4_K / Q6_K / Q8_0 tensor (and Q4_0 / Q4_1 / Q5_0 / Q5_1
+ * / Q8_1, resident dequantized) of a parsed image once, as
  * resident device weights (realm_hip_weights_register with n = dims4[1],
  * k = dims4[0]), in place of the per-call tensor copies of
  * ModelStorage / quantized_to_weight_format (model_storage.rs:444-487,

@@ -14,7 +14,8 @@
 //    (as TensorLoader, tensor_loader.rs:76; ModelStorage::store_model reads
 //    at the bare offset);
 //  * a Q8_0 tensor holds 34-byte blocks (BlockQ8_0, quant.rs:52-59), where
-//    TensorDesc::new counts 33 (tensor.rs:145-150).
+//    TensorDesc::new counts 33 (tensor.rs:145-150), and Q4_0 / Q4_1 tensors
+//    18- and 20-byte blocks (quant.rs:10-28), where it counts 16.
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
@@ -164,14 +165,19 @@ int read_value(Reader &r, MetaValue *v)
 }
 
 // Bytes of a tensor of ggml type t with nel elements, for the types whose
-// size this path relies on (tensor.rs:135-175; Q8_0 as 34-byte blocks); 0
-// for the others, which are listed but never registered.
+// size this path relies on (tensor.rs:135-175, with the block sizes of
+// quant.rs:10-70); 0 for the others, which are listed but never registered.
 uint64_t tensor_bytes(int32_t t, uint64_t nel)
 {
     switch (t) {
     case 0: return nel * 4;          // F32
     case 1: return nel * 2;          // F16
+    case 2: return nel / 32 * 18;    // Q4_0 (BlockQ4_0; TensorDesc counts 16)
+    case 3: return nel / 32 * 20;    // Q4_1 (BlockQ4_1; TensorDesc counts 16)
+    case 6: return nel / 32 * 22;    // Q5_0
+    case 7: return nel / 32 * 24;    // Q5_1
     case 8: return nel / 32 * 34;    // Q8_0
+    case 9: return nel / 32 * 36;    // Q8_1
     case 12: return nel / 256 * 144; // Q4_K
     case 14: return nel / 256 * 210; // Q6_K
     default: return 0;
@@ -454,7 +460,9 @@ REALM_API int realm_hip_gguf_register(uint64_t model, const void *bytes, size_t 
         for (size_t i = 0; i < m->tensors.size(); ++i) {
             const Tensor &t = m->tensors[i];
             const bool quant = t.type == REALM_GGML_Q4_K || t.type == REALM_GGML_Q6_K ||
-                               t.type == REALM_GGML_Q8_0;
+                               t.type == REALM_GGML_Q8_0 || t.type == REALM_GGML_Q4_0 ||
+                               t.type == REALM_GGML_Q4_1 || t.type == REALM_GGML_Q5_0 ||
+                               t.type == REALM_GGML_Q5_1 || t.type == REALM_GGML_Q8_1;
             if (!quant || t.dims.size() != 2 || t.weight)
                 continue;
             if (t.abs > len || t.nbytes > len - t.abs)

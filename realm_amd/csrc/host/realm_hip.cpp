@@ -904,9 +904,20 @@ int run_gemm(const Weight &w, const void *d_x, bool bf16, size_t M, float *d_y, 
     return gemm_launch(w, p, bf16, M, tile, d_y, s, lora);
 }
 
+int dense_launch(const float *da, const float *db, float *dc, size_t m, size_t k, size_t n,
+                 int bt, hipStream_t s);
+
 int run_matmul(const Weight &w, const void *d_x, bool bf16, size_t M, float *d_y,
                hipStream_t s, const LoraCall *lora)
 {
+    if (is_block32(w.type)) { // resident as dequantized f32 [n][k]: y = x W^T
+        if (bf16 || lora)
+            return fail(REALM_BACKEND_UNSUPPORTED,
+                        "bf16 input and LoRA take Q4_K, Q6_K or Q8_0 weights");
+        if (M == 0 || w.n == 0)
+            return REALM_OK;
+        return dense_launch((const float *)d_x, (const float *)w.w0, d_y, M, w.k, w.n, 1, s);
+    }
     if (M <= 4 && !bf16 && !lora) {
         const Weight *ws[1] = {&w};
         float *ys[1] = {d_y};
@@ -1643,7 +1654,7 @@ REALM_API int realm_hip_weights_register(int type, const void *blocks, size_t nb
 {
     if (!handle)
         return fail(REALM_INVALID_ARGUMENT, "handle is null");
-    if (type != GGML_Q4_K && type != GGML_Q6_K && type != GGML_Q8_0)
+    if (type != GGML_Q4_K && type != GGML_Q6_K && type != GGML_Q8_0 && !is_block32(type))
         return fail(REALM_BACKEND_UNSUPPORTED,
                     "ggml type " + std::to_string(type) + " is not supported by the HIP backend");
     size_t qk = block_elems(type);
@@ -1660,6 +1671,38 @@ REALM_API int realm_hip_weights_register(int type, const void *blocks, size_t nb
     CHECK(ensure_init());
     hipStream_t s;
     CHECK(thread_stream(&s));
+    if (is_block32(type)) {
+        // the 32-element formats stay resident dequantized (f32 [n][k],
+        // 4 bytes per weight), their products on the f32 GEMM
+        void *dev = nullptr, *raw = nullptr;
+        CHECK(ws_get(s, WS_RAW, nbytes, &raw));
+        HIP_TRY(hipMalloc(&dev, n * k * 4));
+        long long lnb = (long long)(n * (k / 32));
+        int it = type;
+        void *args[] = {&raw, &dev, &lnb, &it};
+        int rc = hipMemcpyAsync(raw, blocks, nbytes, hipMemcpyHostToDevice, s) == hipSuccess
+                     ? launch("realm_dequant_q32", dim3((unsigned)((n * k + 255) / 256)),
+                              dim3(256), 0, s, args)
+                     : fail(REALM_GENERIC_FAILURE, "upload failed");
+        if (rc == REALM_OK && hipStreamSynchronize(s) != hipSuccess)
+            rc = fail(REALM_GENERIC_FAILURE, "dequantization failed");
+        if (rc != REALM_OK) {
+            (void)hipFree(dev);
+            return rc;
+        }
+        Weight w;
+        w.type = type;
+        w.n = n;
+        w.k = w.kx = k;
+        w.bytes = n * k * 4;
+        w.dev = dev;
+        w.w0 = dev;
+        std::lock_guard<std::mutex> lk(g_mu);
+        uint64_t h = g_next_handle++;
+        g_weights[h] = w;
+        *handle = h;
+        return REALM_OK;
+    }
     size_t off[3], kx;
     size_t total = layout(type, n, k, off, &kx);
     void *dev;
@@ -1766,6 +1809,11 @@ REALM_API int realm_hip_weights_matmul_group_dev(const uint64_t *handles, size_t
         return fail(REALM_INVALID_ARGUMENT, "batch exceeds 2^31-1");
     hipStream_t s;
     CHECK(pick_stream(stream, &s));
+    if (is_block32(w[0].type)) { // dequantized f32 weights: one dense product each
+        for (size_t i = 0; i < count; ++i)
+            CHECK(run_matmul(w[i], d_input, false, batch, d_outs[i], s, nullptr));
+        return REALM_OK;
+    }
     if (batch >= 1 && batch <= 4) {
         int rc = run_gemv(wp, (int)count, d_input, (int)batch, d_outs, s);
         if (rc != REALM_BACKEND_UNSUPPORTED)
@@ -1958,6 +2006,8 @@ namespace {
 int lora_lookup(uint64_t wh, uint64_t sh, size_t batch, Weight *w, AdapterSet *set)
 {
     CHECK(get_weight(wh, w));
+    if (is_block32(w->type))
+        return fail(REALM_BACKEND_UNSUPPORTED, "multi-LoRA takes Q4_K, Q6_K or Q8_0 base weights");
     {
         std::lock_guard<std::mutex> lk(g_mu);
         auto it = g_sets.find(sh);

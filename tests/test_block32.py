@@ -112,3 +112,43 @@ def test_fused_validation(backend):
         backend.fused_dequant_matmul_q40(raw, np.zeros(64, np.float32), 1, 1, 64)
     with pytest.raises(InvalidShape):   # input length
         backend.fused_dequant_matmul_q40(raw, np.zeros(63, np.float32), 1, 2, 64)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("t", [2, 3, 6, 7, 9])
+def test_resident_weights(backend, oracle, t):
+    """Registered once (kept dequantized on the device), then products at 1,
+    3 and 20 tokens, alone and in a grouped call, against the oracle; LoRA
+    on such a base is refused."""
+    from realm_amd.backend import BackendError
+    g = np.random.default_rng(500 + t)
+    n, k = 96, 512
+    raw = _random_blocks(g, t, n * k // 32)
+    h = backend.register_weights(t, raw, n, k)
+    h2 = backend.register_weights(t, raw, n, k)
+    try:
+        for m in (1, 3, 20):
+            x = g.standard_normal(m * k).astype(np.float32)
+            got = backend.weights_matmul(h, x.reshape(m, k))
+            rc, want = oracle.candle_fused(t, raw, x, m, n, k)
+            assert rc == 0 and rel_l2(got, want.reshape(m, n)) < 1e-3, m
+            dx = backend.alloc(x.nbytes).upload(x)
+            dys = [backend.alloc(m * n * 4) for _ in range(2)]
+            backend.matmul_group_dev([h, h2], dx.ptr, m, [d.ptr for d in dys])
+            backend.synchronize()
+            for d in dys:
+                assert rel_l2(d.download(np.float32, m * n), want) < 1e-3
+            for b in dys + [dx]:
+                b.close()
+        a = (g.standard_normal((8, k)) * 0.01).astype(np.float32)
+        b = (g.standard_normal((n, 8)) * 0.01).astype(np.float32)
+        ah = backend.lora_register(a, b, 8, 16.0, k, n)
+        sh = backend.lora_set_create([ah])
+        with pytest.raises(BackendError):
+            backend.multi_lora_matmul(h, sh, g.standard_normal((2, k)).astype(np.float32),
+                                      np.zeros(2, np.int32))
+        backend.lora_set_release(sh)
+        backend.lora_release(ah)
+    finally:
+        backend.release_weights(h)
+        backend.release_weights(h2)
