@@ -62,12 +62,13 @@ class Model7B:
         self.be = be
         g = synth.rng(1)
         host = [(name, t, n, k, synth.blocks(g, t, n, k)) for name, t, n, k in LAYER]
+        self.host = {name: b for name, _t, _n, _k, b in host}
         self.layers = []
         for _ in range(layers):
             self.layers.append([(name, t, n, k, be.register_weights(t, b, n, k))
                                 for name, t, n, k, b in host])
-        self.x = {k: be.alloc(max_m * k * 4).upload(synth.activations(g, max_m, k))
-                  for k in (4096, 11008)}
+        self.x_host = {k: synth.activations(g, max_m, k) for k in (4096, 11008)}
+        self.x = {k: be.alloc(max_m * k * 4).upload(self.x_host[k]) for k in (4096, 11008)}
         self.y = {name: be.alloc(max_m * n * 4) for name, _, n, _ in LAYER}
 
     # launch groups of a layer (indices into LAYER): matrices in one group
@@ -425,34 +426,60 @@ def dense(be, stream: int, reps: int) -> dict:
     return out
 
 
-def cpu_baseline(seconds: float) -> tuple[dict, dict]:
-    """The oracle's C restatement of realm-compute-cpu on this host's cores:
-    Q4_K 4096x4096 matvec (batch 1), dequantize-row-then-dot on all cores, and
-    fused.rs semantics on one core.  Bounded to about `seconds` each."""
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def median_rate(fn, nbytes: int, seconds: float, trials: int = 10) -> tuple[float, int]:
+    """Median GB/s over `trials` timed trials of about seconds/trials each
+    (after one warm-up call); also the total number of calls."""
+    fn()
+    rates, calls = [], 0
+    for _ in range(trials):
+        t0, reps = time.perf_counter(), 0
+        while reps == 0 or time.perf_counter() - t0 < seconds / trials:
+            fn()
+            reps += 1
+        rates.append(nbytes * reps / (time.perf_counter() - t0) / 1e9)
+        calls += reps
+    return float(np.median(rates)), calls
+
+
+def cpu_baseline(seconds: float, blocks, x, gpu_y) -> tuple[dict, dict]:
+    """The oracle's C restatement of realm-compute-cpu on this host's cores,
+    on the timed step's own Wq (Q4_K 4096x4096) and input (batch 1):
+    dequantize-row-then-dot on all cores (OpenMP, one row per iteration),
+    and fused.rs semantics on one core; each the median of 10 trials within
+    about `seconds`.  The oracle's output doubles as the check of the GPU's
+    Wq output from the last timed step (gpu_y): relative L2 error reported."""
     from oracle import oracle as o  # checker/baseline only
-    g = synth.rng(1)
     n = k = 4096
-    blocks = synth.q4k_blocks(g, n, k)
-    x = synth.activations(g, 1, k)
     nbytes = alg_bytes(GGML_Q4_K, n, k, 1)
     threads = len(os.sched_getaffinity(0))
-    used, _ = o.fused_parallel(GGML_Q4_K, blocks, x, 1, n, k, threads)
-    t0, reps = time.perf_counter(), 0
-    while time.perf_counter() - t0 < seconds:
-        o.fused_parallel(GGML_Q4_K, blocks, x, 1, n, k, threads)
-        reps += 1
-    par = nbytes * reps / (time.perf_counter() - t0) / 1e9
-    t0, reps1 = time.perf_counter(), 0
-    while time.perf_counter() - t0 < seconds:
-        o.fused(GGML_Q4_K, blocks, x, 1, n, k)
-        reps1 += 1
-    one = nbytes * reps1 / (time.perf_counter() - t0) / 1e9
+    used, ref = o.fused_parallel(GGML_Q4_K, blocks, x, 1, n, k, threads)
+    err = float(np.linalg.norm(gpu_y - ref) / np.linalg.norm(ref))
+    par, reps = median_rate(lambda: o.fused_parallel(GGML_Q4_K, blocks, x, 1, n, k, threads),
+                            nbytes, seconds)
+    one, reps1 = median_rate(lambda: o.fused(GGML_Q4_K, blocks, x, 1, n, k), nbytes, seconds)
+    env = {v: os.environ.get(v) for v in ("OMP_NUM_THREADS", "OMP_PROC_BIND", "OMP_PLACES")}
     base = {"value": round(par, 3), "unit": "GB/s", "cores": int(used), "kind": "port",
-            "sample": f"Q4_K 4096x4096 matvec, batch 1, dequantize row + f32 dot "
-                      f"(CandleCpuBackend semantics), {reps} reps in ~{seconds:.0f}s on {used} "
-                      f"threads; oracle/realm_oracle.c"}
+            "sample": f"Q4_K 4096x4096 matvec (the timed step's Wq and input), batch 1, "
+                      f"dequantize row + f32 dot (CandleCpuBackend semantics), median of 10 "
+                      f"trials, {reps} calls in ~{seconds:.0f}s on {used} OpenMP threads; "
+                      f"oracle/realm_oracle.c",
+            "cpu_model": cpu_model(), "omp_env": env,
+            "gpu_check": {"output": "Wq of the last timed step", "rel_l2": err,
+                          "ok": bool(err < 1e-3)}}
     single = {"value": round(one, 3), "unit": "GB/s", "cores": 1,
-              "sample": f"same matvec with fused.rs semantics, {reps1} reps, 1 thread"}
+              "sample": f"same matvec with fused.rs semantics, median of 10 trials, "
+                        f"{reps1} calls, 1 thread"}
     return base, single
 
 
@@ -525,6 +552,9 @@ def main() -> int:
     wall = (time.perf_counter() - t0) / args.steps
     ev_ms = be.elapsed_ms(e0, e1) / args.steps
     be.graph_release(graph)
+    # outside the timed region: what the last step wrote for Wq (checked
+    # against the oracle in the CPU-baseline leg)
+    wq_out = model.y["wq"].download(np.float32, 4096)
     step_bytes = model.bytes_per_step(m)
     value = step_bytes / wall / 1e9
     log(f"decode b1: {wall * 1e3:.3f} ms/step (events {ev_ms:.3f}), {value:.1f} GB/s")
@@ -553,6 +583,7 @@ def main() -> int:
                                          "tok_per_s": round(mb / (ms * 1e-3), 1),
                                          "gb_per_s": round(gbs, 1)}
             log(f"decode b{mb}: {ms:.3f} ms/step, {gbs:.1f} GB/s")
+    wq_host, x_host = model.host["wq"], model.x_host[4096][:1]
     model.close()
     if args.extra_only == "batched":
         return 0
@@ -566,7 +597,7 @@ def main() -> int:
         log(f"config4: {extra['config4_70b_layer']}")
         extra["dense_f32"] = dense(be, stream, 10)
         log(f"dense: {extra['dense_f32']}")
-        cpu, cpu1 = cpu_baseline(args.cpu_seconds)
+        cpu, cpu1 = cpu_baseline(args.cpu_seconds, wq_host, x_host, wq_out)
         extra["cpu_baseline_1thread"] = cpu1
         log(f"cpu baseline: {cpu}")
 

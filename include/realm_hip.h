@@ -438,12 +438,21 @@ int realm_hip_gguf_release(uint64_t model);
 /* Capture the device-pointer calls issued on `stream` (not NULL) between
  * begin and end into a replayable HIP graph, for launch-bound loops such as a
  * decode step.  Run the same calls once eagerly before capturing so that the
- * library's scratch buffers are already sized (nothing may allocate during a
- * capture).  No memset is recorded into a graph. */
+ * library's scratch buffers are already sized.  No memset is recorded into a
+ * graph.  While a graph captured on a stream is alive, the stream's scratch
+ * buffers are never freed: a later, larger eager call on that stream gets new
+ * buffers and the replaced ones are kept until the stream's last graph is
+ * released, so replays stay valid. */
 int realm_hip_graph_begin(void *stream);
 int realm_hip_graph_end(void *stream, uint64_t *graph_handle);
 int realm_hip_graph_launch(uint64_t graph_handle, void *stream);
 int realm_hip_graph_release(uint64_t graph_handle);
+
+/* The scratch buffers of `stream` (NULL = this thread's): bytes held,
+ * replaced buffers kept for live graphs, live graphs captured on it.  No
+ * counterpart in the reference (which has no device scratch); for tests and
+ * memory accounting. */
+int realm_hip_workspace_info(void *stream, size_t *bytes, size_t *retired, int *graphs);
 
 /* ----------------------------------------- device memory and timing */
 

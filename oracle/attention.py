@@ -60,7 +60,10 @@ def attention(q, k, v, seq_len: int, kv_len: int, position: int, num_heads: int,
         for i in range(seq_len):
             row = scores[i].copy()
             row[np.arange(kv_len) > position + i] = -np.inf
-            mx = np.max(row) if kv_len else -np.inf
+            # the max is a fold of f32::max from -inf: NaN scores are skipped
+            # (standard.rs:114-116)
+            kept = row[~np.isnan(row)]
+            mx = np.max(kept) if kept.size else -np.inf
             e = np.where(np.isfinite(row), np.exp(row - mx), 0).astype(np.float32)
             s = np.float32(e.sum(dtype=np.float32))
             if s > 0:

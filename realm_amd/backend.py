@@ -319,6 +319,14 @@ class HipGpuBackend:
     def graph_release(self, graph: int) -> None:
         self._check(self.lib.realm_hip_graph_release(graph))
 
+    def workspace_info(self, stream=None) -> tuple:
+        """(bytes held, replaced buffers kept for live graphs, live graphs) of
+        a stream's scratch buffers."""
+        nb, ret, gr = ctypes.c_size_t(), ctypes.c_size_t(), ctypes.c_int()
+        self._check(self.lib.realm_hip_workspace_info(
+            c_void_p(stream or 0), ctypes.byref(nb), ctypes.byref(ret), ctypes.byref(gr)))
+        return nb.value, ret.value, gr.value
+
     def multi_lora_matmul_dev(self, wh: int, sh: int, d_x: int, batch: int, d_ids: int,
                               d_y: int, stream=None) -> None:
         self._check(self.lib.realm_hip_multi_lora_matmul_dev(

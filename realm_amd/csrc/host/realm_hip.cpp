@@ -247,30 +247,58 @@ int pick_stream(void *user, hipStream_t *s)
 
 // Per-stream scratch buffers (grow-only).  Work on one stream is ordered, so
 // reusing a stream's buffers for its next call is safe.
+//
+// A HIP graph captured on a stream holds the addresses of the buffers its
+// calls used.  So while such a graph is alive (captured through
+// realm_hip_graph_begin/end and not yet released), or while the stream is
+// capturing, a buffer that has to grow is not freed: it goes on the
+// stream's retired list, freed when the stream's last graph is released.
+// Buffers replaced while the stream was capturing outside
+// realm_hip_graph_begin are never freed (the library cannot tell when such
+// a graph ends).
 enum Slot { WS_RAW, WS_WEIGHT, WS_X, WS_Y, WS_XH, WS_XL, WS_XM, WS_TS, WS_U, WS_IDS, WS_PART,
-            WS_LAYER, WS_ATT, WS_N };
+            WS_LAYER, WS_ATT, WS_NF, WS_N };
 
 struct Workspace {
     void *buf[WS_N] = {};
     size_t cap[WS_N] = {};
+    int graphs = 0;              // live graphs captured on this stream (and open captures)
+    std::vector<void *> retired; // replaced buffers a live graph may still use
 };
 std::unordered_map<hipStream_t, std::unique_ptr<Workspace>> g_ws;
+
+// The stream's workspace (created on first use); g_mu must be held.
+Workspace *ws_of_locked(hipStream_t s)
+{
+    auto &p = g_ws[s];
+    if (!p)
+        p.reset(new Workspace);
+    return p.get();
+}
 
 int ws_get(hipStream_t s, Slot slot, size_t bytes, void **out)
 {
     Workspace *w;
     {
         std::lock_guard<std::mutex> lk(g_mu);
-        auto &p = g_ws[s];
-        if (!p)
-            p.reset(new Workspace);
-        w = p.get();
+        w = ws_of_locked(s);
     }
     bytes = std::max<size_t>(bytes, 256);
     if (w->cap[slot] < bytes) {
         if (w->buf[slot]) {
-            HIP_TRY(hipStreamSynchronize(s));
-            HIP_TRY(hipFree(w->buf[slot]));
+            hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+            HIP_TRY(hipStreamIsCapturing(s, &cs));
+            int graphs;
+            {
+                std::lock_guard<std::mutex> lk(g_mu);
+                graphs = w->graphs;
+                if (graphs > 0)
+                    w->retired.push_back(w->buf[slot]);
+            }
+            if (graphs == 0 && cs == hipStreamCaptureStatusNone) {
+                HIP_TRY(hipStreamSynchronize(s));
+                HIP_TRY(hipFree(w->buf[slot]));
+            } // else: retired (or, under a capture the library does not track, kept)
             w->buf[slot] = nullptr;
             w->cap[slot] = 0;
         }
@@ -425,8 +453,9 @@ int run_gemv(const Weight *const *ws, int count, const float *d_x, int M, float 
     int upl = (U + lpr - 1) / lpr;
     const int rpp = 64 / lpr;
     const int nt = M <= 1 ? 1 : (M == 2 ? 2 : 4);
-    // per token: 8 x records + up to 2 meta float4 per unit
-    size_t lds = (size_t)U * 16 * 10 * nt;
+    // per token: 8 x records + up to 2 meta float4 per unit; then one flag
+    // word per token (its x needs the exact path)
+    size_t lds = (size_t)U * 16 * 10 * nt + 16;
     if (M < 1 || M > 4 || upl > 8 || lds > g_dev.max_lds || count < 1 ||
         count > REALM_GEMV_MAX_MATS)
         return REALM_BACKEND_UNSUPPORTED;
@@ -609,7 +638,11 @@ GemmTile gemm_tile(const Weight &w, size_t M, bool bf16)
 struct XPrep {
     void *xh = nullptr, *xl = nullptr, *xm = nullptr, *ts = nullptr;
     size_t Mp = 0;
+    const void *x = nullptr; // the caller's activations (read again on the exact path)
+    bool bf16 = false;
 };
+
+int fmt_code(int type) { return type == GGML_Q4_K ? 0 : type == GGML_Q6_K ? 1 : 2; }
 
 // xprep limit: the kernel holds 4 rounds of 1024 x 8 positions per thread
 constexpr size_t XPREP_MAX_KX = 32768;
@@ -634,6 +667,8 @@ int prep_x(const Weight &w, const void *d_x, bool bf16, size_t M, const GemmTile
     if (w.type == GGML_Q4_K)
         CHECK(ws_get(s, WS_XM, rows * B * 64, &p->xm));
     CHECK(ws_get(s, WS_TS, rows * 4, &p->ts));
+    p->x = d_x;
+    p->bf16 = bf16;
     int ibf = bf16 ? 1 : 0, iM = (int)M, iK = (int)w.k, iKX = (int)w.kx;
     void *args[] = {(void *)&d_x, &ibf, &p->xh, &p->xl, &p->xm, &p->ts, &iM, &iK, &iKX};
     return launch(std::string("realm_xprep_") + fmt_name(w.type) + (tile.ord ? "_o1" : ""),
@@ -670,6 +705,9 @@ int tiled_launch(const Weight *const *w, float *const *d_y, int count, const XPr
     g.xl = p.xl;
     g.xm = p.xm;
     g.tscale = (const float *)p.ts;
+    g.x = p.x;
+    g.xbf16 = p.bf16 ? 1 : 0;
+    g.fmt = fmt_code(w0.type);
     g.K = (int)w0.k;
     g.KX = (int)w0.kx;
     g.M = (int)M;
@@ -874,6 +912,9 @@ int gemm_launch(const Weight &w, const XPrep &p, bool bf16, size_t M, const Gemm
         g.xl = p.xl;
         g.xm = p.xm;
         g.tscale = (const float *)p.ts;
+        g.x = p.x;
+        g.xbf16 = p.bf16 ? 1 : 0;
+        g.fmt = fmt_code(w.type);
         g.y = d_y;
         g.N = (int)w.n;
         g.K = (int)w.k;
@@ -1078,6 +1119,17 @@ int dense_launch(const float *da, const float *db, float *dc, size_t m, size_t k
     return REALM_OK;
 }
 
+// out[0 .. n) = v on stream s.
+int fill_launch(float *out, size_t n, float v, hipStream_t s)
+{
+    if (n == 0)
+        return REALM_OK;
+    long long ln = (long long)n;
+    const unsigned wgs = (unsigned)std::min<size_t>((n + 255) / 256, (size_t)g_dev.cu_count * 8);
+    void *args[] = {&out, &ln, &v};
+    return launch("realm_fill_f32", dim3(wgs), dim3(256), 0, s, args);
+}
+
 // Dense f32 C = A @ B (or A @ B^T) with host pointers.
 int dense_host(const float *a, const float *b, float *c, size_t m, size_t k, size_t n, int bt)
 {
@@ -1177,10 +1229,8 @@ REALM_API int realm_hip_matmul_dev(const float *d_a, const float *d_b, float *d_
         return REALM_OK;
     if (m > (uint32_t)INT32_MAX || n > (uint32_t)INT32_MAX || k > (uint32_t)INT32_MAX)
         return fail(REALM_INVALID_ARGUMENT, "dimension exceeds 2^31-1");
-    if (k == 0) {
-        HIP_TRY(hipMemsetAsync(d_c, 0, (size_t)m * n * sizeof(float), s));
-        return REALM_OK;
-    }
+    if (k == 0) // C = 0 by a fill kernel: no memset node goes into a captured graph
+        return fill_launch(d_c, (size_t)m * n, 0.f, s);
     return dense_launch(d_a, d_b, d_c, m, k, n, b_transposed ? 1 : 0, s);
 }
 
@@ -2125,8 +2175,32 @@ REALM_API int realm_hip_multi_lora_matmul(uint64_t weight_handle, uint64_t set_h
 // ------------------------------------------------------------ HIP graphs
 
 namespace {
-std::unordered_map<uint64_t, hipGraphExec_t> g_graphs;
+// A live graph and the stream it was captured on (whose workspace buffers
+// it may use: see ws_get).
+struct GraphRec {
+    hipGraphExec_t exec;
+    hipStream_t stream;
+};
+std::unordered_map<uint64_t, GraphRec> g_graphs;
+
+// One graph of stream s fewer (a release, or a capture that failed): when
+// none is left, the buffers retired meanwhile are freed.
+int graph_unpin(hipStream_t s)
+{
+    std::vector<void *> drop;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        Workspace *w = ws_of_locked(s);
+        if (w->graphs > 0 && --w->graphs == 0)
+            drop.swap(w->retired);
+    }
+    if (!drop.empty())
+        HIP_TRY(hipDeviceSynchronize());
+    for (void *p : drop)
+        HIP_TRY(hipFree(p));
+    return REALM_OK;
 }
+} // namespace
 
 REALM_API int realm_hip_graph_begin(void *stream)
 {
@@ -2134,6 +2208,8 @@ REALM_API int realm_hip_graph_begin(void *stream)
         return fail(REALM_INVALID_ARGUMENT, "graph capture needs an explicit stream");
     CHECK(ensure_init());
     HIP_TRY(hipStreamBeginCapture((hipStream_t)stream, hipStreamCaptureModeThreadLocal));
+    std::lock_guard<std::mutex> lk(g_mu);
+    ws_of_locked((hipStream_t)stream)->graphs++;
     return REALM_OK;
 }
 
@@ -2141,16 +2217,23 @@ REALM_API int realm_hip_graph_end(void *stream, uint64_t *graph_handle)
 {
     if (!stream || !graph_handle)
         return fail(REALM_INVALID_ARGUMENT, "null argument");
+    const hipStream_t s = (hipStream_t)stream;
     hipGraph_t graph;
-    HIP_TRY(hipStreamEndCapture((hipStream_t)stream, &graph));
+    hipError_t e = hipStreamEndCapture(s, &graph);
+    if (e != hipSuccess) {
+        (void)graph_unpin(s);
+        return fail(hip_code(e), std::string("hipStreamEndCapture: ") + hipGetErrorString(e));
+    }
     hipGraphExec_t exec;
-    hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
     (void)hipGraphDestroy(graph);
-    if (e != hipSuccess)
+    if (e != hipSuccess) {
+        (void)graph_unpin(s);
         return fail(hip_code(e), std::string("hipGraphInstantiate: ") + hipGetErrorString(e));
+    }
     std::lock_guard<std::mutex> lk(g_mu);
     uint64_t h = g_next_handle++;
-    g_graphs[h] = exec;
+    g_graphs[h] = GraphRec{exec, s};
     *graph_handle = h;
     return REALM_OK;
 }
@@ -2163,7 +2246,7 @@ REALM_API int realm_hip_graph_launch(uint64_t graph_handle, void *stream)
         auto it = g_graphs.find(graph_handle);
         if (it == g_graphs.end())
             return fail(REALM_INVALID_ARGUMENT, "unknown graph " + std::to_string(graph_handle));
-        exec = it->second;
+        exec = it->second.exec;
     }
     hipStream_t s;
     CHECK(pick_stream(stream, &s));
@@ -2173,17 +2256,37 @@ REALM_API int realm_hip_graph_launch(uint64_t graph_handle, void *stream)
 
 REALM_API int realm_hip_graph_release(uint64_t graph_handle)
 {
-    hipGraphExec_t exec;
+    GraphRec rec;
     {
         std::lock_guard<std::mutex> lk(g_mu);
         auto it = g_graphs.find(graph_handle);
         if (it == g_graphs.end())
             return fail(REALM_INVALID_ARGUMENT, "unknown graph " + std::to_string(graph_handle));
-        exec = it->second;
+        rec = it->second;
         g_graphs.erase(it);
     }
     HIP_TRY(hipDeviceSynchronize());
-    HIP_TRY(hipGraphExecDestroy(exec));
+    HIP_TRY(hipGraphExecDestroy(rec.exec));
+    return graph_unpin(rec.stream);
+}
+
+REALM_API int realm_hip_workspace_info(void *stream, size_t *bytes, size_t *retired,
+                                       int *graphs)
+{
+    CHECK(ensure_init());
+    hipStream_t s;
+    CHECK(pick_stream(stream, &s));
+    std::lock_guard<std::mutex> lk(g_mu);
+    const Workspace *w = ws_of_locked(s);
+    size_t total = 0;
+    for (int i = 0; i < WS_N; ++i)
+        total += w->cap[i];
+    if (bytes)
+        *bytes = total;
+    if (retired)
+        *retired = w->retired.size();
+    if (graphs)
+        *graphs = w->graphs;
     return REALM_OK;
 }
 

@@ -150,3 +150,13 @@ extern "C" __global__ __launch_bounds__(256) void realm_dense_reduce(const float
         s += part[(size_t)z * n + i];
     C[i] = s;
 }
+
+// out[i] = v for i < n (a kernel node, where a memset node would otherwise
+// be recorded into a captured graph)
+extern "C" __global__ __launch_bounds__(256) void realm_fill_f32(float *__restrict__ out,
+                                                                 long long n, float v)
+{
+    const long long stride = (long long)gridDim.x * 256;
+    for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n; i += stride)
+        out[i] = v;
+}

@@ -36,7 +36,9 @@ using namespace realm;
 //                       ORD 0: xm[t][b][c][8] = (Sxh(2c), Sxh(2c+1), Sxl(2c),
 //                              Sxl(2c+1), 0, 0, 0, 0)
 //                       ORD 1: xm[t][b][h][8] = (Sxh(4h..4h+3), Sxl(4h..4h+3))
-//   tscale[t] = 2^e_t
+//   tscale[t] = 2^e_t, or NaN when the token needs the exact path (exact.h:
+//               a NaN / Inf element, or max |x| outside [EXACT_LO, EXACT_HI]);
+//               its prepared activations are then zero
 // Tokens t >= M get zeros.  Position group pg = p/8 (8 slots) is handled by
 // thread pg % 1024: it loads the 8 x of its window once, takes part in the
 // token's max, then converts them; the Q4_K sums come from the threads that
@@ -92,9 +94,10 @@ REALM_DEV void xprep(const void *__restrict__ x, int bf16, _Float16 *__restrict_
                 v[r][w] = (live && pg < ngroups && k < K) ? load_x(x, bf16, xrow + k) : 0.f;
             }
         }
+        // a non-finite element counts as +Inf in the max (fmaxf would drop a NaN)
 #pragma unroll
         for (int w = 0; w < 8; ++w)
-            amax = fmaxf(amax, fabsf(v[r][w]));
+            amax = fmaxf(amax, __builtin_isfinite(v[r][w]) ? fabsf(v[r][w]) : __builtin_inff());
     }
     // workgroup max: wave reduction (lane 63 ends with it), then LDS
     for (int off = 32; off > 0; off >>= 1)
@@ -106,15 +109,16 @@ REALM_DEV void xprep(const void *__restrict__ x, int bf16, _Float16 *__restrict_
 #pragma unroll
     for (int w = 0; w < XPREP_TH / 64; ++w)
         amax = fmaxf(amax, red[w]);
+    const bool exact = exact_needed(amax, !__builtin_isfinite(amax));
     int e = 0;
-    if (amax > 0.f && __builtin_isfinite(amax)) {
+    if (amax > 0.f && !exact) {
         int ex;
-        frexpf(amax, &ex); // amax = m * 2^ex, m in [0.5, 1)
+        frexpf(amax, &ex); // amax = m * 2^ex, m in [0.5, 1); |ex| <= 101 here
         e = ex - 10;
     }
-    const float down = ldexpf(1.f, -e);
+    const float down = exact ? 0.f : ldexpf(1.f, -e);
     if (threadIdx.x == 0)
-        tscale[t] = ldexpf(1.f, e);
+        tscale[t] = exact ? __builtin_nanf("") : ldexpf(1.f, e);
 
     const size_t orow = (size_t)t * KX;
     const int B = K >> 8;
@@ -125,7 +129,7 @@ REALM_DEV void xprep(const void *__restrict__ x, int bf16, _Float16 *__restrict_
         float sum = 0.f, shi = 0.f; // of this thread's x * down: all 8 / the upper 4
 #pragma unroll
         for (int s2 = 0; s2 < 8; ++s2) {
-            const float val = v[r][pi8(s2)] * down;
+            const float val = exact ? 0.f : v[r][pi8(s2)] * down;
             const _Float16 h = (_Float16)val;
             hv[s2] = h;
             lv[s2] = (_Float16)(val - (float)h);
@@ -541,7 +545,13 @@ REALM_DEV void gemm_body(const GemmArgs &g)
                 if (row >= N)
                     continue;
                 float sum = PACK ? acc[a][bb][v] + acc[a][bb][v + 1] : acc[a][bb][v];
-                g.y[(size_t)tok * N + row] = sum * ts[bb][v];
+                float out = sum * ts[bb][v];
+                if (__builtin_expect(__builtin_isnan(ts[bb][v]), 0)) // flagged by xprep
+                    out = exact_dot<FMT>(g.w0, g.w1, g.w2, row, g.K, g.KX,
+                                         (const uint8_t *)g.x +
+                                             (size_t)tok * g.K * (g.xbf16 ? 2 : 4),
+                                         g.xbf16, g.nan_fb, 0, 1);
+                g.y[(size_t)tok * N + row] = out;
             }
         }
 }
@@ -715,7 +725,10 @@ REALM_DEV void shrink_body(const _Float16 *__restrict__ xh, const _Float16 *__re
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
             const int tj = tc + 4 * c + v;
-            ts[v] = tscale[toks[tj < count ? tj : 0]];
+            const float t = tscale[toks[tj < count ? tj : 0]];
+            // a token on the exact path (NaN scale) gets no LoRA delta: its
+            // base row is recomputed in f32 and carries the +-Inf / NaN
+            ts[v] = __builtin_isnan(t) ? 0.f : t;
         }
 #pragma unroll
         for (int v = 0; v < 4; ++v) {

@@ -671,7 +671,13 @@ REALM_DEV void gemm_tiled(const GemmArgs &g)
                 const int row = row0 + 32 * a;
                 if (row >= mat.N)
                     continue;
-                yseg[(size_t)tok * mat.N + row] = vals[bb][v / VS][a];
+                float out = vals[bb][v / VS][a];
+                if (__builtin_expect(__builtin_isnan(ts[bb][v]), 0)) // flagged by xprep
+                    out = exact_dot<FMT>(mat.w0, mat.w1, mat.w2, row, g.K, g.KX,
+                                         (const uint8_t *)g.x +
+                                             (size_t)tok * g.K * (g.xbf16 ? 2 : 4),
+                                         g.xbf16, g.nan_fb, 0, 1);
+                yseg[(size_t)tok * mat.N + row] = out;
             }
         }
 }
@@ -730,5 +736,15 @@ extern "C" __global__ __launch_bounds__(256) void realm_gemm_tiled_reduce(GemmAr
     float sum = p[0];
     for (int c = 1; c < g.ksplit; ++c)
         sum += p[(size_t)c * TILE];
+    if (__builtin_expect(__builtin_isnan(g.tscale[tok]), 0)) { // flagged by xprep
+        const void *w0 = pick(g.seg_w0[0], g.seg_w0[1], g.seg_w0[2], g.seg_w0[3]);
+        const void *w1 = pick(g.seg_w1[0], g.seg_w1[1], g.seg_w1[2], g.seg_w1[3]);
+        const void *w2 = pick(g.seg_w2[0], g.seg_w2[1], g.seg_w2[2], g.seg_w2[3]);
+        const uint8_t *x = (const uint8_t *)g.x + (size_t)tok * g.K * (g.xbf16 ? 2 : 4);
+        // the reduce serves Q4_K and Q6_K launches: the format from the layout
+        sum = g.fmt == FMT_Q4K
+                  ? exact_dot<FMT_Q4K>(w0, w1, w2, row, g.K, g.KX, x, g.xbf16, g.nan_fb, 0, 1)
+                  : exact_dot<FMT_Q6K>(w0, w1, w2, row, g.K, g.KX, x, g.xbf16, g.nan_fb, 0, 1);
+    }
     y[(size_t)tok * N + row] = sum;
 }

@@ -24,6 +24,7 @@
 // position), laid out [position][unit], so lanes of a wave read consecutive
 // records (no bank conflicts).
 #include "common.h"
+#include "exact.h"
 #include "kernel_args.h"
 
 using namespace realm;
@@ -114,18 +115,27 @@ REALM_DEV uint32_t pack_u8(float b0, float b1, float b2, float b3)
     return __builtin_amdgcn_cvt_pk_u8_f32(b3, 3, r);
 }
 
+// A block whose values the int8 scaling cannot represent (a NaN or Inf, or
+// a max |x| outside [EXACT_LO, EXACT_HI]) sets *flag: the token's rows are
+// then recomputed on the exact f32 path (exact.h).
 template <int FMT, int TH>
-REALM_DEV void quant_round(int4 *rec, float4 *meta, const float4 (&v)[2], int U, int rd)
+REALM_DEV void quant_round(int4 *rec, float4 *meta, int *flag, const float4 (&v)[2], int U,
+                           int rd)
 {
     const int gid = rd * TH + threadIdx.x;
     const int blk = gid >> 2, part = gid & 3;
     const bool live = blk < 2 * U;
     const float xs[8] = {v[0].x, v[0].y, v[0].z, v[0].w, v[1].x, v[1].y, v[1].z, v[1].w};
     float amax = 0.f;
+    bool nonfinite = false;
 #pragma unroll
-    for (int e = 0; e < 8; ++e)
+    for (int e = 0; e < 8; ++e) {
         amax = fmaxf(amax, fabsf(xs[e]));
+        nonfinite = nonfinite || !__builtin_isfinite(xs[e]);
+    }
     amax = quad_max(amax);
+    if (live && exact_needed(amax, nonfinite))
+        *flag = 1;
     const float s = amax * (1.f / 127.f);
     const float inv = amax > 0.f ? 127.f / amax : 0.f;
     const float inv2 = 254.f * inv;
@@ -415,6 +425,8 @@ REALM_DEV void gemv(const GemvArgs &a)
     const int TS = 10 * U;
     int4 *rec = lds;
     float4 *meta = reinterpret_cast<float4 *>(lds + 8 * U);
+    // per token: set when a block of its x needs the exact path
+    int *xflag = reinterpret_cast<int *>(lds + NT * TS);
     const int M = NT == 1 ? 1 : a.m;
     // x of the lane's unit held in registers (one unit per lane, NT > 1)
     constexpr bool XREG = UPL == 1 && NT > 1;
@@ -435,6 +447,7 @@ REALM_DEV void gemv(const GemvArgs &a)
     float *const yv[4] = {a.y[0], a.y[1], a.y[2], a.y[3]};
     const float *const xp = a.x;
     const int nan_fb = a.nan_fb;
+    int xbad = 0; // bit t: token t's x needs the exact path (set after staging)
     // Every kernel argument is read here, in one batch of scalar loads ahead
     // of the first vector load (one statement, so all are live at once):
     // left alone, the compiler sinks some of these loads next to their uses,
@@ -532,6 +545,26 @@ REALM_DEV void gemv(const GemvArgs &a)
         for (int t = 0; t < NT; ++t)
             v[t] = group_total<LPR>(acc[t]);
         const int row = (gw + i * nw) * RPP + slot;
+        if (__builtin_expect(xbad != 0, 0)) {
+            // tokens flagged while staging x: the row on the exact f32 path,
+            // K split over the row's LPR lanes (a padding row reads the last
+            // row and is not stored)
+            const int rc = min(row, rows - 1);
+            int m = 0, lr = rc;
+            if constexpr (NM > 1) {
+                m = (rc >= rs1 ? 1 : 0) + (rc >= rs2 ? 1 : 0) + (rc >= rs3 ? 1 : 0);
+                lr = rc - (m == 0 ? 0 : (m == 1 ? rs1 : (m == 2 ? rs2 : rs3)));
+            }
+            const void *e0 = m == 0 ? w0[0] : (m == 1 ? w0[1] : (m == 2 ? w0[2] : w0[3]));
+            const void *e1 = m == 0 ? w1[0] : (m == 1 ? w1[1] : (m == 2 ? w1[2] : w1[3]));
+            const void *e2 = m == 0 ? w2[0] : (m == 1 ? w2[1] : (m == 2 ? w2[2] : w2[3]));
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+                if ((xbad >> t) & 1)
+                    v[t] = group_total<LPR>(exact_dot<FMT>(e0, e1, e2, lr, K, KX,
+                                                           xp + (size_t)min(t, M - 1) * K, 0,
+                                                           nan_fb, l, LPR));
+        }
         if (l == LPR - 1 && row < rows) {
             float *y = yv[0];
             int lr = row, nrow = rows;
@@ -563,12 +596,17 @@ REALM_DEV void gemv(const GemvArgs &a)
 #pragma unroll
         for (int rd = 0; rd < XH; ++rd)
             x_round<TH>(xp + (size_t)min(t, M - 1) * K, K, U, rd, xv[t][rd]);
+    if (threadIdx.x < NT)
+        xflag[threadIdx.x] = 0;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     // Every wave of the workgroup issues its x loads before any wave issues
     // a weight load: the CU's vector memory path returns data in request
     // order, so x requests queued behind other waves' weight requests would
     // hold up the quantization (and the barrier) by a full weight fetch.
+    // (The barrier also orders the flag reset above before any flag write.)
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
     __builtin_amdgcn_sched_barrier(0);
     W w[D][UPL];
     load_pass(w[0], 0);
@@ -577,15 +615,21 @@ REALM_DEV void gemv(const GemvArgs &a)
 #pragma unroll
         for (int rd = 0; rd < XH; ++rd)
             if (rd < rounds)
-                quant_round<FMT, TH>(rec + t * TS, meta + t * TS, xv[t][rd], U, rd);
+                quant_round<FMT, TH>(rec + t * TS, meta + t * TS, xflag + t, xv[t][rd], U, rd);
 #pragma unroll
     for (int t = 0; t < NT; ++t)
         for (int rd = XH; rd < rounds; ++rd) {
             float4 v[2];
             x_round<TH>(xp + (size_t)min(t, M - 1) * K, K, U, rd, v);
-            quant_round<FMT, TH>(rec + t * TS, meta + t * TS, v, U, rd);
+            quant_round<FMT, TH>(rec + t * TS, meta + t * TS, xflag + t, v, U, rd);
         }
     lds_barrier();
+    // bit t: token t takes the exact path (wave-uniform)
+    int xbad_v = 0;
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+        xbad_v |= (xflag[t] != 0 ? 1 : 0) << t;
+    xbad = __builtin_amdgcn_readfirstlane(xbad_v);
     // One unit per lane, several tokens: the lane's unit is the same in
     // every pass, so its records and metadata of every token move to
     // registers once (re-reading them from LDS each pass would take NT x

@@ -50,7 +50,10 @@ struct GemmArgs {
     const void *xh;     // f16 activations, hi part [Mp][KX]
     const void *xl;     // f16 lo part (null for bf16 input)
     const void *xm;     // Q4_K min fragments [Mp][K/256][4][8] f16
-    const float *tscale;
+    const float *tscale; // per token 2^e; NaN: the token takes the exact path (exact.h)
+    const void *x;      // the activations as the caller passed them [M][K] (exact path)
+    int32_t xbf16;      // x is bf16 (else f32)
+    int32_t fmt;        // 0 Q4_K, 1 Q6_K, 2 Q8_0 (the K-split reduce's exact path)
     float *y;           // [M][N]
     int32_t N, K, KX, M;
     int32_t nan_fb;

@@ -220,9 +220,11 @@ extern "C" __global__ __launch_bounds__(ATT_TH) void realm_attention(
     mx = red[0];
     for (int w = 1; w < ATT_NW; ++w)
         mx = fmaxf(mx, red[w]);
+    // a non-finite score gets weight 0 (standard.rs:119-126); the max
+    // ignores NaN and may be +Inf, which leaves every finite weight 0
     float sum = 0.f;
     for (int j = threadIdx.x; j < vis; j += ATT_TH) {
-        const float e = expf(sc[j] - mx);
+        const float e = __builtin_isfinite(sc[j]) ? expf(sc[j] - mx) : 0.f;
         sc[j] = e;
         sum += e;
     }
@@ -331,9 +333,9 @@ extern "C" __global__ __launch_bounds__(256) void realm_attention_split(
         red[threadIdx.x >> 6] = mx;
     __syncthreads();
     mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    float sum = 0.f;
+    float sum = 0.f; // non-finite scores: weight 0, as in realm_attention
     for (int j = threadIdx.x; j < n; j += 256) {
-        const float e = expf(sc[j] - mx);
+        const float e = __builtin_isfinite(sc[j]) ? expf(sc[j] - mx) : 0.f;
         sc[j] = e;
         sum += e;
     }

@@ -4,6 +4,7 @@
 #pragma once
 
 #include "common.h"
+#include "exact.h"
 
 #define FMT_Q4K 0
 #define FMT_Q6K 1
