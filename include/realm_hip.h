@@ -208,6 +208,20 @@ int realm_hip_weights_matmul(uint64_t handle, const float *input, size_t batch,
 int realm_hip_weights_matmul_dev(uint64_t handle, const float *d_input, size_t batch,
                                  float *d_out, void *stream);
 
+/* No counterpart in the reference: for callers that cannot allocate (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  realm_hip_weights_matmul_dev's product, but every scratch
+ * buffer (activation staging, K-split partials) is cut from a fixed 32 MiB
+ * device array the library holds per GPU until the process ends, so the call
+ * makes no hipMalloc, hipFree or other allocating call.  Needs a prior
+ * realm_hip_init and an explicit stream.  A product whose staging does not
+ * fit (batch x K beyond about 1,900 x 4096 for f32 input) returns
+ * REALM_INVALID_ARGUMENT; K splits are reduced until their partials fit.
+ * Every call on a GPU shares that GPU's array: calls that overlap on one GPU
+ * (several streams or threads at once) race. */
+int realm_hip_weights_matmul_noalloc_dev(uint64_t handle, const float *d_input, size_t batch,
+                                         float *d_out, void *stream);
+
 /* Grouped form for 1..4 resident weights of one format and K that share the
  * input, e.g. the q/k/v projections (or gate/up) that realm_forward_layer
  * issues back to back on the same normed hidden state

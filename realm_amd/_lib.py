@@ -42,6 +42,8 @@ SIGNATURES = {
                                        POINTER(c_size_t), POINTER(c_size_t)]),
     "realm_hip_weights_matmul": (c_int, [c_uint64, c_void_p, c_size_t, c_void_p]),
     "realm_hip_weights_matmul_dev": (c_int, [c_uint64, c_void_p, c_size_t, c_void_p, c_void_p]),
+    "realm_hip_weights_matmul_noalloc_dev": (c_int, [c_uint64, c_void_p, c_size_t, c_void_p,
+                                                     c_void_p]),
     "realm_hip_weights_matmul_group_dev": (c_int, [POINTER(c_uint64), c_size_t, c_void_p,
                                                    c_size_t, POINTER(c_void_p), c_void_p]),
     "realm_hip_weights_matmul_bf16_dev": (c_int, [c_uint64, c_void_p, c_size_t, c_void_p,

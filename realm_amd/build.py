@@ -1,7 +1,9 @@
 """Build the gfx950 code object and the C-ABI host library, in-tree.
 
     realm_amd/lib/realm_kernels.hsaco   hipcc --genco --offload-arch=gfx950
-    realm_amd/lib/librealm_hip.so       g++ (realm_hip.cpp, gguf.cpp), embeds the code
+    realm_amd/lib/librealm_hip.so       g++ (realm_hip.cpp, gguf.cpp) plus the hipcc
+                                        object of noalloc.hip (the no-allocation
+                                        entry point's device array), embeds the code
                                         objects, links libamdhip64
 
 Run as ``python -m realm_amd.build`` (or through ``__graft_entry__.build()``).
@@ -47,7 +49,8 @@ HIP_FLAGS = [
 
 def _run(cmd: list[str]) -> None:
     proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
-    out = "\n".join(l for l in proc.stdout.splitlines() if "unknown target feature" not in l)
+    out = "\n".join(l for l in proc.stdout.splitlines()
+                    if "unknown target feature" not in l and "packed-fp32-ops" not in l)
     if proc.returncode != 0:
         raise RuntimeError(f"command failed ({proc.returncode}): {' '.join(cmd)}\n{out}")
     if out.strip():
@@ -72,18 +75,33 @@ def build_all_hsaco(out_dir: str = LIB_DIR, defines: tuple = ()) -> list:
         return list(ex.map(lambda j: build_hsaco(*j), jobs))
 
 
+def build_noalloc_object(out_dir: str = LIB_DIR) -> str:
+    """hipcc object (host code + gfx950 device code) holding the fixed
+    scratch array of the no-allocation entry point and its address lookup."""
+    os.makedirs(out_dir, exist_ok=True)
+    out = os.path.join(out_dir, "noalloc.o")
+    _run([os.path.join(ROCM, "bin", "hipcc"), "-c", "-fPIC", "-fvisibility=hidden",
+          "--offload-arch=gfx950", "-O2",
+          "-std=c++17", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+          "-I", HDIR, os.path.join(HDIR, "noalloc.hip"), "-o", out + ".tmp"])
+    os.replace(out + ".tmp", out)
+    return out
+
+
 def build_host(out: str = LIBSO, hsacos: list | None = None) -> str:
     if hsacos is None:
         hsacos = [os.path.join(LIB_DIR, name + ".hsaco") for name, _, _ in HSACO_UNITS]
     os.makedirs(os.path.dirname(out), exist_ok=True)
     tmp = out + ".tmp"
     embeds = [f"-DREALM_HSACO_FILE{i}={p}" for i, p in enumerate(hsacos)]
+    noalloc = build_noalloc_object(os.path.dirname(out))
     _run(["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-fvisibility=hidden",
           "-Wall", "-Wextra", "-Wno-unused-parameter",
           "-D__HIP_PLATFORM_AMD__", f"-DREALM_HSACO_COUNT={len(hsacos)}", *embeds,
           "-I", os.path.join(ROCM, "include"), "-I", os.path.join(REPO, "include"),
-          "-I", KDIR,
-          os.path.join(HDIR, "realm_hip.cpp"), os.path.join(HDIR, "gguf.cpp"), "-o", tmp,
+          "-I", KDIR, "-I", HDIR,
+          os.path.join(HDIR, "realm_hip.cpp"), os.path.join(HDIR, "gguf.cpp"), noalloc,
+          "-o", tmp,
           "-L", os.path.join(ROCM, "lib"), "-Wl,-rpath," + os.path.join(ROCM, "lib"),
           "-lamdhip64", "-lpthread"])
     os.replace(tmp, out)

@@ -23,6 +23,7 @@
 #include <vector>
 
 #include "kernel_args.h"
+#include "noalloc.h"
 #include "realm_hip.h"
 
 #define REALM_STR2(x) #x
@@ -124,6 +125,9 @@ struct Device {
     int id = 0;
     int cu_count = 256;
     size_t max_lds = 65536;
+    // this device's copy of the no-allocation entry point's scratch array
+    // (noalloc.hip), resolved once at init with the device current
+    void *noalloc_scratch = nullptr;
     hipModule_t modules[REALM_HSACO_COUNT] = {};
     std::unordered_map<std::string, hipFunction_t> fns;
 };
@@ -155,6 +159,10 @@ int init_locked(int device)
     g_dev.max_lds = prop.sharedMemPerBlock;
     for (int i = 0; i < REALM_HSACO_COUNT; ++i)
         HIP_TRY(hipModuleLoadData(&g_dev.modules[i], realm_hsacos[i]));
+    if (int e = realm_noalloc_scratch_address(&g_dev.noalloc_scratch))
+        return fail(REALM_GENERIC_FAILURE,
+                    std::string("hipGetSymbolAddress of the no-allocation scratch: ") +
+                        hipGetErrorString((hipError_t)e));
     g_dev.id = device;
     g_dev.ready = true;
     return REALM_OK;
@@ -267,6 +275,17 @@ struct Workspace {
 };
 std::unordered_map<hipStream_t, std::unique_ptr<Workspace>> g_ws;
 
+// During a call of the no-allocation entry point, every scratch request of
+// the calling thread is cut from the device's fixed scratch array (in
+// order, 256-byte aligned) instead of the stream's workspace; a request
+// that does not fit fails instead of allocating.
+struct FixedScratch {
+    uint8_t *base;
+    size_t cap, used = 0;
+    size_t room() const { return used >= cap ? 0 : cap - align256(used); }
+};
+thread_local FixedScratch *t_fixed = nullptr;
+
 // The stream's workspace (created on first use); g_mu must be held.
 Workspace *ws_of_locked(hipStream_t s)
 {
@@ -278,6 +297,16 @@ Workspace *ws_of_locked(hipStream_t s)
 
 int ws_get(hipStream_t s, Slot slot, size_t bytes, void **out)
 {
+    if (FixedScratch *f = t_fixed) {
+        const size_t off = align256(f->used);
+        if (off > f->cap || bytes > f->cap - off)
+            return fail(REALM_INVALID_ARGUMENT,
+                        "the product needs more scratch than the no-allocation entry point's " +
+                            std::to_string(f->cap >> 20) + " MiB");
+        *out = f->base + off;
+        f->used = off + bytes;
+        return REALM_OK;
+    }
     Workspace *w;
     {
         std::lock_guard<std::mutex> lk(g_mu);
@@ -732,6 +761,11 @@ int tiled_launch(const Weight *const *w, float *const *d_y, int count, const XPr
     g.rtiles = (int)rt;
     const int nblk = (int)(w0.kx / 256);
     g.ksplit = tile.ks < nblk ? tile.ks : nblk;
+    // in the fixed scratch region, fewer K splits when the parts would not fit
+    while (t_fixed && g.ksplit > 1 &&
+           rt * TT * g.ksplit * tile.rows_per_wg * tile.toks_per_wg * sizeof(float) >
+               t_fixed->room())
+        g.ksplit /= 2;
     if (g.ksplit > 1) {
         void *part = nullptr;
         CHECK(ws_get(s, WS_PART,
@@ -1102,6 +1136,8 @@ int dense_launch(const float *da, const float *db, float *dc, size_t m, size_t k
     if (const char *env = getenv("REALM_DENSE_KS")) // tuning override
         ks = std::max(1, std::min(64, atoi(env)));
     ks = (int)std::min<size_t>((size_t)ks, k); // every split owns at least one k
+    while (t_fixed && ks > 1 && (size_t)ks * m * n * sizeof(float) > t_fixed->room())
+        ks /= 2; // fixed scratch region: fewer K splits when the parts would not fit
     void *part = nullptr;
     if (ks > 1)
         CHECK(ws_get(s, WS_PART, (size_t)ks * m * n * sizeof(float), &part));
@@ -1838,6 +1874,35 @@ REALM_API int realm_hip_weights_matmul_dev(uint64_t handle, const float *d_input
     hipStream_t s;
     CHECK(pick_stream(stream, &s));
     return run_matmul(w, d_input, false, batch, d_out, s, nullptr);
+}
+
+// realm_hip_weights_matmul_dev with every scratch buffer cut from the
+// device's fixed scratch array: no hipMalloc, hipFree or other allocating
+// call.  The library must already be initialised on the device and the
+// stream given; calls that overlap on one GPU share the array and race.
+REALM_API int realm_hip_weights_matmul_noalloc_dev(uint64_t handle, const float *d_input,
+                                                   size_t batch, float *d_out, void *stream)
+{
+    if (!stream)
+        return fail(REALM_INVALID_ARGUMENT, "noalloc: needs an explicit stream");
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        if (!g_dev.ready || !g_dev.noalloc_scratch)
+            return fail(REALM_INVALID_ARGUMENT,
+                        "noalloc: call realm_hip_init first (this entry point allocates nothing)");
+    }
+    Weight w;
+    CHECK(get_weight(handle, &w));
+    if (batch > (size_t)INT32_MAX)
+        return fail(REALM_INVALID_ARGUMENT, "batch exceeds 2^31-1");
+    if (batch && (!d_input || !d_out))
+        return fail(REALM_INVALID_ARGUMENT, "noalloc: null pointer argument");
+    HIP_TRY(hipSetDevice(g_dev.id));
+    FixedScratch fixed{(uint8_t *)g_dev.noalloc_scratch, REALM_NOALLOC_SCRATCH_BYTES};
+    t_fixed = &fixed;
+    const int rc = run_matmul(w, d_input, false, batch, d_out, (hipStream_t)stream, nullptr);
+    t_fixed = nullptr;
+    return rc;
 }
 
 REALM_API int realm_hip_weights_matmul_group_dev(const uint64_t *handles, size_t count,
