@@ -162,6 +162,51 @@ def decode_roofline(be, model: Model7B, stream: int, reps: int) -> dict:
             "shape": "grouped W_gate + W_up, 2 x (11008 x 4096) Q4_K, batch 1"}
 
 
+def stream_ceiling(be, stream: int, reps: int) -> dict:
+    """The practical HBM read ceiling, from the library's plain streaming
+    kernel (realm_hip_checksum_dev: 16-byte loads, four per lane in flight,
+    nothing else) over a separate 4 GB region:
+      chain_128: the decode step's launch structure -- 32 layers x the four
+        launch groups' byte counts, each launch a checksum of its own slice,
+        replayed from one graph (the ceiling for a stream-ordered step);
+      gate_up_size: one launch of the roofline kernel's size (the grouped
+        gate/up bytes), 32 distinct slices per graph;
+      single_4gb: one launch over the whole region."""
+    sizes = [Model7B.group_bytes(gi, 1) for gi in range(len(Model7B.GROUPS))]
+    sizes = [(s + 255) // 256 * 256 for s in sizes]
+    total = LAYERS * sum(sizes)
+    buf = be.alloc(total)
+    parts = be.alloc(4096 * 4)
+    cu = 256
+    out = {}
+
+    def run(name, fn, nbytes):
+        gr = capture(be, stream, fn)
+        time_graph(be, gr, stream, 2)
+        ms = time_graph(be, gr, stream, reps)
+        be.graph_release(gr)
+        out[name] = {"us": round(ms * 1e3, 2), "gb_per_s": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+
+    def chain():
+        off = 0
+        for _ in range(LAYERS):
+            for s in sizes:
+                be.checksum_dev(buf.ptr + off, s, parts.ptr, cu, stream=stream)
+                off += s
+    run("chain_128", chain, total)
+
+    def gate_up():
+        for l in range(LAYERS):
+            be.checksum_dev(buf.ptr + l * sizes[2], sizes[2], parts.ptr, cu, stream=stream)
+    run("gate_up_size", gate_up, LAYERS * sizes[2])
+    out["gate_up_size"]["us"] = round(out["gate_up_size"]["us"] / LAYERS, 3)
+    run("single_4gb", lambda: be.checksum_dev(buf.ptr, total, parts.ptr, cu, stream=stream), total)
+    out["kernel"] = "realm_checksum (1024 threads x 4 x 16 B in flight, one workgroup per CU)"
+    buf.close()
+    parts.close()
+    return out
+
+
 def full_layers(be, model: Model7B, stream: int, reps: int, context: int = 512) -> dict:
     """The whole decoder layer on the device (realm_hip_forward_layers_dev:
     norm, Q/K/V, RoPE, KV append, attention, Wo, residual + norm, gate/up,
@@ -564,6 +609,8 @@ def main() -> int:
                                "gb_per_s": round(value, 1)}}}
     roof = decode_roofline(be, model, stream, max(5, args.steps))
     log(f"roofline: {roof['achieved']} GB/s ({roof['frac'] * 100:.1f}% of peak)")
+    extra["stream_ceiling"] = stream_ceiling(be, stream, max(5, args.steps))
+    log(f"stream ceiling: {extra['stream_ceiling']}")
     if args.extra_only in ("batched", "layer"):
         args.skip_extra = False
     if args.extra_only == "layer":

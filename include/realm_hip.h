@@ -468,6 +468,18 @@ int realm_hip_graph_release(uint64_t graph_handle);
  * memory accounting. */
 int realm_hip_workspace_info(void *stream, size_t *bytes, size_t *retired, int *graphs);
 
+/* ------------------------------------------------------------ checksum */
+
+/* XOR of the little-endian 32-bit words of a device buffer (a trailing
+ * partial word zero-padded): an integrity check of uploaded data, read once
+ * at the HBM streaming rate.  No counterpart in the reference.  The _dev
+ * form launches n_partials (1..4096) workgroups on `stream`, each folding a
+ * contiguous share into d_partials[i]; the checksum is the XOR of the
+ * partials.  The plain form returns it, synchronously. */
+int realm_hip_checksum_dev(const void *d_buf, size_t nbytes, uint32_t *d_partials,
+                           size_t n_partials, void *stream);
+int realm_hip_checksum(const void *d_buf, size_t nbytes, uint32_t *checksum);
+
 /* ----------------------------------------- device memory and timing */
 
 /* Plumbing for callers without another GPU runtime (tests, bench): device

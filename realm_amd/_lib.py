@@ -66,6 +66,8 @@ SIGNATURES = {
     "realm_hip_graph_release": (c_int, [c_uint64]),
     "realm_hip_workspace_info": (c_int, [c_void_p, POINTER(c_size_t), POINTER(c_size_t),
                                          POINTER(c_int)]),
+    "realm_hip_checksum_dev": (c_int, [c_void_p, c_size_t, c_void_p, c_size_t, c_void_p]),
+    "realm_hip_checksum": (c_int, [c_void_p, c_size_t, POINTER(c_uint32)]),
     "realm_hip_malloc": (c_int, [POINTER(c_void_p), c_size_t]),
     "realm_hip_free": (c_int, [c_void_p]),
     "realm_hip_memcpy_htod": (c_int, [c_void_p, c_void_p, c_size_t]),

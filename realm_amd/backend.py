@@ -319,6 +319,19 @@ class HipGpuBackend:
     def graph_release(self, graph: int) -> None:
         self._check(self.lib.realm_hip_graph_release(graph))
 
+    def checksum(self, buf: "DeviceBuffer", nbytes: int | None = None) -> int:
+        """XOR of the buffer's little-endian 32-bit words (tail zero-padded)."""
+        out = ctypes.c_uint32()
+        self._check(self.lib.realm_hip_checksum(c_void_p(buf.ptr),
+                                                buf.nbytes if nbytes is None else nbytes,
+                                                ctypes.byref(out)))
+        return out.value
+
+    def checksum_dev(self, d_buf: int, nbytes: int, d_partials: int, n_partials: int,
+                     stream=None) -> None:
+        self._check(self.lib.realm_hip_checksum_dev(c_void_p(d_buf), nbytes, c_void_p(d_partials),
+                                                    n_partials, c_void_p(stream or 0)))
+
     def workspace_info(self, stream=None) -> tuple:
         """(bytes held, replaced buffers kept for live graphs, live graphs) of
         a stream's scratch buffers."""

@@ -549,8 +549,11 @@ int run_gemv(const Weight *const *ws, int count, const float *d_x, int M, float 
         const long t8 = (npass + cu * 8 - 1) / (cu * 8);
         d = (int)std::min<long>(std::max<long>(t8, 1), 3);
     } else if (upl == 1) {
+        // one pass in flight while a wave has at most 3 (7B Q/K/V 7.76 us
+        // against 8.05 us at depth 3), two beyond (gate/up: 11.46 us at
+        // depth 2, 11.83 at 1, 11.93 at 3)
         const long t1 = (npass + cu * 16 - 1) / (cu * 16); // passes per wave
-        d = t1 <= 3 ? (int)std::max<long>(t1, 1) : 2;
+        d = t1 <= 3 ? 1 : 2;
     } else if ((upl == 2 || upl == 3) && npass >= 2 * cu * 8 && nt == 1) {
         d = 2; // (multi-token: one pass in flight measured faster)
     }
@@ -2352,6 +2355,44 @@ REALM_API int realm_hip_workspace_info(void *stream, size_t *bytes, size_t *reti
         *retired = w->retired.size();
     if (graphs)
         *graphs = w->graphs;
+    return REALM_OK;
+}
+
+// ------------------------------------------------------------- checksum
+
+REALM_API int realm_hip_checksum_dev(const void *d_buf, size_t nbytes, uint32_t *d_partials,
+                                     size_t n_partials, void *stream)
+{
+    if (n_partials == 0 || n_partials > 4096 || !d_partials || (nbytes && !d_buf))
+        return fail(REALM_INVALID_ARGUMENT, "checksum: 1..4096 partials and non-null pointers");
+    if (nbytes > ((size_t)1 << 62))
+        return fail(REALM_INVALID_ARGUMENT, "checksum: buffer too large");
+    CHECK(ensure_init());
+    hipStream_t s;
+    CHECK(pick_stream(stream, &s));
+    long long n = (long long)nbytes;
+    void *args[] = {(void *)&d_buf, &n, &d_partials};
+    return launch("realm_checksum", dim3((unsigned)n_partials), dim3(1024), 0, s, args);
+}
+
+REALM_API int realm_hip_checksum(const void *d_buf, size_t nbytes, uint32_t *checksum)
+{
+    if (!checksum)
+        return fail(REALM_INVALID_ARGUMENT, "checksum: null output");
+    CHECK(ensure_init());
+    hipStream_t s;
+    CHECK(thread_stream(&s));
+    const size_t np = (size_t)g_dev.cu_count;
+    void *part;
+    CHECK(ws_get(s, WS_IDS, np * 4, &part));
+    CHECK(realm_hip_checksum_dev(d_buf, nbytes, (uint32_t *)part, np, s));
+    std::vector<uint32_t> h(np);
+    HIP_TRY(hipMemcpyAsync(h.data(), part, np * 4, hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipStreamSynchronize(s));
+    uint32_t r = 0;
+    for (uint32_t v : h)
+        r ^= v;
+    *checksum = r;
     return REALM_OK;
 }
 

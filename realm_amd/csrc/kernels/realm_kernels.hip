@@ -6,3 +6,4 @@
 #include "gemm.hip"
 #include "dense.hip"
 #include "layer_ops.hip"
+#include "stream.hip"

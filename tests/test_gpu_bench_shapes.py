@@ -43,7 +43,7 @@ def _check(oracle, t, blocks, x, got, n, k, rows=None, tag=""):
 # W_down, batch 1, LLaMA-7B shapes; the kernel names are the variants the
 # host picks on a 256-CU MI355X (the roofline kernel is the gate/up one).
 BENCH_LAUNCHES = [
-    ("qkv", GGML_Q4_K, (4096, 4096, 4096), 4096, "realm_gemv_q4k_l64_u1_d3_m4"),
+    ("qkv", GGML_Q4_K, (4096, 4096, 4096), 4096, "realm_gemv_q4k_l64_u1_d1_m4"),
     ("wo", GGML_Q4_K, (4096,), 4096, "realm_gemv_q4k_l64_u1_d1_m1"),
     ("gate_up", GGML_Q4_K, (11008, 11008), 4096, "realm_gemv_q4k_l64_u1_d2_m4"),
     ("w_down", GGML_Q6_K, (4096,), 11008, "realm_gemv_q6k_l64_u3_d2_m1"),
@@ -192,6 +192,30 @@ def test_config4_lora_qkvo(backend, oracle):
         derr = rel_l2(y[:, rows] - base, ref - base)
         print(f"config4 lora {name} rel_l2={err:.3e} delta rel_l2={derr:.3e}")
         assert err < REL_TOL and derr < 1e-2, name
+
+
+def test_checksum(backend):
+    """realm_hip_checksum: XOR of the little-endian words of a device
+    buffer, a trailing partial word zero-padded (numpy restatement), for
+    sizes around the 16-byte chunking, and through the _dev form's
+    partials."""
+    g = np.random.default_rng(77)
+    for nbytes in (1, 15, 16, 17, 4096, 1_000_003, 50_000_000):
+        host = g.integers(0, 256, nbytes, dtype=np.uint8)
+        padded = np.zeros((nbytes + 3) // 4 * 4, np.uint8)
+        padded[:nbytes] = host
+        want = int(np.bitwise_xor.reduce(padded.view("<u4"))) if padded.size else 0
+        d = backend.alloc(nbytes).upload(host)
+        try:
+            assert backend.checksum(d) == want, nbytes
+            parts = backend.alloc(256 * 4)
+            backend.checksum_dev(d.ptr, nbytes, parts.ptr, 256)
+            backend.synchronize()
+            got = int(np.bitwise_xor.reduce(parts.download(np.uint32, 256)))
+            parts.close()
+            assert got == want, nbytes
+        finally:
+            d.close()
 
 
 # ---------------------------------------- graphs and scratch buffers
