@@ -55,8 +55,12 @@ typedef enum realm_status {
 #define REALM_GGML_Q5_1 7
 #define REALM_GGML_Q8_0 8
 #define REALM_GGML_Q8_1 9
+#define REALM_GGML_Q2_K 10
+#define REALM_GGML_Q3_K 11
 #define REALM_GGML_Q4_K 12
+#define REALM_GGML_Q5_K 13
 #define REALM_GGML_Q6_K 14
+#define REALM_GGML_Q8_K 15
 
 /* Adapter storage dtypes for LoRA A/B. */
 #define REALM_DTYPE_F32 0
@@ -144,6 +148,30 @@ int realm_hip_fused_dequant_matmul_q51(const void *blocks, size_t n_blocks,
                                        const float *input, size_t input_len,
                                        size_t batch_size, size_t n, size_t k, float *out);
 int realm_hip_fused_dequant_matmul_q81(const void *blocks, size_t n_blocks,
+                                       const float *input, size_t input_len,
+                                       size_t batch_size, size_t n, size_t k, float *out);
+
+/* GpuBackendTrait::fused_dequant_matmul_q5k / _q8k / _q2k / _q3k
+ * (gpu_backend_trait.rs:31-79) on the reference's own 256-element layouts
+ * (crates/realm-core/src/quant.rs:71-95, 200-222: the #[repr(C)] sizes Q5_K
+ * 178 B, Q8_K 292 B, Q2_K 116 B, Q3_K 196 B, which are not ggml's), as
+ * CandleGpuBackend computes them (candle_backend.rs:507-571, 639-836):
+ * k % 256 == 0 and n_blocks == n*k/256 (else REALM_INVALID_ARGUMENT), an
+ * input of another length fails as the reference's tensor creation does
+ * (REALM_GENERIC_FAILURE); the blocks are dequantized bit-exactly on the
+ * device (quant.rs:453-638, including Q5_K's zero upper half), then
+ * y = x W^T on the f32 MFMA GEMM.  Registered as resident weights they stay
+ * dequantized (f32), like the 32-element formats. */
+int realm_hip_fused_dequant_matmul_q5k(const void *blocks, size_t n_blocks,
+                                       const float *input, size_t input_len,
+                                       size_t batch_size, size_t n, size_t k, float *out);
+int realm_hip_fused_dequant_matmul_q8k(const void *blocks, size_t n_blocks,
+                                       const float *input, size_t input_len,
+                                       size_t batch_size, size_t n, size_t k, float *out);
+int realm_hip_fused_dequant_matmul_q2k(const void *blocks, size_t n_blocks,
+                                       const float *input, size_t input_len,
+                                       size_t batch_size, size_t n, size_t k, float *out);
+int realm_hip_fused_dequant_matmul_q3k(const void *blocks, size_t n_blocks,
                                        const float *input, size_t input_len,
                                        size_t batch_size, size_t n, size_t k, float *out);
 

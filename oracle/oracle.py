@@ -19,10 +19,14 @@ LIB_PATH = os.path.join(HERE, "build", "librealm_oracle.so")
 
 GGML_Q8_0, GGML_Q4_K, GGML_Q6_K = 8, 12, 14
 GGML_Q4_0, GGML_Q4_1, GGML_Q5_0, GGML_Q5_1, GGML_Q8_1 = 2, 3, 6, 7, 9
-# bytes per block and elements per block of every format restated here
+GGML_Q2_K, GGML_Q3_K, GGML_Q5_K, GGML_Q8_K = 10, 11, 13, 15
+# bytes per block and elements per block of every format restated here (the
+# reference's own #[repr(C)] sizes for Q2_K/Q3_K/Q5_K/Q8_K)
 BLOCK_BYTES = {GGML_Q4_K: 144, GGML_Q6_K: 210, GGML_Q8_0: 34, GGML_Q4_0: 18, GGML_Q4_1: 20,
-               GGML_Q5_0: 22, GGML_Q5_1: 24, GGML_Q8_1: 36}
-BLOCK_ELEMS = {t: (256 if t in (GGML_Q4_K, GGML_Q6_K) else 32) for t in BLOCK_BYTES}
+               GGML_Q5_0: 22, GGML_Q5_1: 24, GGML_Q8_1: 36, GGML_Q2_K: 116, GGML_Q3_K: 196,
+               GGML_Q5_K: 178, GGML_Q8_K: 292}
+BLOCK_ELEMS = {t: (256 if t in (GGML_Q4_K, GGML_Q6_K, GGML_Q2_K, GGML_Q3_K, GGML_Q5_K,
+                                GGML_Q8_K) else 32) for t in BLOCK_BYTES}
 OK, INVALID_ARGUMENT, MODEL_PARSE_ERROR, PANIC = 0, 3, 4, -1
 
 _lib = None

@@ -187,6 +187,81 @@ int ro_block32_bytes(int type)
 
 static uint16_t rd16(const uint8_t *p) { return (uint16_t)(p[0] | (p[1] << 8)); }
 
+/* The reference's own 256-element Q2_K, Q3_K, Q5_K and Q8_K blocks
+ * (crates/realm-core/src/quant.rs:71-95, 200-222; #[repr(C)] sizes, not
+ * ggml's), dequantized as quant.rs:453-638 does:
+ *   Q2_K (116 B: d, dmin, scales[16], qh[32], qs[64]): element i of group
+ *        l = i/16 has q = ((qs[i/4] >> 2(i%4)) & 3 | ((qh[i/8] >> (i%8)) & 1)
+ *        << 2) - 2 and scale nibble l%2 of scales[l/2]; y = d sc q + dmin
+ *   Q3_K (196 B: d, dmin, scales[32], qh[32], qs[128]): group l = i/8, scale
+ *        (scales[l/4] >> 2(l%4)) & 63, q = (2 qs bits | qh bit << 2) - 4 with
+ *        the Q2_K indexing; y = d sc q + dmin
+ *   Q5_K (178 B: ql[128], qh[32], scales[16] i8, d): only elements 0..127
+ *        are written (ql has 128 bytes; the reference's loop stops there and
+ *        leaves the rest of its zeroed output); element i = 16 l + k has
+ *        q = int8(ql[i] | ((qh[2l + k/8] >> 4((k%8)/4)) & 15) << 4),
+ *        y = d scales[l] q
+ *   Q8_K (292 B: quants[256] i8, scales[32], d, dmin): group l = i/8,
+ *        scale nibble l%2 of scales[l/2]; y = d sc q + dmin
+ * Each product and sum rounds to f32 on its own, left to right. */
+int ro_kquant_bytes(int type)
+{
+    switch (type) {
+    case RO_GGML_Q2_K: return 116;
+    case RO_GGML_Q3_K: return 196;
+    case RO_GGML_Q5_K: return 178;
+    case RO_GGML_Q8_K: return 292;
+    default: return 0;
+    }
+}
+
+static void dequantize_kquant(int type, const uint8_t *b, float *y)
+{
+    volatile float t; /* keeps each rounding step separate */
+    if (type == RO_GGML_Q5_K) {
+        const uint8_t *ql = b, *qh = b + 128;
+        const int8_t *scales = (const int8_t *)(b + 160);
+        const float d = ro_f16_to_f32(rd16(b + 176));
+        for (int i = 0; i < 256; ++i)
+            y[i] = 0.0f;
+        for (int l = 0; l < 8; ++l) /* l >= 8: ql index past 127, loop stops */
+            for (int k = 0; k < 16; ++k) {
+                const int i = 16 * l + k;
+                const int qhv = (qh[2 * l + k / 8] >> (4 * ((k % 8) / 4))) & 0xF;
+                const int8_t q = (int8_t)(uint8_t)(ql[i] | ((qhv << 4) & 0xFF));
+                t = d * (float)scales[l];
+                y[i] = t * (float)q;
+            }
+        return;
+    }
+    const int off = type == RO_GGML_Q8_K ? 288 : 0; /* d, dmin */
+    const float d = ro_f16_to_f32(rd16(b + off)), dmin = ro_f16_to_f32(rd16(b + off + 2));
+    for (int i = 0; i < 256; ++i) {
+        int sc, q;
+        if (type == RO_GGML_Q8_K) {
+            const int l = i / 8, sb = b[256 + l / 2];
+            sc = (l % 2 == 0) ? (sb & 0xF) : (sb >> 4);
+            q = (int8_t)b[i];
+        } else {
+            const uint8_t *scales = b + 4;
+            const uint8_t *qh = scales + (type == RO_GGML_Q2_K ? 16 : 32), *qs = qh + 32;
+            const int qsb = (qs[i / 4] >> ((i % 4) * 2)) & 3, qhb = (qh[i / 8] >> (i % 8)) & 1;
+            if (type == RO_GGML_Q2_K) {
+                const int l = i / 16, sb = scales[l / 2];
+                sc = (l % 2 == 0) ? (sb & 0xF) : (sb >> 4);
+                q = (qsb | (qhb << 2)) - 2;
+            } else {
+                const int l = i / 8;
+                sc = (scales[l / 4] >> ((l % 4) * 2)) & 0x3F;
+                q = (qsb | (qhb << 2)) - 4;
+            }
+        }
+        t = d * (float)sc;
+        t = t * (float)q;
+        y[i] = (float)(t + dmin);
+    }
+}
+
 static void dequantize_block32(int type, const uint8_t *b, float *y)
 {
     volatile float t; /* keeps each rounding step separate */
@@ -258,6 +333,14 @@ int ro_dequantize_tensor(const uint8_t *data, size_t nbytes, int type,
             memcpy(&b, data + i * sizeof b, sizeof b);
             ro_dequantize_q8_0(&b, out + i * RO_QK8_0);
         }
+        return RO_OK;
+    }
+    if (ro_kquant_bytes(type)) { /* quant.rs:722-756, 859-892: no size validation */
+        const size_t bb = (size_t)ro_kquant_bytes(type), nb = nbytes / bb;
+        if (nb * 256 > element_count)
+            return RO_PANIC;
+        for (size_t i = 0; i < nb; ++i)
+            dequantize_kquant(type, data + i * bb, out + i * 256);
         return RO_OK;
     }
     if (ro_block32_bytes(type)) { /* quant.rs:773-856: no size validation */
@@ -453,6 +536,9 @@ int ro_candle_fused(int type, const void *blocks, size_t nblocks,
             ro_dequantize_q6_k((const ro_block_q6_k *)blocks + i, w + i * per);
         else if (type == RO_GGML_Q8_0)
             ro_dequantize_q8_0((const ro_block_q8_0 *)blocks + i, w + i * per);
+        else if (ro_kquant_bytes(type))
+            dequantize_kquant(type, (const uint8_t *)blocks + i * ro_kquant_bytes(type),
+                              w + i * per);
         else if (ro_block32_bytes(type))
             dequantize_block32(type, (const uint8_t *)blocks + i * ro_block32_bytes(type),
                                w + i * per);

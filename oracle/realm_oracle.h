@@ -43,8 +43,12 @@ extern "C" {
 #define RO_GGML_Q5_1 7
 #define RO_GGML_Q8_0 8
 #define RO_GGML_Q8_1 9
+#define RO_GGML_Q2_K 10
+#define RO_GGML_Q3_K 11
 #define RO_GGML_Q4_K 12
+#define RO_GGML_Q5_K 13
 #define RO_GGML_Q6_K 14
+#define RO_GGML_Q8_K 15
 
 #define RO_QK_K 256
 #define RO_QK8_0 32
@@ -75,6 +79,9 @@ float ro_f16_to_f32(uint16_t h);
 /* Bytes per block of the 32-element formats Q4_0/Q4_1/Q5_0/Q5_1/Q8_1 (0 for
  * others). */
 int ro_block32_bytes(int type);
+/* bytes of one 256-element block of the reference's own Q2_K / Q3_K / Q5_K /
+ * Q8_K layouts (their #[repr(C)] sizes), 0 for other types */
+int ro_kquant_bytes(int type);
 uint16_t ro_f32_to_f16(float f);
 
 void ro_get_scale_min_k4(int j, const uint8_t *scales, uint8_t *sc, uint8_t *m);

@@ -119,6 +119,14 @@ SIGNATURES = {
                                                    c_size_t, c_size_t, c_size_t, c_void_p]),
     "realm_hip_fused_dequant_matmul_q81": (c_int, [c_void_p, c_size_t, c_void_p, c_size_t,
                                                    c_size_t, c_size_t, c_size_t, c_void_p]),
+    "realm_hip_fused_dequant_matmul_q5k": (c_int, [c_void_p, c_size_t, c_void_p, c_size_t,
+                                                   c_size_t, c_size_t, c_size_t, c_void_p]),
+    "realm_hip_fused_dequant_matmul_q8k": (c_int, [c_void_p, c_size_t, c_void_p, c_size_t,
+                                                   c_size_t, c_size_t, c_size_t, c_void_p]),
+    "realm_hip_fused_dequant_matmul_q2k": (c_int, [c_void_p, c_size_t, c_void_p, c_size_t,
+                                                   c_size_t, c_size_t, c_size_t, c_void_p]),
+    "realm_hip_fused_dequant_matmul_q3k": (c_int, [c_void_p, c_size_t, c_void_p, c_size_t,
+                                                   c_size_t, c_size_t, c_size_t, c_void_p]),
 }
 
 _lib = None

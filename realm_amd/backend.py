@@ -142,11 +142,14 @@ class HipGpuBackend:
     def fused_dequant_matmul_q80(self, blocks, input, batch_size, n, k):
         return self._fused(GGML_Q8_0, blocks, input, batch_size, n, k)
 
-    # the reference's 32-element formats: bytes per block (quant.rs:10-70)
-    BLOCK32_BYTES = {"q40": 18, "q41": 20, "q50": 22, "q51": 24, "q81": 36}
+    # bytes per block of the formats passed as raw bytes: the reference's
+    # 32-element formats (quant.rs:10-70) and its own 256-element Q5_K,
+    # Q8_K, Q2_K, Q3_K layouts (quant.rs:71-95, 200-222)
+    BLOCK32_BYTES = {"q40": 18, "q41": 20, "q50": 22, "q51": 24, "q81": 36,
+                     "q5k": 178, "q8k": 292, "q2k": 116, "q3k": 196}
 
     def _fused_raw(self, fmt: str, blocks, input, batch_size: int, n: int, k: int):
-        """Q4_0/Q4_1/Q5_0/Q5_1/Q8_1 blocks as raw bytes (or a record array)."""
+        """Blocks of the formats above as raw bytes (or a record array)."""
         raw = np.ascontiguousarray(blocks).view(np.uint8).reshape(-1)
         x = np.ascontiguousarray(input, np.float32)
         out = np.empty(batch_size * n, np.float32)
@@ -155,20 +158,17 @@ class HipGpuBackend:
                        batch_size, n, k, _ptr(out)))
         return out
 
-    def _unsupported(self, fmt: str):
-        raise BackendError(BACKEND_UNSUPPORTED, f"{fmt} is not supported by the HIP backend")
+    def fused_dequant_matmul_q5k(self, blocks, input, batch_size, n, k):
+        return self._fused_raw("q5k", blocks, input, batch_size, n, k)
 
-    def fused_dequant_matmul_q5k(self, *a):
-        self._unsupported("Q5_K")
+    def fused_dequant_matmul_q8k(self, blocks, input, batch_size, n, k):
+        return self._fused_raw("q8k", blocks, input, batch_size, n, k)
 
-    def fused_dequant_matmul_q8k(self, *a):
-        self._unsupported("Q8_K")
+    def fused_dequant_matmul_q2k(self, blocks, input, batch_size, n, k):
+        return self._fused_raw("q2k", blocks, input, batch_size, n, k)
 
-    def fused_dequant_matmul_q2k(self, *a):
-        self._unsupported("Q2_K")
-
-    def fused_dequant_matmul_q3k(self, *a):
-        self._unsupported("Q3_K")
+    def fused_dequant_matmul_q3k(self, blocks, input, batch_size, n, k):
+        return self._fused_raw("q3k", blocks, input, batch_size, n, k)
 
     def fused_dequant_matmul_q40(self, blocks, input, batch_size, n, k):
         return self._fused_raw("q40", blocks, input, batch_size, n, k)

@@ -28,6 +28,8 @@
 
 // realm_hip.cpp: sets the calling thread's last-error message, returns code
 int realm_set_error(int code, const std::string &msg);
+// Free device memory of the library's device, in bytes (initialises it).
+int realm_device_free_bytes(size_t *bytes);
 
 namespace {
 
@@ -471,6 +473,22 @@ REALM_API int realm_hip_gguf_register(uint64_t model, const void *bytes, size_t 
             todo.emplace_back(i, t);
         }
     }
+    // the device footprint of all of them first (the 32-element formats stay
+    // resident dequantized, 4 bytes per weight): an image that cannot fit is
+    // refused before anything is registered
+    size_t need = 0, free_bytes = 0;
+    for (auto &it : todo) {
+        const Tensor &t = it.second;
+        const bool f32res = t.type != REALM_GGML_Q4_K && t.type != REALM_GGML_Q6_K &&
+                            t.type != REALM_GGML_Q8_0;
+        need += f32res ? (size_t)(t.dims[0] * t.dims[1] * 4) : (size_t)t.nbytes + (size_t)t.nbytes / 8;
+    }
+    GG_TRY(realm_device_free_bytes(&free_bytes));
+    if (need > free_bytes)
+        return realm_set_error(REALM_OUT_OF_MEMORY,
+                               "registering the image's quantized tensors needs about " +
+                                   std::to_string(need) + " bytes of device memory, " +
+                                   std::to_string(free_bytes) + " are free");
     size_t count = 0;
     for (auto &it : todo) {
         const Tensor &t = it.second;

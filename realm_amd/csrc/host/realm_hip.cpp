@@ -105,15 +105,36 @@ constexpr int GGML_Q8_0 = REALM_GGML_Q8_0, GGML_Q4_K = REALM_GGML_Q4_K,
 // (quant.rs:10-70): dequantized on the device, products through the dense
 // f32 GEMM (as CandleGpuBackend's fused_dequant_matmul_q40 etc.).
 bool is_block32(int t) { return t == 2 || t == 3 || t == 6 || t == 7 || t == 9; }
-size_t block32_bytes(int t)
+// The reference's own 256-element Q2_K, Q3_K, Q5_K, Q8_K layouts
+// (quant.rs:71-95, 200-222; #[repr(C)] sizes 116, 196, 178, 292 bytes, not
+// ggml's): the same treatment as the 32-element formats.
+bool is_kq(int t) { return t == 10 || t == 11 || t == 13 || t == 15; }
+// formats kept dequantized in f32 on the device
+bool is_dq(int t) { return is_block32(t) || is_kq(t); }
+size_t dq_bytes(int t)
 {
-    return t == 2 ? 18 : t == 3 ? 20 : t == 6 ? 22 : t == 7 ? 24 : t == 9 ? 36 : 0;
+    return t == 2 ? 18 : t == 3 ? 20 : t == 6 ? 22 : t == 7 ? 24 : t == 9 ? 36
+         : t == 10 ? 116 : t == 11 ? 196 : t == 13 ? 178 : t == 15 ? 292 : 0;
 }
 size_t block_bytes(int t)
 {
-    return t == GGML_Q4_K ? 144 : t == GGML_Q6_K ? 210 : is_block32(t) ? block32_bytes(t) : 34;
+    return t == GGML_Q4_K ? 144 : t == GGML_Q6_K ? 210 : is_dq(t) ? dq_bytes(t) : 34;
 }
-size_t block_elems(int t) { return (t == GGML_Q4_K || t == GGML_Q6_K) ? 256 : 32; }
+size_t block_elems(int t) { return (t == GGML_Q4_K || t == GGML_Q6_K || is_kq(t)) ? 256 : 32; }
+const char *dq_name(int t)
+{
+    switch (t) {
+    case 2: return "Q4_0";
+    case 3: return "Q4_1";
+    case 6: return "Q5_0";
+    case 7: return "Q5_1";
+    case 9: return "Q8_1";
+    case 10: return "Q2_K";
+    case 11: return "Q3_K";
+    case 13: return "Q5_K";
+    default: return "Q8_K";
+    }
+}
 size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 size_t round_up(size_t v, size_t m) { return (v + m - 1) / m * m; }
 const char *fmt_name(int t) { return t == GGML_Q4_K ? "q4k" : t == GGML_Q6_K ? "q6k" : "q80"; }
@@ -988,7 +1009,7 @@ int dense_launch(const float *da, const float *db, float *dc, size_t m, size_t k
 int run_matmul(const Weight &w, const void *d_x, bool bf16, size_t M, float *d_y,
                hipStream_t s, const LoraCall *lora)
 {
-    if (is_block32(w.type)) { // resident as dequantized f32 [n][k]: y = x W^T
+    if (is_dq(w.type)) { // resident as dequantized f32 [n][k]: y = x W^T
         if (bf16 || lora)
             return fail(REALM_BACKEND_UNSUPPORTED,
                         "bf16 input and LoRA take Q4_K, Q6_K or Q8_0 weights");
@@ -1044,22 +1065,42 @@ int validate_fused(int type, size_t n_blocks, size_t input_len, size_t batch, si
 int dense_launch(const float *da, const float *db, float *dc, size_t m, size_t k, size_t n,
                  int bt, hipStream_t s);
 
-// Q4_0 / Q4_1 / Q5_0 / Q5_1 / Q8_1 (candle_backend.rs:837-1103): validated
-// as the reference does, dequantized on the device into f32 W [n][k], then
-// y = x W^T on the f32 MFMA GEMM.
+// Dequantize nb blocks of a kept-dequantized format (raw reference bytes on
+// the device) into f32 y on stream s.
+int dq_launch(int type, const void *raw, float *y, size_t nb, hipStream_t s)
+{
+    long long lnb = (long long)nb;
+    int it = type;
+    void *args[] = {(void *)&raw, &y, &lnb, &it};
+    const size_t per = block_elems(type);
+    return launch(is_kq(type) ? "realm_dequant_kq" : "realm_dequant_q32",
+                  dim3((unsigned)((nb * per + 255) / 256)), dim3(256), 0, s, args);
+}
+
+// Q4_0 / Q4_1 / Q5_0 / Q5_1 / Q8_1 (candle_backend.rs:837-1103) and the
+// reference's Q5_K / Q8_K / Q2_K / Q3_K (candle_backend.rs:507-571,
+// 639-836): validated as the reference does, dequantized on the device into
+// f32 W [n][k], then y = x W^T on the f32 MFMA GEMM.
 int fused_block32(int type, const void *blocks, size_t n_blocks, const float *input,
                   size_t input_len, size_t batch, size_t n, size_t k, float *out)
 {
-    if (k % 32)
+    const size_t qk = block_elems(type);
+    if (k % qk)
         return fail(REALM_INVALID_ARGUMENT, "K dimension " + std::to_string(k) +
-                                                " must be multiple of 32");
-    if (n_blocks != n * (k / 32))
-        return fail(REALM_INVALID_ARGUMENT, "Expected " + std::to_string(n * (k / 32)) +
-                                                " blocks, got " + std::to_string(n_blocks));
-    if (input_len != batch * k)
+                                                " must be multiple of " + std::to_string(qk));
+    if (n_blocks != n * (k / qk))
+        return fail(REALM_INVALID_ARGUMENT, "Expected " + std::to_string(n * (k / qk)) + " " +
+                                                dq_name(type) + " blocks, got " +
+                                                std::to_string(n_blocks));
+    if (input_len != batch * k) {
+        // the 32-element formats check the input length (InvalidShape); for
+        // the K formats the tensor creation fails (Error::Runtime)
+        if (is_kq(type))
+            return fail(REALM_GENERIC_FAILURE, "Failed to create input tensor: shape mismatch");
         return fail(REALM_INVALID_ARGUMENT, "Input length " + std::to_string(input_len) +
                                                 " does not match batch_size * k = " +
                                                 std::to_string(batch * k));
+    }
     if (!out || (n_blocks && !blocks) || (input_len && !input))
         return fail(REALM_INVALID_ARGUMENT, "null pointer argument");
     if (n > (size_t)INT32_MAX || k > (size_t)INT32_MAX || batch > (size_t)INT32_MAX)
@@ -1074,18 +1115,14 @@ int fused_block32(int type, const void *blocks, size_t n_blocks, const float *in
     hipStream_t s;
     CHECK(thread_stream(&s));
     void *raw, *w, *dx, *dy;
-    const size_t bb = block32_bytes(type);
+    const size_t bb = dq_bytes(type);
     CHECK(ws_get(s, WS_RAW, n_blocks * bb, &raw));
     CHECK(ws_get(s, WS_WEIGHT, n * k * 4, &w));
     CHECK(ws_get(s, WS_X, batch * k * 4, &dx));
     CHECK(ws_get(s, WS_Y, batch * n * 4, &dy));
     HIP_TRY(hipMemcpyAsync(raw, blocks, n_blocks * bb, hipMemcpyHostToDevice, s));
     HIP_TRY(hipMemcpyAsync(dx, input, batch * k * 4, hipMemcpyHostToDevice, s));
-    long long lnb = (long long)n_blocks;
-    int it = type;
-    void *args[] = {&raw, &w, &lnb, &it};
-    CHECK(launch("realm_dequant_q32", dim3((unsigned)((n_blocks * 32 + 255) / 256)), dim3(256),
-                 0, s, args));
+    CHECK(dq_launch(type, raw, (float *)w, n_blocks, s));
     CHECK(dense_launch((const float *)dx, (const float *)w, (float *)dy, batch, k, n, 1, s));
     HIP_TRY(hipMemcpyAsync(out, dy, batch * n * 4, hipMemcpyDeviceToHost, s));
     HIP_TRY(hipStreamSynchronize(s));
@@ -1095,7 +1132,7 @@ int fused_block32(int type, const void *blocks, size_t n_blocks, const float *in
 int fused_host(int type, const void *blocks, size_t n_blocks, const float *input,
                size_t input_len, size_t batch, size_t n, size_t k, float *out)
 {
-    if (is_block32(type))
+    if (is_dq(type))
         return fused_block32(type, blocks, n_blocks, input, input_len, batch, n, k, out);
     if (type != GGML_Q4_K && type != GGML_Q6_K && type != GGML_Q8_0)
         return fail(REALM_BACKEND_UNSUPPORTED,
@@ -1643,6 +1680,38 @@ REALM_API int realm_hip_fused_dequant_matmul_q81(const void *blocks, size_t n_bl
     return fused_host(9, blocks, n_blocks, input, input_len, batch_size, n, k, out);
 }
 
+REALM_API int realm_hip_fused_dequant_matmul_q5k(const void *blocks, size_t n_blocks,
+                                                 const float *input, size_t input_len,
+                                                 size_t batch_size, size_t n, size_t k,
+                                                 float *out)
+{
+    return fused_host(13, blocks, n_blocks, input, input_len, batch_size, n, k, out);
+}
+
+REALM_API int realm_hip_fused_dequant_matmul_q8k(const void *blocks, size_t n_blocks,
+                                                 const float *input, size_t input_len,
+                                                 size_t batch_size, size_t n, size_t k,
+                                                 float *out)
+{
+    return fused_host(15, blocks, n_blocks, input, input_len, batch_size, n, k, out);
+}
+
+REALM_API int realm_hip_fused_dequant_matmul_q2k(const void *blocks, size_t n_blocks,
+                                                 const float *input, size_t input_len,
+                                                 size_t batch_size, size_t n, size_t k,
+                                                 float *out)
+{
+    return fused_host(10, blocks, n_blocks, input, input_len, batch_size, n, k, out);
+}
+
+REALM_API int realm_hip_fused_dequant_matmul_q3k(const void *blocks, size_t n_blocks,
+                                                 const float *input, size_t input_len,
+                                                 size_t batch_size, size_t n, size_t k,
+                                                 float *out)
+{
+    return fused_host(11, blocks, n_blocks, input, input_len, batch_size, n, k, out);
+}
+
 REALM_API int realm_hip_fused_dequant_matmul_q4k(const void *blocks, size_t n_blocks,
                                                  const float *input, size_t input_len,
                                                  size_t batch_size, size_t n, size_t k,
@@ -1692,7 +1761,7 @@ REALM_API int32_t realm_hip_candle_matmul_transposed(uint8_t *mem, size_t mem_le
 REALM_API int realm_hip_dequantize(int type, const void *data, size_t nbytes,
                                    size_t element_count, float *out)
 {
-    if (type != GGML_Q4_K && type != GGML_Q6_K && type != GGML_Q8_0 && !is_block32(type))
+    if (type != GGML_Q4_K && type != GGML_Q6_K && type != GGML_Q8_0 && !is_dq(type))
         return fail(REALM_BACKEND_UNSUPPORTED,
                     "ggml type " + std::to_string(type) + " is not supported by the HIP backend");
     size_t bb = block_bytes(type), qk = block_elems(type);
@@ -1722,11 +1791,8 @@ REALM_API int realm_hip_dequantize(int type, const void *data, size_t nbytes,
     CHECK(ws_get(s, WS_Y, nb * qk * 4, &dy));
     HIP_TRY(hipMemcpyAsync(raw, data, nb * bb, hipMemcpyHostToDevice, s));
     long long lnb = (long long)nb;
-    if (is_block32(type)) {
-        int it = type;
-        void *args[] = {&raw, &dy, &lnb, &it};
-        CHECK(launch("realm_dequant_q32", dim3((unsigned)((nb * 32 + 255) / 256)), dim3(256), 0, s,
-                     args));
+    if (is_dq(type)) {
+        CHECK(dq_launch(type, raw, (float *)dy, nb, s));
     } else {
         void *args[] = {&raw, &dy, &lnb};
         size_t threads = nb * (type == GGML_Q4_K ? 128 : type == GGML_Q6_K ? 64 : 32);
@@ -1743,7 +1809,7 @@ REALM_API int realm_hip_weights_register(int type, const void *blocks, size_t nb
 {
     if (!handle)
         return fail(REALM_INVALID_ARGUMENT, "handle is null");
-    if (type != GGML_Q4_K && type != GGML_Q6_K && type != GGML_Q8_0 && !is_block32(type))
+    if (type != GGML_Q4_K && type != GGML_Q6_K && type != GGML_Q8_0 && !is_dq(type))
         return fail(REALM_BACKEND_UNSUPPORTED,
                     "ggml type " + std::to_string(type) + " is not supported by the HIP backend");
     size_t qk = block_elems(type);
@@ -1760,18 +1826,15 @@ REALM_API int realm_hip_weights_register(int type, const void *blocks, size_t nb
     CHECK(ensure_init());
     hipStream_t s;
     CHECK(thread_stream(&s));
-    if (is_block32(type)) {
-        // the 32-element formats stay resident dequantized (f32 [n][k],
-        // 4 bytes per weight), their products on the f32 GEMM
+    if (is_dq(type)) {
+        // the 32-element formats and the reference's own Q2_K / Q3_K / Q5_K /
+        // Q8_K stay resident dequantized (f32 [n][k], 4 bytes per weight),
+        // their products on the f32 GEMM
         void *dev = nullptr, *raw = nullptr;
         CHECK(ws_get(s, WS_RAW, nbytes, &raw));
         HIP_TRY(hipMalloc(&dev, n * k * 4));
-        long long lnb = (long long)(n * (k / 32));
-        int it = type;
-        void *args[] = {&raw, &dev, &lnb, &it};
         int rc = hipMemcpyAsync(raw, blocks, nbytes, hipMemcpyHostToDevice, s) == hipSuccess
-                     ? launch("realm_dequant_q32", dim3((unsigned)((n * k + 255) / 256)),
-                              dim3(256), 0, s, args)
+                     ? dq_launch(type, raw, (float *)dev, n * (k / qk), s)
                      : fail(REALM_GENERIC_FAILURE, "upload failed");
         if (rc == REALM_OK && hipStreamSynchronize(s) != hipSuccess)
             rc = fail(REALM_GENERIC_FAILURE, "dequantization failed");
@@ -1927,7 +1990,7 @@ REALM_API int realm_hip_weights_matmul_group_dev(const uint64_t *handles, size_t
         return fail(REALM_INVALID_ARGUMENT, "batch exceeds 2^31-1");
     hipStream_t s;
     CHECK(pick_stream(stream, &s));
-    if (is_block32(w[0].type)) { // dequantized f32 weights: one dense product each
+    if (is_dq(w[0].type)) { // dequantized f32 weights: one dense product each
         for (size_t i = 0; i < count; ++i)
             CHECK(run_matmul(w[i], d_input, false, batch, d_outs[i], s, nullptr));
         return REALM_OK;
@@ -2124,7 +2187,7 @@ namespace {
 int lora_lookup(uint64_t wh, uint64_t sh, size_t batch, Weight *w, AdapterSet *set)
 {
     CHECK(get_weight(wh, w));
-    if (is_block32(w->type))
+    if (is_dq(w->type))
         return fail(REALM_BACKEND_UNSUPPORTED, "multi-LoRA takes Q4_K, Q6_K or Q8_0 base weights");
     {
         std::lock_guard<std::mutex> lk(g_mu);
@@ -2489,3 +2552,11 @@ REALM_API int realm_hip_event_elapsed_ms(void *start, void *stop, float *ms)
 }
 
 int realm_set_error(int code, const std::string &msg) { return fail(code, msg); }
+
+int realm_device_free_bytes(size_t *bytes)
+{
+    CHECK(ensure_init());
+    size_t total = 0;
+    HIP_TRY(hipMemGetInfo(bytes, &total));
+    return REALM_OK;
+}

@@ -226,3 +226,61 @@ extern "C" __global__ __launch_bounds__(256) void realm_dequant_q32(const uint8_
     const float t = __fmul_rn((float)q, s);
     y[e] = delta ? __fadd_rn(t, d) : t;
 }
+
+// The reference's own 256-element Q2_K (type 10, 116 B), Q3_K (11, 196 B),
+// Q5_K (13, 178 B) and Q8_K (15, 292 B) blocks (crates/realm-core/src/
+// quant.rs:71-95, 200-222, their #[repr(C)] sizes, not ggml's), dequantized
+// as quant.rs:453-638 does, one thread per output element; separate f32
+// roundings (__fmul_rn / __fadd_rn) in the reference's left-to-right order:
+//   Q2_K: d * sc * q + dmin, q = 2 bits of qs[i/4] | bit of qh[i/8] << 2, - 2;
+//         sc = nibble (i/16)%2 of scales[i/32]
+//   Q3_K: the same bits, - 4; sc = (scales[i/32] >> 2((i/8)%4)) & 63
+//   Q5_K: d * scales[i/16] * q for i < 128, q = int8(ql[i] | (qh nibble
+//         (i%16)/4 %2 of qh[2(i/16) + (i%16)/8]) << 4); elements 128..255 are
+//         never written by the reference (ql holds 128 bytes) and stay 0
+//   Q8_K: d * sc * quants[i] + dmin, sc = nibble (i/8)%2 of scales[i/16]
+extern "C" __global__ __launch_bounds__(256) void realm_dequant_kq(const uint8_t *raw, float *y,
+                                                                  long long nb, int type)
+{
+    const long long e = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (e >= nb * 256)
+        return;
+    const int i = (int)(e & 255);
+    const int bb = type == 10 ? 116 : type == 11 ? 196 : type == 13 ? 178 : 292;
+    const uint8_t *b = raw + (e >> 8) * bb;
+    if (type == 13) {
+        if (i >= 128) {
+            y[e] = 0.f;
+            return;
+        }
+        const int l = i >> 4, k = i & 15;
+        const int qhv = (b[128 + 2 * l + (k >> 3)] >> (4 * ((k & 7) >> 2))) & 0xF;
+        const int q = (int8_t)(uint8_t)(b[i] | ((qhv << 4) & 0xFF));
+        const float d = realm::f16_bits_to_f32(b[176] | (b[177] << 8));
+        y[e] = __fmul_rn(__fmul_rn(d, (float)(int8_t)b[160 + l]), (float)q);
+        return;
+    }
+    const int off = type == 15 ? 288 : 0;
+    const float d = realm::f16_bits_to_f32(b[off] | (b[off + 1] << 8));
+    const float dmin = realm::f16_bits_to_f32(b[off + 2] | (b[off + 3] << 8));
+    int sc, q;
+    if (type == 15) {
+        const int l = i >> 3, sbyte = b[256 + (l >> 1)];
+        sc = (l & 1) ? (sbyte >> 4) : (sbyte & 0xF);
+        q = (int8_t)b[i];
+    } else {
+        const uint8_t *scales = b + 4;
+        const uint8_t *qh = scales + (type == 10 ? 16 : 32), *qs = qh + 32;
+        const int qsb = (qs[i >> 2] >> ((i & 3) * 2)) & 3, qhb = (qh[i >> 3] >> (i & 7)) & 1;
+        if (type == 10) {
+            const int l = i >> 4, sbyte = scales[l >> 1];
+            sc = (l & 1) ? (sbyte >> 4) : (sbyte & 0xF);
+            q = (qsb | (qhb << 2)) - 2;
+        } else {
+            const int l = i >> 3;
+            sc = (scales[l >> 2] >> ((l & 3) * 2)) & 0x3F;
+            q = (qsb | (qhb << 2)) - 4;
+        }
+    }
+    y[e] = __fadd_rn(__fmul_rn(__fmul_rn(d, (float)sc), (float)q), dmin);
+}

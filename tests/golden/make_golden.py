@@ -20,6 +20,41 @@ fixtures check both.  Sources:
              elements 128h+l / 128h+l+64, ql[64h+l+32] low/high -> +32 / +96,
              with the 2 high bits from qh[32h+l] bits (0-1, 2-3, 4-5, 6-7);
              value 63 - 32 = 31 at the probe, -32 elsewhere.
+  q5k_kat    quant.rs:1043-1075 (the reference's own 178-byte Q5_K: scales 1,
+             d=1, ql[0]=0x10, the rest 0): element 0 is the byte 0x10 = 16;
+             every other element of 0..127 is 0, and 128..255 are never
+             written (ql holds 128 bytes) -> 0.
+  q8k_kat    quant.rs:1077-1109 (292-byte Q8_K: d=1, dmin=0, quants[0]=10,
+             scales[0]=0x11): groups 0 and 1 have scale 1, the rest 0, and
+             only quants[0] is non-zero -> 10 at element 0, 0 elsewhere.
+  q2k_pos /  one-hot probes of the reference's Q2_K (116 B) and Q3_K (196 B):
+  q3k_pos    element i takes its two low bits from qs[i/4] at bit 2(i%4)
+             and its third bit from qh[i/8] at bit i%8 (quant.rs:565-575,
+             614-624); the probe sets all three for element i only, so q is
+             7 - 2 = 5 (Q2_K) or 7 - 4 = 3 (Q3_K) there and -2 / -4 elsewhere.
+             Q2_K scales 0x11 (every group scale 1); Q3_K scales 0xFF, whose
+             group scales are (0xFF >> 2(l%4)) & 63 = 63, 63, 15, 3 for
+             l%4 = 0..3 (groups of 8).  d=1, dmin=0.
+  q2k_scale  Q2_K scale nibbles: scales[j] = 2j | (2j+1) << 4 gives group l
+             (16 elements) the scale l; every q is (1 | 0) - 2 = -1, so
+             element i is -(i // 16).
+  q3k_scale  Q3_K scales all 0xE4: group scales 0x24 = 36, 0x39 = 57,
+             0xE4 >> 4 = 14, 0xE4 >> 6 = 3 for l%4 = 0..3; every q is 1 - 4 =
+             -3 -> -3 x those, eight elements per group.
+  q5k_pos    Q5_K probes: ql[i] = 0x0F for one i < 128 -> 15 there (scales 1,
+             d=1), 0 elsewhere; ql[i] = 0x80 -> int8 -128; qh[j] = 0x0F sets
+             the fifth bit of elements 16(j//2) + 8(j%2) + 0..3 (byte 0xF0 as
+             int8: -16), qh[j] = 0xF0 of elements 16(j//2) + 8(j%2) + 4..7;
+             qh[16..31] feed nothing.
+  q8k_scale  Q8_K: scales[j] = 0x21 for j < 16 and 0xFF beyond (unused:
+             groups read scales[l/2] for l < 32); quants 1, d=1, dmin=0.5 ->
+             group scale 1 or 2 by group parity: 1.5 and 2.5 in runs of 8.
+  q5_0_qh /  the reference's own Q5_0 / Q5_1 high-bit map (quant.rs:283-350),
+  q5_1_qh    written out by hand: in each qh byte j, Q5_0 feeds elements
+             8j + (0,1) from bit 0, (4,5) from bit 2, (2,3) from bit 4, (6,7)
+             from bit 6 (bits 1, 3, 5, 7 unused); Q5_1 feeds 8j + (0,1,4,5)
+             from bit 0 and (2,3,6,7) from bit 4.  With ql all 0 and scale 1,
+             a fed element is 16 - 16 = 0 and every other one -16.
   dense      crates/realm-compute-cpu/src/gemm.rs:197-226 ([22,28,49,64],
              [7,10,15,22]) and crates/realm-compute-gpu/src/
              candle_backend.rs:1258-1276 ([19,22,43,50]).
@@ -92,6 +127,107 @@ def main():
                 idx.append(128 * h + l + 32 * t)
     out["q6k_pos_blocks"] = np.concatenate(blocks)
     out["q6k_pos_index"] = np.array(idx, np.int32)
+    # --- the reference's own Q5_K / Q8_K / Q2_K / Q3_K layouts
+    def q5k_block(ql, qh, scales, d):
+        b = bytes(ql) + bytes(qh) + np.asarray(scales, np.int8).tobytes() + int(d).to_bytes(2, "little")
+        assert len(b) == 178
+        return np.frombuffer(b, np.uint8)
+
+    def q8k_block(quants, scales, d, dmin):
+        b = np.asarray(quants, np.int8).tobytes() + bytes(scales) + int(d).to_bytes(2, "little")
+        b += int(dmin).to_bytes(2, "little")
+        assert len(b) == 292
+        return np.frombuffer(b, np.uint8)
+
+    def q23k_block(nsc, scales, qh, qs, d, dmin):
+        b = int(d).to_bytes(2, "little") + int(dmin).to_bytes(2, "little")
+        b += bytes(scales) + bytes(qh) + bytes(qs)
+        assert len(b) == (116 if nsc == 16 else 196)
+        return np.frombuffer(b, np.uint8)
+
+    ql = [0] * 128
+    ql[0] = 0x10
+    out["q5k_kat_block"] = q5k_block(ql, [0] * 32, [1] * 16, F16(1.0))
+    e = np.zeros(256, np.float32)
+    e[0] = 16.0
+    out["q5k_kat_expected"] = e
+    qu = [0] * 256
+    qu[0] = 10
+    sc = [0] * 32
+    sc[0] = 0x11
+    out["q8k_kat_block"] = q8k_block(qu, sc, F16(1.0), F16(0.0))
+    e = np.zeros(256, np.float32)
+    e[0] = 10.0
+    out["q8k_kat_expected"] = e
+    # Q2_K / Q3_K one-hot probes, one block per element
+    q3_group_scale = [63, 63, 15, 3]  # (0xFF >> 2(l%4)) & 63
+    for name, nsc, scales, hot, cold in (("q2k", 16, [0x11] * 16, 5.0, -2.0),
+                                         ("q3k", 32, [0xFF] * 32, 3.0, -4.0)):
+        nqs = 64 if nsc == 16 else 128
+        blocks, exp = [], []
+        for i in range(256):
+            qs = [0] * nqs
+            qh = [0] * 32
+            qs[i // 4] = 3 << (2 * (i % 4))
+            qh[i // 8] = 1 << (i % 8)
+            blocks.append(q23k_block(nsc, scales, qh, qs, F16(1.0), F16(0.0)))
+            row = np.full(256, cold, np.float32)
+            row[i] = hot
+            if name == "q3k":
+                row *= np.array([q3_group_scale[(j // 8) % 4] for j in range(256)], np.float32)
+            exp.append(row)
+        out[f"{name}_pos_blocks"] = np.concatenate(blocks)
+        out[f"{name}_pos_expected"] = np.concatenate(exp)
+    # scale maps: every q-bit pattern (qs 1, qh 0) in every element
+    qs1 = [0x55] * 64  # 2-bit fields all 1
+    out["q2k_scale_block"] = q23k_block(16, [(2 * j) | ((2 * j + 1) << 4) for j in range(8)] + [0] * 8,
+                                        [0] * 32, qs1, F16(1.0), F16(0.0))
+    out["q2k_scale_expected"] = -np.repeat(np.arange(16, dtype=np.float32), 16)
+    out["q3k_scale_block"] = q23k_block(32, [0xE4] * 32, [0] * 32, [0x55] * 128, F16(1.0), F16(0.0))
+    out["q3k_scale_expected"] = np.tile(np.repeat(np.array([36, 57, 14, 3], np.float32), 8), 8) * -3
+    # Q5_K probes
+    blocks, exp = [], []
+    for i in range(128):
+        for byte, val in ((0x0F, 15.0), (0x80, -128.0)):
+            ql = [0] * 128
+            ql[i] = byte
+            blocks.append(q5k_block(ql, [0] * 32, [1] * 16, F16(1.0)))
+            row = np.zeros(256, np.float32)
+            row[i] = val
+            exp.append(row)
+    for j in range(32):
+        for byte in (0x0F, 0xF0):
+            qh = [0] * 32
+            qh[j] = byte
+            blocks.append(q5k_block([0] * 128, qh, [1] * 16, F16(1.0)))
+            row = np.zeros(256, np.float32)
+            if j < 16:
+                first = 16 * (j // 2) + 8 * (j % 2) + (0 if byte == 0x0F else 4)
+                row[first:first + 4] = -16.0
+            exp.append(row)
+    out["q5k_pos_blocks"] = np.concatenate(blocks)
+    out["q5k_pos_expected"] = np.concatenate(exp)
+    # Q8_K scale map
+    out["q8k_scale_block"] = q8k_block([1] * 256, [0x21] * 16 + [0xFF] * 16, F16(1.0), F16(0.5))
+    out["q8k_scale_expected"] = np.tile(np.repeat(np.array([1.5, 2.5], np.float32), 8), 16)
+    # Q5_0 / Q5_1 high-bit tables (hand-written from quant.rs:283-350)
+    Q50_BITS = {0: (0, 1), 2: (4, 5), 4: (2, 3), 6: (6, 7)}
+    Q51_BITS = {0: (0, 1, 4, 5), 4: (2, 3, 6, 7)}
+    for name, bb, table in (("q5_0", 22, Q50_BITS), ("q5_1", 24, Q51_BITS)):
+        blocks, exp = [], []
+        for j in range(4):
+            for bit in range(8):
+                b = bytearray(bb)
+                b[0:2] = F16(1.0).to_bytes(2, "little")
+                qh_off = 2 if bb == 22 else 4  # Q5_1: scale, delta (0), qh
+                b[qh_off + j] = 1 << bit
+                blocks.append(np.frombuffer(bytes(b), np.uint8))
+                row = np.full(32, -16.0, np.float32)
+                for el in table.get(bit, ()):
+                    row[8 * j + el] = 0.0
+                exp.append(row)
+        out[f"{name}_qh_blocks"] = np.concatenate(blocks)
+        out[f"{name}_qh_expected"] = np.concatenate(exp)
     # --- dense KATs: (a, b, m, k, n, transposed, expected)
     out["dense_a1"] = np.array([1, 2, 3, 4, 5, 6], np.float32)
     out["dense_b1"] = np.array([1, 2, 3, 4, 5, 6], np.float32)

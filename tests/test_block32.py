@@ -3,11 +3,11 @@
 forms (CPU), the HIP dequantization bit-exact against it and the fused
 dequant x matmul (CandleGpuBackend semantics) within 1e-3 relative L2 (GPU).
 
-Parity note: which qh bit feeds which Q5_0 / Q5_1 element is the
-reference's own index formula (quant.rs:283-350; neither matches ggml and no
-reference test covers it); the checks below pin the low nibbles and that a
-set high bit adds 16, not the bit-to-element map, which stays parity
-unpinned."""
+Which qh bit feeds which Q5_0 / Q5_1 element is the reference's own index
+formula (quant.rs:283-350; it matches neither ggml nor any reference test);
+the checks below pin the low nibbles and that a set high bit adds 16, and the
+bit-to-element map is pinned by hand-written one-hot tables
+(tests/golden/make_golden.py, checked in tests/test_kquant_ref.py)."""
 import numpy as np
 import pytest
 

@@ -272,3 +272,42 @@ def test_registered_tensors_by_name(backend, oracle):
                 assert rc == 0 and rel_l2(got, want.reshape(mm, n)) < 1e-3, (name, mm)
     finally:
         m.release()
+
+
+@pytest.mark.gpu
+def test_registered_block32_tensors(backend, oracle):
+    """A hand-assembled image with Q4_0 (18-byte blocks) and Q5_1 (24-byte
+    blocks) tensors, the byte sizes GGUF gives them: the library's and the
+    oracle parser's tensor tables agree on types and offsets, both register
+    as resident weights, and their products agree with the oracle's fused
+    matmul on the bytes at those offsets."""
+    g = np.random.default_rng(13)
+    specs = [("blk.0.attn_q.weight", 2, 18, 96, 256), ("blk.0.ffn_up.weight", 7, 24, 64, 512)]
+    ts = []
+    for name, ty, bb, n, k in specs:
+        raw = g.integers(0, 256, (n * k // 32, bb), dtype=np.uint8)
+        sc = (np.abs(g.standard_normal(n * k // 32)) * 1e-2).astype(np.float16).view(np.uint16)
+        raw[:, 0], raw[:, 1] = sc & 0xFF, sc >> 8
+        if ty == 7:  # Q5_1 delta
+            dl = (g.standard_normal(n * k // 32) * 1e-3).astype(np.float16).view(np.uint16)
+            raw[:, 2], raw[:, 3] = dl & 0xFF, dl >> 8
+        ts.append((name, [k, n], ty, raw.tobytes()))
+    img = gi.image(LLAMA_META, ts)
+    ref = og.parse(img)
+    m = _model(img)
+    try:
+        got_table = [(t.name, t.ggml_type, t.offset, t.nbytes) for t in m.tensors()]
+        assert got_table == [(nm, ty, ref["data_offset"] + off, n * k // 32 * bb)
+                             for (nm, _d, ty, off), (_, _, bb, n, k) in zip(ref["tensors"], specs)]
+        assert m.register() == 2
+        for (name, ty, bb, n, k), (_, _, _, off) in zip(specs, ref["tensors"]):
+            h, nn, kk = m.weight(name)
+            assert (nn, kk) == (n, k)
+            a = ref["data_offset"] + off
+            raw = np.frombuffer(img, np.uint8, count=n * k // 32 * bb, offset=a)
+            for mm in (1, 6):
+                x = g.standard_normal((mm, k)).astype(np.float32)
+                rc, want = oracle.candle_fused(ty, raw, x, mm, n, k)
+                assert rc == 0 and rel_l2(backend.weights_matmul(h, x), want.reshape(mm, n)) < 1e-3
+    finally:
+        m.release()

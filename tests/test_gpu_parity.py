@@ -92,7 +92,7 @@ def test_dequantize_tensor_semantics(backend, oracle):
     with pytest.raises(InvalidShape):  # the reference panics here
         backend.dequantize(GGML_Q6_K, b6, 300)
     with pytest.raises(BackendError):
-        backend.dequantize(10, b6, 256)  # Q2_K: not built here
+        backend.dequantize(1, b6, 256)  # F16: not a block format of this path
 
 
 def test_trait_validation(backend):
@@ -108,8 +108,13 @@ def test_trait_validation(backend):
     with pytest.raises(InvalidShape):
         backend.fused_dequant_matmul_q80(np.zeros(2, Q80_DTYPE), np.zeros(40, np.float32),
                                          1, 1, 40)
-    with pytest.raises(BackendError):
-        backend.fused_dequant_matmul_q5k(None, None, 1, 1, 256)
+    # a type the backend does not build (F16 here): a cheap BackendUnsupported,
+    # so dispatch_matmul falls back to the CPU
+    x = np.zeros(256, np.float32)
+    out = np.zeros(1, np.float32)
+    rc = backend.lib.realm_hip_fused_dequant_matmul(1, x.ctypes.data, 1, x.ctypes.data, 256, 1, 1,
+                                                    256, out.ctypes.data)
+    assert rc == 5, rc
     # empty K: zero output, like the reference's empty accumulation
     y = backend.fused_dequant_matmul_q4k(np.zeros(0, Q4K_DTYPE), np.zeros(0, np.float32), 2, 3, 0)
     assert np.array_equal(y, np.zeros(6, np.float32))
