@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define REALM_HIP_ABI_VERSION 1
+#define REALM_HIP_ABI_VERSION 2
 
 /* Error codes: crates/realm-runtime/src/lib.rs:110-135 (ErrorCode) and the
  * From<realm_core::Error> mapping there: InvalidShape -> InvalidArgument,
@@ -372,12 +372,25 @@ int realm_hip_add_dev(const float *d_a, const float *d_b, size_t n, float *d_out
  * registered weight handles (Wq, Wo [hidden x hidden], Wk, Wv [kv_heads *
  * head_dim x hidden], W_gate, W_up [intermediate x hidden], W_down
  * [hidden x intermediate]), the two norm weight vectors on the device, and
- * the TransformerConfig fields the layer reads (gguf.rs:212-280). */
+ * the TransformerConfig fields the layer reads (gguf.rs:212-280).
+ *
+ * Per-tenant LoRA (apply_lora_to_weight_format on each of the seven
+ * projections, memory64_host.rs:625-680, 2232-2274, 2347-2378, with keys
+ * layer.N.attn_q .. ffn_down as lora_integration.rs:198-270 builds them):
+ * lora_q .. lora_down are adapter sets (realm_hip_lora_set_create, 0 = no
+ * adapters on that projection) whose slot t holds tenant t's adapter for it;
+ * token i of the call uses slot d_adapter_ids[i] of every set (-1, or a slot
+ * past a set's size: that projection's base product).  The reference merges
+ * one tenant's delta into the weights; here y = W x + s B (A x) per token,
+ * the same product, for a batch that mixes tenants.  Calls with adapters
+ * take at most 1024 tokens. */
 typedef struct realm_layer {
     uint64_t wq, wk, wv, wo, w_gate, w_up, w_down;
     const float *attn_norm, *ffn_norm;
     uint32_t hidden, num_heads, num_kv_heads, head_dim, intermediate;
     float rms_norm_eps, rope_theta;
+    uint64_t lora_q, lora_k, lora_v, lora_o, lora_gate, lora_up, lora_down;
+    const int32_t *d_adapter_ids;
 } realm_layer;
 
 /* realm_forward_layer (crates/realm-runtime/src/memory64_host.rs:1915-2472)

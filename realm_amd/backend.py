@@ -424,7 +424,12 @@ class RealmLayer(ctypes.Structure):
                 ("hidden", ctypes.c_uint32), ("num_heads", ctypes.c_uint32),
                 ("num_kv_heads", ctypes.c_uint32), ("head_dim", ctypes.c_uint32),
                 ("intermediate", ctypes.c_uint32), ("rms_norm_eps", ctypes.c_float),
-                ("rope_theta", ctypes.c_float)]
+                ("rope_theta", ctypes.c_float),
+                # per-tenant LoRA: adapter sets per projection (0 = none), device
+                # adapter slot per token
+                ("lora_q", c_uint64), ("lora_k", c_uint64), ("lora_v", c_uint64),
+                ("lora_o", c_uint64), ("lora_gate", c_uint64), ("lora_up", c_uint64),
+                ("lora_down", c_uint64), ("d_adapter_ids", c_void_p)]
 
 
 __all__ = ["HipGpuBackend", "RealmLayer", "RealmError", "InvalidShape", "BackendError",

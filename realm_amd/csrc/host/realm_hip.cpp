@@ -854,6 +854,8 @@ realm::LoraGroupArgs lora_group_args(const Weight *const *w, const LoraCall *lc,
     g.xh = p.xh;
     g.xl = p.xl;
     g.tscale = (const float *)p.ts;
+    g.x = p.x;
+    g.xbf16 = p.bf16 ? 1 : 0;
     g.ids = lc[0].d_ids;
     g.M = (int)M;
     g.K = (int)w[0]->k;
@@ -1409,12 +1411,21 @@ REALM_API int realm_hip_attention_dev(const float *d_q, const float *d_k_cache,
         if (v >= 1 && v <= 64)
             splits = (size_t)v;
     }
+    // Any cache length: when the scores of all visible keys do not fit in
+    // one workgroup's LDS, at least as many splits as keep every chunk's
+    // scores (plus q and the reduction slots) inside it.
+    const size_t att_threads = 1024; // ATT_TH in layer_ops.hip
+    const size_t max_chunk = g_dev.max_lds / sizeof(float) - head_dim - 256 - 16;
+    if ((head_dim + kv_len + att_threads) * sizeof(float) + 64 > g_dev.max_lds)
+        splits = std::max(splits, (kv_len + max_chunk - 1) / max_chunk);
     if (splits > 1) {
         const size_t chunk = (kv_len + splits - 1) / splits;
         const size_t lds = (head_dim + chunk + 256) * sizeof(float);
         if (lds + 64 > g_dev.max_lds)
             return fail(REALM_BACKEND_UNSUPPORTED,
                         "attention: " + std::to_string(chunk) + " keys per split exceed the LDS");
+        if (seq_len * num_heads * splits > (size_t)UINT32_MAX)
+            return fail(REALM_INVALID_ARGUMENT, "attention: too many (token, head, split) groups");
         hipStream_t s;
         CHECK(pick_stream(stream, &s));
         void *part = nullptr;
@@ -1431,7 +1442,6 @@ REALM_API int realm_hip_attention_dev(const float *d_q, const float *d_k_cache,
         return launch("realm_attention_combine", dim3((unsigned)(seq_len * num_heads)),
                       dim3(256), 0, s, cargs);
     }
-    const size_t att_threads = 1024; // ATT_TH in layer_ops.hip
     const size_t lds = (head_dim + kv_len + att_threads) * sizeof(float);
     if (lds + 64 > g_dev.max_lds)
         return fail(REALM_BACKEND_UNSUPPORTED,
@@ -1508,6 +1518,17 @@ int check_layer(const realm_layer *L, size_t seq_len, size_t position, size_t ma
                                                  " + " + std::to_string(seq_len) + " > " +
                                                  std::to_string(max_seq_len));
     const uint64_t h[7] = {L->wq, L->wk, L->wv, L->wo, L->w_gate, L->w_up, L->w_down};
+    const uint64_t lora[7] = {L->lora_q,  L->lora_k,    L->lora_v,   L->lora_o,
+                              L->lora_gate, L->lora_up, L->lora_down};
+    bool any_lora = false;
+    for (int i = 0; i < 7; ++i)
+        any_lora = any_lora || lora[i] != 0;
+    if (any_lora && !L->d_adapter_ids)
+        return fail(REALM_INVALID_ARGUMENT,
+                    "forward_layer: adapter sets given without device adapter ids");
+    if (any_lora && seq_len > 1024)
+        return fail(REALM_INVALID_ARGUMENT,
+                    "forward_layer: calls with adapters take at most 1024 tokens");
     const size_t n[7] = {H, kv_dim, kv_dim, H, I, I, H}, k[7] = {H, H, H, H, H, H, I};
     for (int i = 0; i < 7; ++i) {
         Weight w;
@@ -1548,21 +1569,35 @@ int layer_steps(const realm_layer *L, const int type[7], const float *x, const f
                                      nullptr, normed, s));
     }
     // matrices of one format share a grouped product (GGUF quant mixes
-    // often keep V or up in Q6_K: then separate products)
-    auto products = [&](const uint64_t *hs, const int *ts, float *const *out, int n) {
-        bool same = true;
-        for (int i = 1; i < n; ++i)
+    // often keep V or up in Q6_K: then separate products); with adapter sets
+    // on every member, one grouped multi-LoRA product, on some of them, one
+    // product per projection
+    const int32_t *ids = L->d_adapter_ids;
+    auto one = [&](uint64_t hw, uint64_t set, const float *in, float *out) {
+        return set ? realm_hip_multi_lora_matmul_dev(hw, set, in, seq_len, ids, out, s)
+                   : realm_hip_weights_matmul_dev(hw, in, seq_len, out, s);
+    };
+    auto products = [&](const uint64_t *hs, const uint64_t *sets, const int *ts,
+                        float *const *out, int n) {
+        bool same = true, any = false, all = true;
+        for (int i = 0; i < n; ++i) {
             same = same && ts[i] == ts[0];
-        if (same)
+            any = any || sets[i] != 0;
+            all = all && sets[i] != 0;
+        }
+        if (same && !any)
             return realm_hip_weights_matmul_group_dev(hs, n, normed, seq_len, out, s);
+        if (same && all)
+            return realm_hip_multi_lora_matmul_group_dev(hs, sets, n, normed, seq_len, ids, out, s);
         for (int i = 0; i < n; ++i)
-            if (int rc = realm_hip_weights_matmul_dev(hs[i], normed, seq_len, out[i], s))
+            if (int rc = one(hs[i], sets[i], normed, out[i]))
                 return rc;
         return (int)REALM_OK;
     };
     const uint64_t qkv[3] = {L->wq, L->wk, L->wv};
+    const uint64_t qkv_sets[3] = {L->lora_q, L->lora_k, L->lora_v};
     float *const qkv_out[3] = {q, k_rows, v_rows};
-    CHECK(products(qkv, type, qkv_out, 3));
+    CHECK(products(qkv, qkv_sets, type, qkv_out, 3));
     { // RoPE of Q and of this call's K rows in one launch
         int iq = (int)heads, ik = (int)kvh, is = (int)seq_len, id = (int)hd, ip = (int)position;
         float theta = L->rope_theta;
@@ -1573,13 +1608,14 @@ int layer_steps(const realm_layer *L, const int type[7], const float *x, const f
     }
     CHECK(realm_hip_attention_dev(q, kc, vc, seq_len, position + seq_len, position, heads, kvh,
                                   hd, att, s));
-    CHECK(realm_hip_weights_matmul_dev(L->wo, att, seq_len, o, s));
+    CHECK(one(L->wo, L->lora_o, att, o));
     CHECK(realm_hip_rms_norm_dev(h, o, L->ffn_norm, L->rms_norm_eps, seq_len, H, h2, normed, s));
     const uint64_t gu[2] = {L->w_gate, L->w_up};
+    const uint64_t gu_sets[2] = {L->lora_gate, L->lora_up};
     float *const gu_out[2] = {gate, up};
-    CHECK(products(gu, type + 4, gu_out, 2));
+    CHECK(products(gu, gu_sets, type + 4, gu_out, 2));
     CHECK(realm_hip_swiglu_dev(gate, up, seq_len * I, gate, s));
-    return realm_hip_weights_matmul_dev(L->w_down, gate, seq_len, down, s);
+    return one(L->w_down, L->lora_down, gate, down);
 }
 
 } // namespace

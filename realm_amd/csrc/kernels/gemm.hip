@@ -647,9 +647,9 @@ REALM_DEV void adapter_tokens(const int *__restrict__ ids, int M, int a, int *to
 #define SHRINK_NS (SHRINK_KC / 32)
 template <int FMT, bool LO, int ORD, bool F16A>
 REALM_DEV void shrink_body(const _Float16 *__restrict__ xh, const _Float16 *__restrict__ xl,
-                           const float *__restrict__ tscale, const LoraEntry &e, const int *toks,
-                           int count, float *__restrict__ part, int K, int KX, int rmax,
-                           int pstride)
+                           const float *__restrict__ tscale, const void *__restrict__ x,
+                           int xbf16, const LoraEntry &e, const int *toks, int count,
+                           float *__restrict__ part, int K, int KX, int rmax, int pstride)
 {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int r16 = lane & 15, c = lane >> 4;
@@ -725,17 +725,39 @@ REALM_DEV void shrink_body(const _Float16 *__restrict__ xh, const _Float16 *__re
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
             const int tj = tc + 4 * c + v;
-            const float t = tscale[toks[tj < count ? tj : 0]];
-            // a token on the exact path (NaN scale) gets no LoRA delta: its
-            // base row is recomputed in f32 and carries the +-Inf / NaN
-            ts[v] = __builtin_isnan(t) ? 0.f : t;
+            ts[v] = tscale[toks[tj < count ? tj : 0]];
         }
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-            // D[token slot 4c+v][adapter row r16]
+            // D[token slot 4c+v][adapter row r16]; a token on the exact path
+            // (NaN scale, prepared activations zero) holds 0 in parts past
+            // the first, and the first is written below
             const int tj = tc + 4 * c + v;
-            if (tj < count && j < e.rank)
-                pk[(size_t)toks[tj] * rmax + j] = P[v] * ts[v];
+            const bool ex = __builtin_isnan(ts[v]);
+            if (tj < count && j < e.rank && !(ex && kc == 0))
+                pk[(size_t)toks[tj] * rmax + j] = ex ? 0.f : P[v] * ts[v];
+        }
+        // Tokens on the exact path (a NaN / Inf element, or max |x| outside
+        // the range the f16 split covers) get u in plain f32 from the
+        // caller's activations: whole rows, in the first part, the wave's 64
+        // lanes striding K for each of the chunk's 16 adapter rows.
+        unsigned long long exm =
+            __ballot(ti < count && __builtin_isnan(tscale[tok])) & 0xFFFFull; // slots r16
+        if (kc != 0)
+            exm = 0;
+        while (exm) { // uniform
+            const int te = toks[tc + __builtin_ctzll(exm)];
+            exm &= exm - 1;
+            for (int rr = 0; rr < 16 && jc + rr < e.rank; ++rr) {
+                float acc = 0.f;
+                for (int k = lane; k < K; k += 64)
+                    acc = fmaf(lora_elem(e.a, e.dtype, (size_t)(jc + rr) * K + k),
+                               load_x(x, xbf16, (size_t)te * K + k), acc);
+                for (int off = 32; off > 0; off >>= 1)
+                    acc += __shfl_xor(acc, off, 64);
+                if (lane == 0)
+                    pk[(size_t)te * rmax + jc + rr] = acc;
+            }
         }
     }
 }
@@ -771,11 +793,11 @@ REALM_DEV void lora_shrink(const LoraGroupArgs &g)
     if ((int)blockIdx.y * 16 >= e.rank || count == 0)
         return;
     if (e.dtype)
-        shrink_body<FMT, LO, ORD, true>(xh, xl, g.tscale, e, toks, count, part, g.K, g.KX, rmax,
-                                        pstride);
+        shrink_body<FMT, LO, ORD, true>(xh, xl, g.tscale, g.x, g.xbf16, e, toks, count, part,
+                                        g.K, g.KX, rmax, pstride);
     else
-        shrink_body<FMT, LO, ORD, false>(xh, xl, g.tscale, e, toks, count, part, g.K, g.KX, rmax,
-                                         pstride);
+        shrink_body<FMT, LO, ORD, false>(xh, xl, g.tscale, g.x, g.xbf16, e, toks, count, part,
+                                         g.K, g.KX, rmax, pstride);
 }
 
 // ------------------------------------------------------------ LoRA expand
@@ -840,11 +862,12 @@ REALM_DEV void expand_body(const float *__restrict__ u, const LoraEntry &e,
         // this wave's A fragments (u of its 16 tokens, up to 64 ranks): the
         // sum of the shrink's K parts, in part order, loads before the first
         // add; rank steps past the adapter's rank are skipped (uniform)
-        half8_t ah[EXPAND_KK], al[EXPAND_KK];
+        float us[EXPAND_KK][8];
 #pragma unroll
         for (int q2 = 0; q2 < EXPAND_KK; ++q2) {
-            ah[q2] = half8_t{};
-            al[q2] = half8_t{};
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+                us[q2][q] = 0.f;
             if (q2 >= nkk)
                 continue;
             const int j0 = 32 * (kk0 + q2) + 8 * c; // this lane's 8 ranks
@@ -869,13 +892,45 @@ REALM_DEV void expand_body(const float *__restrict__ u, const LoraEntry &e,
                 }
             }
 #pragma unroll
+            for (int q = 0; q < 8; ++q)
+                us[q2][q] = j0 + q < e.rank ? uv[q] : 0.f;
+        }
+        // u is in the activations' units (a down projection's input can
+        // reach 1e7 and more): each token slot's values of this pass are
+        // rescaled by an exact power of two 2^-eu so that their max lands in
+        // [512, 1024) before the f16 hi/lo split, as xprep does for x; the
+        // product is multiplied back by 2^eu.  The four lanes c = 0..3 of a
+        // token slot r16 hold its ranks.
+        float umax = 0.f;
+#pragma unroll
+        for (int q2 = 0; q2 < EXPAND_KK; ++q2)
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+                umax = fmaxf(umax, fabsf(us[q2][q]));
+        umax = fmaxf(umax, __shfl_xor(umax, 16, 64));
+        umax = fmaxf(umax, __shfl_xor(umax, 32, 64));
+        int eu = 0;
+        if (umax > 0.f && __builtin_isfinite(umax)) {
+            int ex;
+            frexpf(umax, &ex);
+            eu = max(ex - 10, -126); // 2^-eu and 2^eu stay normal floats
+        }
+        const float udown = ldexpf(1.f, -eu), uup = ldexpf(1.f, eu);
+        half8_t ah[EXPAND_KK], al[EXPAND_KK];
+#pragma unroll
+        for (int q2 = 0; q2 < EXPAND_KK; ++q2)
+#pragma unroll
             for (int q = 0; q < 8; ++q) {
-                const float vq = j0 + q < e.rank ? uv[q] : 0.f;
+                const float vq = us[q2][q] * udown;
                 const _Float16 h = (_Float16)vq;
                 ah[q2][q] = h;
                 al[q2][q] = (_Float16)(vq - (float)h);
             }
-        }
+        // the scale of each D token slot 4c + v (held by lane 4c + v)
+        float dup[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+            dup[v] = __shfl(uup, 4 * c + v, 64);
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
@@ -913,7 +968,7 @@ REALM_DEV void expand_body(const float *__restrict__ u, const LoraEntry &e,
             for (int v = 0; v < 4; ++v) {
                 const int tj = tc + 4 * c + v;
                 if (tj < count && row < N)
-                    y[(size_t)toks[tj] * N + row] = yv[rt][v] + e.scale * P[v];
+                    y[(size_t)toks[tj] * N + row] = yv[rt][v] + e.scale * (P[v] * dup[v]);
             }
         }
     }

@@ -29,8 +29,10 @@ struct LoraEntry {
 struct LoraGroupArgs {
     const void *xh;            // shrink: prepared activations (f16 hi)
     const void *xl;            // shrink: f16 lo part (null for bf16 input)
-    const float *tscale;       // shrink: per-token scales
+    const float *tscale;       // shrink: per-token scales (NaN: exact path)
+    const void *x;             // shrink: the caller's activations [M][K] (exact path)
     const int32_t *ids;        // adapter slot per token (-1 none)
+    int32_t xbf16;             // x is bf16 (else f32)
     int32_t M, K, KX;
     int32_t nparts;            // shrink K parts (512 positions each)
     int32_t a_start[REALM_GEMM_MAX_SEGS + 1];

@@ -301,3 +301,132 @@ def test_forward_layers_chain(backend, oracle):
             backend.release_weights(h)
         for b in bufs:
             b.close()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("which", ["all", "some"])
+def test_forward_layer_lora(backend, oracle, which):
+    """Per-tenant LoRA inside realm_hip_forward_layer_dev: adapter sets on all
+    seven projections (grouped multi-LoRA products for q/k/v and gate/up), or
+    on q, v, o and down only (per-projection products where a group is
+    mixed); tokens of three tenants, one without adapter (-1) and one past
+    the sets' size (base only); a 6-token prefill, then a 1- and a 2-token
+    decode.  Against the oracle's composition of the reference's steps with
+    each projection's product y = W x + s B (A x) (lora.rs:91-144 unmerged),
+    on every token."""
+    from realm_amd import synth
+    from realm_amd.backend import RealmLayer
+    from realm_amd.formats import GGML_Q4_K, GGML_Q6_K
+    H, heads, kvh, hd, inter, max_len = 256, 4, 2, 64, 512, 12
+    kv_dim = kvh * hd
+    cfg = {"hidden": H, "heads": heads, "kv_heads": kvh, "head_dim": hd, "eps": 1e-5,
+           "theta": 10000.0}
+    g = synth.rng(90 + (which == "some"))
+    shapes = {"wq": (H, H), "wk": (kv_dim, H), "wv": (kv_dim, H), "wo": (H, H),
+              "w_gate": (inter, H), "w_up": (inter, H), "w_down": (H, inter)}
+    types = {name: (GGML_Q6_K if name == "w_down" else GGML_Q4_K) for name in shapes}
+    blocks = {name: synth.blocks(g, types[name], n, k) for name, (n, k) in shapes.items()}
+    for b in blocks.values():
+        b["d"] = (b["d"].view(np.float16) * np.float16(40)).view(np.uint16)
+    handles = {name: backend.register_weights(types[name], blocks[name], *shapes[name])
+               for name in shapes}
+    with_lora = list(shapes) if which == "all" else ["wq", "wv", "wo", "w_down"]
+    adapters, sets, lhs = {}, {}, []
+    for name in with_lora:
+        n, k = shapes[name]
+        ads = []
+        for r in (4, 16):  # two tenants with adapters on this projection
+            a, b = synth.lora_adapter(g, r, k, n)
+            b = (b.astype(np.float32) * 20).astype(np.float16)  # deltas that matter
+            ads.append((a, b, r, 16.0))
+        hs = [backend.lora_register(a, b, r, al, k, n) for a, b, r, al in ads]
+        lhs += hs
+        adapters[name] = ads
+        sets[name] = backend.lora_set_create(hs)
+    norms = {"attn": (1 + 0.1 * g.standard_normal(H)).astype(np.float32),
+             "ffn": (1 + 0.1 * g.standard_normal(H)).astype(np.float32)}
+    dn = {key: backend.alloc(v.nbytes).upload(v) for key, v in norms.items()}
+    kc_ref = np.zeros(max_len * kv_dim, np.float32)
+    vc_ref = np.zeros(max_len * kv_dim, np.float32)
+    dkc, dvc = backend.alloc(kc_ref.nbytes), backend.alloc(vc_ref.nbytes)
+    pos = 0
+    try:
+        for seq, ids in ((6, [0, 1, -1, 1, 5, 0]), (1, [1]), (2, [0, -1])):
+            ids = np.array(ids, np.int32)
+            d_ids = backend.alloc(ids.nbytes).upload(ids)
+            layer = RealmLayer(wq=handles["wq"], wk=handles["wk"], wv=handles["wv"],
+                               wo=handles["wo"], w_gate=handles["w_gate"], w_up=handles["w_up"],
+                               w_down=handles["w_down"], attn_norm=dn["attn"].ptr,
+                               ffn_norm=dn["ffn"].ptr, hidden=H, num_heads=heads,
+                               num_kv_heads=kvh, head_dim=hd, intermediate=inter,
+                               rms_norm_eps=1e-5, rope_theta=10000.0,
+                               lora_q=sets.get("wq", 0), lora_k=sets.get("wk", 0),
+                               lora_v=sets.get("wv", 0), lora_o=sets.get("wo", 0),
+                               lora_gate=sets.get("w_gate", 0), lora_up=sets.get("w_up", 0),
+                               lora_down=sets.get("w_down", 0), d_adapter_ids=d_ids.ptr)
+
+            def matmul(name, x, m, ids=ids):
+                n, k = shapes[name]
+                x = np.ascontiguousarray(x, np.float32)
+                rc, y = oracle.candle_fused(types[name], blocks[name], x, m, n, k)
+                assert rc == 0
+                y = y.reshape(m, n)
+                if name in adapters:
+                    ad = [(a.astype(np.float32), b.astype(np.float32), r, al)
+                          for a, b, r, al in adapters[name]]
+                    y = oracle.multi_lora_delta(x, ids, ad, y.copy())
+                return y
+
+            x = g.standard_normal((seq, H)).astype(np.float32)
+            dx, dy = backend.alloc(x.nbytes).upload(x), backend.alloc(x.nbytes)
+            backend.forward_layer_dev(layer, dx.ptr, seq, pos, dkc.ptr, dvc.ptr, max_len, dy.ptr)
+            backend.synchronize()
+            got = dy.download(np.float32, x.size).reshape(seq, H)
+            want = oa.forward_layer(matmul, x, blocks, norms, cfg, kc_ref, vc_ref, pos, seq)
+            # the adapters change the output (the check has teeth)
+            base = oa.forward_layer(lambda nm, a, m: matmul(nm, a, m, ids=np.full(m, -1, np.int32)),
+                                    x, blocks, norms, cfg, kc_ref.copy(), vc_ref.copy(), pos, seq)
+            err, change = rel_l2(got, want), rel_l2(want, base)
+            print(f"forward_layer lora={which} seq={seq} rel_l2={err:.3e} lora effect={change:.3e}")
+            assert err < 1e-3, (seq, pos)
+            # the residual dilutes one token's delta at the layer output: the
+            # deltas still stand two orders of magnitude above the error
+            assert change > 1e-3 and err < change / 100, (seq, change, err)
+            pos += seq
+            for b in (dx, dy, d_ids):
+                b.close()
+    finally:
+        for s in sets.values():
+            backend.lora_set_release(s)
+        for h in lhs:
+            backend.lora_release(h)
+        for h in handles.values():
+            backend.release_weights(h)
+        for b in list(dn.values()) + [dkc, dvc]:
+            b.close()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seq,kv", [(1, 100_000), (2, 60_001)])
+def test_attention_long_cache(backend, seq, kv):
+    """Caches longer than one workgroup's LDS holds scores for (about 39 K
+    keys): the split form with enough splits that every chunk fits, against
+    the oracle (StandardAttention takes any kv_len, standard.rs:36-210)."""
+    heads, kvh, hd = 4, 2, 64
+    pos = kv - seq
+    g = np.random.default_rng(kv)
+    q = g.standard_normal(seq * heads * hd).astype(np.float32)
+    k = (0.3 * g.standard_normal(kv * kvh * hd)).astype(np.float32)
+    v = g.standard_normal(kv * kvh * hd).astype(np.float32)
+    dq, dk, dv = (backend.alloc(a.nbytes).upload(a) for a in (q, k, v))
+    do = backend.alloc(q.nbytes)
+    try:
+        backend.attention_dev(dq.ptr, dk.ptr, dv.ptr, seq, kv, pos, heads, kvh, hd, do.ptr)
+        backend.synchronize()
+        got = do.download(np.float32, q.size)
+        assert backend.last_kernel() == "realm_attention_combine"
+    finally:
+        for b in (dq, dk, dv, do):
+            b.close()
+    want = oa.attention(q, k, v, seq, kv, pos, heads, kvh, hd)
+    assert rel_l2(got, want) < 1e-5

@@ -548,6 +548,58 @@ def test_multi_lora_small(backend, oracle, t, dtype, shape):
     assert np.array_equal(got[none], base[none]) or rel_l2(got[none], base[none]) < 1e-6
 
 
+@pytest.mark.parametrize("scale", [1e-30, 1e-6, 1e6, 1e20, 1e30])
+@pytest.mark.parametrize("dtype", [np.float16, np.float32])
+def test_multi_lora_activation_range(backend, oracle, scale, dtype):
+    """u = A x takes the activations' units: at 1e6 and beyond it is far past
+    f16 range (the expand rescales it per token by a power of two before its
+    f16 split); at 1e-30 and 1e30 (with a 1e3 outlier: max |x| outside
+    [2^-60, 2^100]) the tokens take the exact f32 path, and their u comes from
+    the caller's activations in f32 — the LoRA delta is kept, as the
+    reference's y = W x + s B (A x) (lora.rs:91-144) keeps it for any finite
+    x.  Single products and a grouped one, 1, 6 and 40 tokens."""
+    g = synth.rng(77)
+    n, k = 192, 1024
+    blocks = synth.q4k_blocks(g, n, k)
+    adapters, handles = [], []
+    for r in (8, 19):
+        a, b = synth.lora_adapter(g, r, k, n)
+        a, b = a.astype(dtype), (b.astype(np.float32) * 20).astype(dtype)
+        adapters.append((a, b, r, 16.0))
+        handles.append(backend.lora_register(a, b, r, 16.0, k, n))
+    wh = backend.register_weights(GGML_Q4_K, blocks, n, k)
+    sh = backend.lora_set_create(handles)
+    try:
+        for m in (1, 6, 40):
+            x = synth.activations(g, m, k) * np.float32(scale)
+            x[:, 5] *= 1e3  # a large outlier per token
+            ids = (np.arange(m) % 3).astype(np.int32)  # slot 2: no adapter
+            ref = _oracle_lora(oracle, GGML_Q4_K, blocks, x, ids, adapters, n, k)
+            base = _oracle_lora(oracle, GGML_Q4_K, blocks, x, np.full(m, -1, np.int32),
+                                adapters, n, k)
+            assert np.isfinite(ref).all() and rel_l2(ref, base) > 1e-2  # deltas matter
+            got = backend.multi_lora_matmul(wh, sh, x, ids)
+            assert np.isfinite(got).all() and rel_l2(got, ref) < REL_TOL, (scale, m)
+            dx = backend.alloc(x.nbytes).upload(x)
+            d_ids = backend.alloc(ids.nbytes).upload(ids)
+            dys = [backend.alloc(m * n * 4) for _ in range(2)]
+            try:
+                backend.multi_lora_matmul_group_dev([wh, wh], [sh, sh], dx.ptr, m, d_ids.ptr,
+                                                    [d.ptr for d in dys])
+                backend.synchronize()
+                for d in dys:
+                    gy = d.download(np.float32, m * n).reshape(m, n)
+                    assert rel_l2(gy, ref) < REL_TOL, ("group", scale, m)
+            finally:
+                for b_ in [dx, d_ids] + dys:
+                    b_.close()
+    finally:
+        backend.lora_set_release(sh)
+        for h in handles:
+            backend.lora_release(h)
+        backend.release_weights(wh)
+
+
 @pytest.mark.parametrize("t", [GGML_Q4_K, GGML_Q6_K])
 @pytest.mark.parametrize("m", [4, 37])
 @pytest.mark.parametrize("rt", ["", "2", "4", "8"])
