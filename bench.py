@@ -257,9 +257,11 @@ def lora_overhead(be, stream: int, reps: int) -> dict:
     """Config 3: q_proj and v_proj (Q4_K 4096x4096) for 64 tokens, 16 adapters
     with ranks from {8,16,64}, Zipf(1.1) tenant ids, 10% without adapter.
     q and v share the input, so base and multi-LoRA products run as grouped
-    calls; warm: the same weights and adapters every replay; cold: 8 rotated
-    copies (base + adapters), 8 x 47 MB, so the adapters are re-read from
-    HBM; warm_per_projection: one call per projection instead."""
+    calls.  Each graph holds 8 calls, timed per call: warm, all 8 on the same
+    weights and adapters (resident in the 256 MB Infinity Cache); cold, on 8
+    rotated copies (base + adapters), 8 x 47 MB, so weights and adapters are
+    re-read from HBM; warm_per_projection: warm with one call per projection
+    instead."""
     g = synth.rng(3)
     n = k = 4096
     m = 64
@@ -302,8 +304,9 @@ def lora_overhead(be, stream: int, reps: int) -> dict:
                                      stream=stream)
 
     res = {}
-    for mode, cs, fb, fl in (("warm", [0], base, lora), ("cold", list(range(copies)), base, lora),
-                             ("warm_per_projection", [0], base1, lora1)):
+    for mode, cs, fb, fl in (("warm", [0] * copies, base, lora),
+                             ("cold", list(range(copies)), base, lora),
+                             ("warm_per_projection", [0] * copies, base1, lora1)):
         gb = capture(be, stream, lambda: [fb(c) for c in cs])
         gl = capture(be, stream, lambda: [fl(c) for c in cs])
         time_graph(be, gb, stream, 5)

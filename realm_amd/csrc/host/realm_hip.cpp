@@ -66,6 +66,7 @@ int realm_set_error(int code, const std::string &msg);
 
 using realm::GemmArgs;
 using realm::LoraEntry;
+using realm::LoraChunk;
 
 namespace {
 
@@ -473,8 +474,9 @@ struct Adapter {
     int uses = 0; // number of sets holding it
 };
 struct AdapterSet {
-    void *table = nullptr;
-    size_t count = 0, in = 0, out = 0;
+    void *table = nullptr;  // device: count LoraEntry, then the chunk list
+    void *chunks = nullptr; // device: nchunks LoraChunk (fused shrink), inside table's allocation
+    size_t count = 0, in = 0, out = 0, nchunks = 0;
     int rmax = 0;
     std::vector<uint64_t> members;
 };
@@ -691,6 +693,7 @@ GemmTile gemm_tile(const Weight &w, size_t M, bool bf16)
 struct XPrep {
     void *xh = nullptr, *xl = nullptr, *xm = nullptr, *ts = nullptr;
     size_t Mp = 0;
+    size_t rows = 0;         // token rows xprep writes (Mp, plus a zero row for the tiled kernels)
     const void *x = nullptr; // the caller's activations (read again on the exact path)
     bool bf16 = false;
 };
@@ -700,8 +703,9 @@ int fmt_code(int type) { return type == GGML_Q4_K ? 0 : type == GGML_Q6_K ? 1 : 
 // xprep limit: the kernel holds 4 rounds of 1024 x 8 positions per thread
 constexpr size_t XPREP_MAX_KX = 32768;
 
-int prep_x(const Weight &w, const void *d_x, bool bf16, size_t M, const GemmTile &tile,
-           hipStream_t s, XPrep *p)
+// The prepared-activation buffers of a batched product (no launch).
+int prep_x_alloc(const Weight &w, const void *d_x, bool bf16, size_t M, const GemmTile &tile,
+                 hipStream_t s, XPrep *p)
 {
     if (w.kx > XPREP_MAX_KX)
         return fail(REALM_INVALID_ARGUMENT,
@@ -711,6 +715,7 @@ int prep_x(const Weight &w, const void *d_x, bool bf16, size_t M, const GemmTile
     // the tiled kernels also read one all-zero token past them
     p->Mp = round_up(M, tile.toks_per_wg);
     const size_t rows = p->Mp + (tile.tiled ? 1 : 0);
+    p->rows = rows;
     size_t B = w.k / 256;
     CHECK(ws_get(s, WS_XH, rows * w.kx * 2, &p->xh));
     if (!bf16)
@@ -722,10 +727,34 @@ int prep_x(const Weight &w, const void *d_x, bool bf16, size_t M, const GemmTile
     CHECK(ws_get(s, WS_TS, rows * 4, &p->ts));
     p->x = d_x;
     p->bf16 = bf16;
-    int ibf = bf16 ? 1 : 0, iM = (int)M, iK = (int)w.k, iKX = (int)w.kx;
-    void *args[] = {(void *)&d_x, &ibf, &p->xh, &p->xl, &p->xm, &p->ts, &iM, &iK, &iKX};
-    return launch(std::string("realm_xprep_") + fmt_name(w.type) + (tile.ord ? "_o1" : ""),
-                  dim3((unsigned)rows), dim3(1024), 0, s, args);
+    return REALM_OK;
+}
+
+// The xprep launch; with L, `nshrink` workgroups past its rows run the fused
+// LoRA shrink (realm_xprep_lora_*).
+int prep_x_launch(const Weight &w, const XPrep &p, size_t M, const GemmTile &tile, hipStream_t s,
+                  const realm::LoraGroupArgs *L = nullptr, int nshrink = 0)
+{
+    const void *d_x = p.x;
+    void *xh = p.xh, *xl = p.xl, *xm = p.xm, *ts = p.ts;
+    int ibf = p.bf16 ? 1 : 0, iM = (int)M, iK = (int)w.k, iKX = (int)w.kx, irows = (int)p.rows;
+    const std::string ord = tile.ord ? "_o1" : "";
+    if (L) {
+        realm::LoraGroupArgs g = *L;
+        void *args[] = {(void *)&d_x, &ibf, &xh, &xl, &xm, &ts, &iM, &iK, &iKX, &irows, &g};
+        return launch(std::string("realm_xprep_lora_") + fmt_name(w.type) + ord,
+                      dim3((unsigned)(p.rows + (size_t)nshrink)), dim3(1024), 0, s, args);
+    }
+    void *args[] = {(void *)&d_x, &ibf, &xh, &xl, &xm, &ts, &iM, &iK, &iKX};
+    return launch(std::string("realm_xprep_") + fmt_name(w.type) + ord, dim3((unsigned)p.rows),
+                  dim3(1024), 0, s, args);
+}
+
+int prep_x(const Weight &w, const void *d_x, bool bf16, size_t M, const GemmTile &tile,
+           hipStream_t s, XPrep *p)
+{
+    CHECK(prep_x_alloc(w, d_x, bf16, M, tile, s, p));
+    return prep_x_launch(w, *p, M, tile, s);
 }
 
 // One launch of the LDS-tiled kernel over 1..4 matrices of one format and K
@@ -733,7 +762,8 @@ int prep_x(const Weight &w, const void *d_x, bool bf16, size_t M, const GemmTile
 // row tiles.  With a K split, realm_gemm_tiled_reduce then sums each tile's
 // parts in split order (deterministic) into the matrices' outputs.
 int tiled_launch(const Weight *const *w, float *const *d_y, int count, const XPrep &p, bool bf16,
-                 size_t M, const GemmTile &tile, hipStream_t s)
+                 size_t M, const GemmTile &tile, hipStream_t s,
+                 const realm::LoraGroupArgs *L = nullptr)
 {
     if (count < 1 || count > REALM_GEMM_MAX_SEGS)
         return fail(REALM_INVALID_ARGUMENT, "a tiled launch takes 1..4 matrices");
@@ -790,7 +820,8 @@ int tiled_launch(const Weight *const *w, float *const *d_y, int count, const XPr
            rt * TT * g.ksplit * tile.rows_per_wg * tile.toks_per_wg * sizeof(float) >
                t_fixed->room())
         g.ksplit /= 2;
-    if (g.ksplit > 1) {
+    // parts for a K split, and for the LoRA-fused reduce even without one
+    if (g.ksplit > 1 || L) {
         void *part = nullptr;
         CHECK(ws_get(s, WS_PART,
                      rt * TT * g.ksplit * tile.rows_per_wg * tile.toks_per_wg * sizeof(float),
@@ -812,12 +843,17 @@ int tiled_launch(const Weight *const *w, float *const *d_y, int count, const XPr
     const dim3 grid((unsigned)(8 * ((rk + xr - 1) / xr) * ((TT + xt - 1) / xt)));
     void *args[] = {&g};
     CHECK(launch(name, grid, dim3(tile.threads), 0, s, args));
-    if (g.ksplit > 1) {
+    if (g.part) {
         int grows = (int)tile.rows_per_wg, gtok = (int)tile.toks_per_wg;
-        void *rargs[] = {&g, &grows, &gtok};
-        CHECK(launch("realm_gemm_tiled_reduce",
-                     dim3((unsigned)(rt * TT), (unsigned)((grows * gtok + 255) / 256)), dim3(256),
-                     0, s, rargs));
+        const dim3 rgrid((unsigned)(rt * TT), (unsigned)((grows * gtok + 255) / 256));
+        if (L) {
+            realm::LoraGroupArgs lg = *L;
+            void *rargs[] = {&g, &grows, &gtok, &lg};
+            CHECK(launch("realm_gemm_tiled_reduce_lora", rgrid, dim3(256), 0, s, rargs));
+        } else {
+            void *rargs[] = {&g, &grows, &gtok};
+            CHECK(launch("realm_gemm_tiled_reduce", rgrid, dim3(256), 0, s, rargs));
+        }
     }
     return REALM_OK;
 }
@@ -946,6 +982,67 @@ int lora_expand_launch(const Weight *const *w, const LoraCall *lc, int count, co
                   dim3(256), 0, s, args);
 }
 
+// Small-batch multi-LoRA with the shrink folded into the xprep launch and
+// the expand into the K-split reduce (gemm.hip lora_shrink_fused,
+// gemm_tiled.hip realm_gemm_tiled_reduce_lora): the three launches of a
+// base call.  Taken for f32 activations (16-byte aligned) of at most
+// LORA_FUSED_MAX_M tokens on the tiled kernels, ranks up to LORA_FUSED_RMAX;
+// otherwise (and with REALM_LORA_FUSED=0, for comparison) the separate
+// shrink and expand launches.
+constexpr size_t LORA_FUSED_MAX_WGS = 65536;
+
+bool lora_fused_ok(const GemmTile &tile, size_t M, bool bf16, const Weight &w0, const void *d_x,
+                   const LoraCall *lc, int count)
+{
+    if (const char *env = getenv("REALM_LORA_FUSED"))
+        if (env[0] == '0')
+            return false;
+    // the fused reduce: a workgroup's 256 elements span at most 3 tokens
+    if (!tile.tiled || bf16 || M > LORA_FUSED_MAX_M || tile.rows_per_wg < 128 ||
+        ((uintptr_t)d_x & 15) != 0)
+        return false;
+    const size_t np = (w0.k + LORA_FUSED_KP - 1) / LORA_FUSED_KP;
+    size_t wgs = 0;
+    for (int i = 0; i < count; ++i) {
+        if (lc[i].set->rmax > LORA_FUSED_RMAX)
+            return false;
+        wgs += lc[i].set->nchunks * np;
+    }
+    return wgs <= LORA_FUSED_MAX_WGS;
+}
+
+int lora_fused_run(const Weight *const *w, const LoraCall *lc, int count, const void *d_x,
+                   size_t M, const GemmTile &tile, float *const *d_y, hipStream_t s)
+{
+    XPrep p;
+    CHECK(prep_x_alloc(*w[0], d_x, false, M, tile, s, &p));
+    const int np = (int)((w[0]->k + LORA_FUSED_KP - 1) / LORA_FUSED_KP);
+    size_t uoff[REALM_GEMM_MAX_SEGS], ubytes = 0;
+    for (int i = 0; i < count; ++i) {
+        uoff[i] = ubytes;
+        ubytes += align256((size_t)np * p.Mp * round_up(lc[i].set->rmax, 8) * sizeof(float));
+    }
+    void *u = nullptr;
+    CHECK(ws_get(s, WS_U, ubytes, &u));
+    void *us[REALM_GEMM_MAX_SEGS];
+    for (int i = 0; i < count; ++i)
+        us[i] = (uint8_t *)u + uoff[i];
+    realm::LoraGroupArgs L = lora_group_args(w, lc, count, p, M, us, d_y);
+    L.nparts = np;
+    int wgs = 0;
+    for (int i = 0; i < count; ++i) {
+        const AdapterSet &set = *lc[i].set;
+        L.pstride[i] = (int)(p.Mp * round_up(set.rmax, 8));
+        L.chunks[i] = (const realm::LoraChunk *)set.chunks;
+        L.wg_start[i] = wgs;
+        wgs += (int)set.nchunks * np;
+    }
+    for (int i = count; i <= REALM_GEMM_MAX_SEGS; ++i)
+        L.wg_start[i] = i == count ? wgs : INT32_MAX;
+    CHECK(prep_x_launch(*w[0], p, M, tile, s, &L, wgs));
+    return tiled_launch(w, d_y, count, p, false, M, tile, s, &L);
+}
+
 int gemm_launch(const Weight &w, const XPrep &p, bool bf16, size_t M, const GemmTile &tile,
                 float *d_y, hipStream_t s, const LoraCall *lora)
 {
@@ -1000,6 +1097,10 @@ int run_gemm(const Weight &w, const void *d_x, bool bf16, size_t M, float *d_y, 
     if (M == 0 || w.n == 0)
         return REALM_OK;
     const GemmTile tile = gemm_tile(w, M, bf16);
+    if (lora && lora_fused_ok(tile, M, bf16, w, d_x, lora, 1)) {
+        const Weight *wp = &w;
+        return lora_fused_run(&wp, lora, 1, d_x, M, tile, &d_y, s);
+    }
     XPrep p;
     CHECK(prep_x(w, d_x, bf16, M, tile, s, &p));
     return gemm_launch(w, p, bf16, M, tile, d_y, s, lora);
@@ -2178,12 +2279,31 @@ REALM_API int realm_hip_lora_set_create(const uint64_t *lora_handles, size_t cou
     }
     set.count = count;
     set.members.assign(lora_handles, lora_handles + count);
+    // the 16-row chunks of every adapter's A, for the fused shrink
+    std::vector<LoraChunk> chunks;
+    for (size_t i = 0; i < count; ++i)
+        for (int rc = 0; rc * 16 < table[i].rank; ++rc) {
+            LoraChunk c;
+            std::memset(&c, 0, sizeof c);
+            c.e = table[i];
+            c.a = (int32_t)i;
+            c.rc = rc;
+            chunks.push_back(c);
+        }
+    set.nchunks = chunks.size();
+    const size_t tbytes = align256(count * sizeof(LoraEntry));
     int rc = REALM_OK;
-    if (hipMalloc(&set.table, count * sizeof(LoraEntry)) != hipSuccess)
+    if (hipMalloc(&set.table, tbytes + chunks.size() * sizeof(LoraChunk)) != hipSuccess) {
+        set.table = nullptr;
         rc = fail(REALM_OUT_OF_MEMORY, "hipMalloc of adapter table failed");
-    else if (hipMemcpy(set.table, table.data(), count * sizeof(LoraEntry),
-                       hipMemcpyHostToDevice) != hipSuccess)
-        rc = fail(REALM_GENERIC_FAILURE, "upload of adapter table failed");
+    } else {
+        set.chunks = (uint8_t *)set.table + tbytes;
+        if (hipMemcpy(set.table, table.data(), count * sizeof(LoraEntry),
+                      hipMemcpyHostToDevice) != hipSuccess ||
+            hipMemcpy(set.chunks, chunks.data(), chunks.size() * sizeof(LoraChunk),
+                      hipMemcpyHostToDevice) != hipSuccess)
+            rc = fail(REALM_GENERIC_FAILURE, "upload of adapter table failed");
+    }
     std::lock_guard<std::mutex> lk(g_mu);
     if (rc != REALM_OK) {
         if (set.table)
@@ -2283,11 +2403,17 @@ REALM_API int realm_hip_multi_lora_matmul_group_dev(const uint64_t *weight_handl
         all.bytes = std::max(all.bytes, w[i].bytes);
     }
     const GemmTile tile = gemm_tile(all, batch, false);
-    XPrep p;
-    CHECK(prep_x(w[0], d_input, false, batch, tile, s, &p));
     LoraCall lc[REALM_GEMM_MAX_SEGS];
     for (size_t i = 0; i < count; ++i)
         lc[i] = LoraCall{&set[i], d_adapter_ids};
+    if (lora_fused_ok(tile, batch, false, w[0], d_input, lc, (int)count)) {
+        const Weight *wp[REALM_GEMM_MAX_SEGS];
+        for (size_t i = 0; i < count; ++i)
+            wp[i] = &w[i];
+        return lora_fused_run(wp, lc, (int)count, d_input, batch, tile, d_outs, s);
+    }
+    XPrep p;
+    CHECK(prep_x(w[0], d_input, false, batch, tile, s, &p));
     if (!tile.tiled) { // per matrix: shrink, base product, expand
         for (size_t i = 0; i < count; ++i)
             CHECK(gemm_launch(w[i], p, false, batch, tile, d_outs[i], s, &lc[i]));

@@ -201,14 +201,8 @@ DEF_XPREP(q80, FMT_Q80)
 // --------------------------------------------------------- LoRA adapter table
 
 // Adapter factors are device allocations reached through pointers read from
-// the adapter table: cast to the global address space so that their loads
-// are global loads (a flat load also counts against the LDS/scalar counter
-// and makes every LDS wait wait for it too).
-typedef __attribute__((address_space(1))) const _Float16 gf16_t;
-typedef __attribute__((address_space(1))) const float gf32_t;
-typedef __attribute__((address_space(1))) const uint4 gu4_t;
-typedef __attribute__((address_space(1))) const uint2 gu2_t;
-typedef __attribute__((address_space(1))) const float4 gf4_t;
+// the adapter table: their loads go through the global address-space types
+// of mfma_common.h (gf16_t, gf32_t, gu4_t, gu2_t, gf4_t).
 
 REALM_DEV float lora_elem(const void *p, int dtype, size_t i)
 {
@@ -799,6 +793,216 @@ REALM_DEV void lora_shrink(const LoraGroupArgs &g)
         shrink_body<FMT, LO, ORD, false>(xh, xl, g.tscale, g.x, g.xbf16, e, toks, count, part,
                                          g.K, g.KX, rmax, pstride);
 }
+
+// ------------------------------------------------- fused LoRA shrink
+//
+// Small batches (the tiled base product with its K-split reduce): the shrink
+// u = A_a x runs in workgroups of the xprep launch past its token rows, so a
+// multi-LoRA call has the launches of a base call.  It cannot use xprep's
+// fragments (written by the same launch) and reads the caller's activations
+// instead (f32: the multi-LoRA calls take f32 activations), in natural k
+// order, split into bf16 terms: x = b1 + b2 + b3 exactly (8 + 8 + 8
+// significand bits), A = a1 + a2
+// exactly for f16 factors (11 bits), a1 + a2 + a3 for f32 ones.  bf16 has
+// f32's exponent range, so no scale is needed at any magnitude; the MFMAs
+// take the terms of the products down to 2^-16 of the leading one (the ones
+// left out are below 2^-24 of it) and accumulate in f32.  NaN and Inf
+// elements give a NaN u, as f32 arithmetic would on the same row.
+//
+// Workgroup (projection, adapter slot, 16-row chunk of A, K part of
+// LORA_FUSED_KP positions); its 16 waves share the part's 32-position steps
+// (wave w: steps w, w + 16, ...) for each 16 of the adapter's tokens and sum
+// through LDS:  u[part][t][j] for the adapter's tokens t and rows j < rank.
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+
+REALM_DEV floatx4 mfma_bf(bf16x8_t a, bf16x8_t b, floatx4 c)
+{
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// v = t1 + t2 (+ t3) in bf16, each term the rounding of what the ones
+// before it leave (a non-finite leading term leaves 0)
+template <int NT>
+REALM_DEV void bf_split(const float (&v)[8], bf16x8_t &t1, bf16x8_t &t2, bf16x8_t &t3)
+{
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const __bf16 h1 = (__bf16)v[i];
+        const float r1 = __builtin_isfinite((float)h1) ? v[i] - (float)h1 : 0.f;
+        t1[i] = h1;
+        if (NT >= 2) {
+            const __bf16 h2 = (__bf16)r1;
+            t2[i] = h2;
+            if (NT >= 3)
+                t3[i] = (__bf16)(r1 - (float)h2);
+        }
+    }
+}
+
+#define FS_SW (LORA_FUSED_KP / 32 / 16) // steps per wave and part
+
+// One workgroup's chunk: adapter slot a (entry e), rows jc .. jc + 15, K
+// positions k0 .. k1 - 1.  idv is ids[threadIdx.x] (-1 past the batch).
+template <bool F16A>
+REALM_DEV void shrink_fused_body(const float *__restrict__ x, int K, const LoraEntry &e, int a,
+                                 int idv, float *__restrict__ pk, int jc, int k0, int k1,
+                                 int rmax, int *toks, int *wsum, float (*red)[256])
+{
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int r16 = lane & 15, c = lane >> 4;
+    const int jr = min(jc + r16, e.rank - 1); // rows past the rank are never stored
+    // A fragments: their loads go out first (they do not depend on the
+    // tokens) and stay in flight across the token compaction
+    uint4 ar[FS_SW][F16A ? 1 : 2];
+#pragma unroll
+    for (int i = 0; i < FS_SW; ++i) {
+        const int k = k0 + 32 * (wave + 16 * i) + 8 * c;
+        const int kk = k < k1 ? k : k0; // a valid address; the values are zeroed
+        if (F16A) {
+            ar[i][0] = *(gu4_t *)((gf16_t *)e.a + (size_t)jr * K + kk);
+        } else {
+            gf32_t *src = (gf32_t *)e.a + (size_t)jr * K + kk;
+            ar[i][0] = __builtin_bit_cast(uint4, *(gf4_t *)src);
+            ar[i][F16A ? 0 : 1] = __builtin_bit_cast(uint4, *(gf4_t *)(src + 4));
+        }
+    }
+    // the adapter's tokens in token order (the batch fits one round: at most
+    // LORA_FUSED_MAX_M tokens); LDS-only barriers leave the loads in flight
+    const bool hit = idv == a;
+    const unsigned long long m = __ballot(hit);
+    if (lane == 0)
+        wsum[wave] = __popcll(m);
+    lds_barrier();
+    int before = 0, count = 0;
+#pragma unroll
+    for (int w = 0; w < XPREP_TH / 64; ++w) {
+        const int ws = wsum[w];
+        before += w < wave ? ws : 0;
+        count += ws;
+    }
+    if (hit)
+        toks[before + __popcll(m & ((1ull << lane) - 1ull))] = threadIdx.x;
+    lds_barrier();
+    if (count == 0) // uniform
+        return;
+    constexpr int NA = F16A ? 2 : 3;
+    bf16x8_t a1[FS_SW], a2[FS_SW], a3[FS_SW];
+#pragma unroll
+    for (int i = 0; i < FS_SW; ++i) {
+        const bool live = k0 + 32 * (wave + 16 * i) + 8 * c < k1;
+        float v[8];
+        if (F16A) {
+            const half8_t hv = __builtin_bit_cast(half8_t, ar[i][0]);
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+                v[q] = live ? (float)hv[q] : 0.f;
+        } else {
+            const float4 f0 = __builtin_bit_cast(float4, ar[i][0]);
+            const float4 f1 = __builtin_bit_cast(float4, ar[i][F16A ? 0 : 1]);
+            const float w[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+                v[q] = live ? w[q] : 0.f;
+        }
+        bf_split<NA>(v, a1[i], a2[i], a3[i]);
+    }
+    for (int tc = 0; tc < count; tc += 16) {
+        const int ti = tc + r16;
+        const int tok = toks[ti < count ? ti : 0];
+        float xv[FS_SW][8];
+#pragma unroll
+        for (int i = 0; i < FS_SW; ++i) {
+            const int k = k0 + 32 * (wave + 16 * i) + 8 * c;
+            const bool live = k < k1;
+            const size_t at = (size_t)tok * K + (live ? k : k0);
+            const float4 f0 = *reinterpret_cast<const float4 *>(x + at);
+            const float4 f1 = *reinterpret_cast<const float4 *>(x + at + 4);
+            xv[i][0] = f0.x; xv[i][1] = f0.y; xv[i][2] = f0.z; xv[i][3] = f0.w;
+            xv[i][4] = f1.x; xv[i][5] = f1.y; xv[i][6] = f1.z; xv[i][7] = f1.w;
+            if (!live)
+#pragma unroll
+                for (int q = 0; q < 8; ++q)
+                    xv[i][q] = 0.f;
+        }
+        floatx4 P = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < FS_SW; ++i) {
+            bf16x8_t b1, b2, b3;
+            bf_split<3>(xv[i], b1, b2, b3);
+            P = mfma_bf(b1, a1[i], P);
+            P = mfma_bf(b1, a2[i], P);
+            if (!F16A)
+                P = mfma_bf(b1, a3[i], P);
+            P = mfma_bf(b2, a1[i], P);
+            P = mfma_bf(b2, a2[i], P);
+            P = mfma_bf(b3, a1[i], P);
+        }
+        // D[token slot 4c + v][row r16] of every wave, summed over the waves
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+            red[wave][4 * lane + v] = P[v];
+        lds_barrier();
+        if (threadIdx.x < 256) {
+            float sum = 0.f;
+#pragma unroll
+            for (int w = 0; w < 16; ++w)
+                sum += red[w][threadIdx.x];
+            const int ln = threadIdx.x >> 2, v = threadIdx.x & 3;
+            const int tj = tc + 4 * (ln >> 4) + v, row = jc + (ln & 15);
+            if (tj < count && row < e.rank)
+                pk[(size_t)toks[tj] * rmax + row] = sum;
+        }
+        lds_barrier();
+    }
+}
+
+// Shrink workgroup wg (0-based past the xprep rows) of a fused launch.
+REALM_DEV void lora_shrink_fused(const LoraGroupArgs &g, int wg)
+{
+    __shared__ int toks[LORA_FUSED_MAX_M];
+    __shared__ int wsum[XPREP_TH / 64];
+    __shared__ float red[16][256];
+    // the token ids and the chunk entry: two independent loads
+    const int idv = (int)threadIdx.x < g.M ? g.ids[threadIdx.x] : -1;
+    const int p = (wg >= g.wg_start[1] ? 1 : 0) + (wg >= g.wg_start[2] ? 1 : 0) +
+                  (wg >= g.wg_start[3] ? 1 : 0);
+    const int local = wg - lora_pick(g.wg_start, p);
+    const int ci = local / g.nparts, kp = local - ci * g.nparts;
+    const LoraChunk ch = lora_pick(g.chunks, p)[ci];
+    const int rmax = lora_pick(g.rmax, p);
+    float *pk = lora_pick(g.u, p) + (size_t)kp * lora_pick(g.pstride, p);
+    const int k0 = kp * LORA_FUSED_KP, k1 = min(g.K, k0 + LORA_FUSED_KP);
+    const float *x = (const float *)g.x;
+    if (ch.e.dtype)
+        shrink_fused_body<true>(x, g.K, ch.e, ch.a, idv, pk, 16 * ch.rc, k0, k1, rmax, toks, wsum,
+                                red);
+    else
+        shrink_fused_body<false>(x, g.K, ch.e, ch.a, idv, pk, 16 * ch.rc, k0, k1, rmax, toks, wsum,
+                                 red);
+}
+
+// xprep for rows 0 .. rows - 1, the fused shrink past them
+#define DEF_XPREP_LORA(NAME, FMT)                                                          \
+    extern "C" __global__ __launch_bounds__(XPREP_TH) void realm_xprep_lora_##NAME(       \
+        const void *x, int bf16, _Float16 *xh, _Float16 *xl, _Float16 *xm, float *tscale, \
+        int M, int K, int KX, int rows, LoraGroupArgs g)                                   \
+    {                                                                                      \
+        if ((int)blockIdx.x < rows)                                                        \
+            xprep<FMT, 0>(x, bf16, xh, xl, xm, tscale, M, K, KX);                          \
+        else                                                                               \
+            lora_shrink_fused(g, (int)blockIdx.x - rows);                                  \
+    }                                                                                      \
+    extern "C" __global__ __launch_bounds__(XPREP_TH) void realm_xprep_lora_##NAME##_o1(  \
+        const void *x, int bf16, _Float16 *xh, _Float16 *xl, _Float16 *xm, float *tscale, \
+        int M, int K, int KX, int rows, LoraGroupArgs g)                                   \
+    {                                                                                      \
+        if ((int)blockIdx.x < rows)                                                        \
+            xprep<FMT, 1>(x, bf16, xh, xl, xm, tscale, M, K, KX);                          \
+        else                                                                               \
+            lora_shrink_fused(g, (int)blockIdx.x - rows);                                  \
+    }
+DEF_XPREP_LORA(q4k, FMT_Q4K)
+DEF_XPREP_LORA(q6k, FMT_Q6K)
 
 // ------------------------------------------------------------ LoRA expand
 //

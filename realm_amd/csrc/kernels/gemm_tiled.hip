@@ -645,9 +645,10 @@ REALM_DEV void gemm_tiled(const GemmArgs &g)
         return wt * TM * TOK + (PACK ? 16 * bb + (slot >> 1) : 32 * bb + slot);
     };
     const int rl0 = wr * TN * 32 + r32; // + 32a
-    if (KS > 1) {
-        // this split's part of the tile; realm_gemm_tiled_reduce adds the
-        // parts in split order
+    if (g.part) {
+        // this split's part of the tile (a K split, or one part when the
+        // reduce also adds LoRA deltas); realm_gemm_tiled_reduce(_lora) adds
+        // the parts in split order
         constexpr int TILE = GROWS * GTOK;
         float *pt = g.part + ((size_t)(rt * TT + tt) * KS + kc) * TILE;
 #pragma unroll
@@ -713,38 +714,177 @@ GEMM_TILED_SET(q6kw, FMT_Q6K, true)
 // are deterministic).  Workgroup (tile, chunk): 256 of the tile's
 // grows x gtok values; tile = row tile x token tiles + token tile, and the
 // row tile's segment names the output matrix.
-extern "C" __global__ __launch_bounds__(256) void realm_gemm_tiled_reduce(GemmArgs g, int grows,
-                                                                          int gtok)
+// Element e of tile `tile`: its segment (output matrix), row and token.
+struct ReduceSite {
+    int seg, N, row, tok, tl, rt, tt;
+    float *y;
+};
+REALM_DEV ReduceSite reduce_site(const GemmArgs &g, int grows, int gtok, int tile, int e)
 {
-    const int TT = (g.M + gtok - 1) / gtok, tile = blockIdx.x;
-    const int rt = tile / TT, tt = tile - rt * TT;
-    const int e = blockIdx.y * 256 + threadIdx.x, TILE = grows * gtok;
-    if (e >= TILE)
-        return;
-    const int seg = (rt >= g.seg_tile[1]) + (rt >= g.seg_tile[2]) + (rt >= g.seg_tile[3]);
+    ReduceSite r;
+    const int TT = (g.M + gtok - 1) / gtok;
+    r.rt = tile / TT;
+    r.tt = tile - r.rt * TT;
+    r.seg = (r.rt >= g.seg_tile[1]) + (r.rt >= g.seg_tile[2]) + (r.rt >= g.seg_tile[3]);
     auto pick = [&](auto a0, auto a1, auto a2, auto a3) {
-        return seg == 0 ? a0 : seg == 1 ? a1 : seg == 2 ? a2 : a3;
+        return r.seg == 0 ? a0 : r.seg == 1 ? a1 : r.seg == 2 ? a2 : a3;
     };
-    const int N = pick(g.seg_n[0], g.seg_n[1], g.seg_n[2], g.seg_n[3]);
-    float *const y = pick(g.seg_y[0], g.seg_y[1], g.seg_y[2], g.seg_y[3]);
-    const int rtl = rt - pick(g.seg_tile[0], g.seg_tile[1], g.seg_tile[2], g.seg_tile[3]);
-    const int tl = e / grows, rl = e - tl * grows;
-    const int row = rtl * grows + rl, tok = tt * gtok + tl;
-    if (row >= N || tok >= g.M)
-        return;
+    r.N = pick(g.seg_n[0], g.seg_n[1], g.seg_n[2], g.seg_n[3]);
+    r.y = pick(g.seg_y[0], g.seg_y[1], g.seg_y[2], g.seg_y[3]);
+    const int rtl = r.rt - pick(g.seg_tile[0], g.seg_tile[1], g.seg_tile[2], g.seg_tile[3]);
+    r.tl = e / grows;
+    r.row = rtl * grows + (e - r.tl * grows);
+    r.tok = r.tt * gtok + r.tl;
+    return r;
+}
+
+// The base product of one element: the parts in split order, or the exact
+// f32 dot product for a token xprep flagged.
+REALM_DEV float reduce_base(const GemmArgs &g, const ReduceSite &r, int tile, int e, int TILE)
+{
     const float *p = g.part + (size_t)tile * g.ksplit * TILE + e;
     float sum = p[0];
     for (int c = 1; c < g.ksplit; ++c)
         sum += p[(size_t)c * TILE];
-    if (__builtin_expect(__builtin_isnan(g.tscale[tok]), 0)) { // flagged by xprep
+    if (__builtin_expect(__builtin_isnan(g.tscale[r.tok]), 0)) { // flagged by xprep
+        auto pick = [&](auto a0, auto a1, auto a2, auto a3) {
+            return r.seg == 0 ? a0 : r.seg == 1 ? a1 : r.seg == 2 ? a2 : a3;
+        };
         const void *w0 = pick(g.seg_w0[0], g.seg_w0[1], g.seg_w0[2], g.seg_w0[3]);
         const void *w1 = pick(g.seg_w1[0], g.seg_w1[1], g.seg_w1[2], g.seg_w1[3]);
         const void *w2 = pick(g.seg_w2[0], g.seg_w2[1], g.seg_w2[2], g.seg_w2[3]);
-        const uint8_t *x = (const uint8_t *)g.x + (size_t)tok * g.K * (g.xbf16 ? 2 : 4);
+        const uint8_t *x = (const uint8_t *)g.x + (size_t)r.tok * g.K * (g.xbf16 ? 2 : 4);
         // the reduce serves Q4_K and Q6_K launches: the format from the layout
         sum = g.fmt == FMT_Q4K
-                  ? exact_dot<FMT_Q4K>(w0, w1, w2, row, g.K, g.KX, x, g.xbf16, g.nan_fb, 0, 1)
-                  : exact_dot<FMT_Q6K>(w0, w1, w2, row, g.K, g.KX, x, g.xbf16, g.nan_fb, 0, 1);
+                  ? exact_dot<FMT_Q4K>(w0, w1, w2, r.row, g.K, g.KX, x, g.xbf16, g.nan_fb, 0, 1)
+                  : exact_dot<FMT_Q6K>(w0, w1, w2, r.row, g.K, g.KX, x, g.xbf16, g.nan_fb, 0, 1);
     }
-    y[(size_t)tok * N + row] = sum;
+    return sum;
+}
+
+extern "C" __global__ __launch_bounds__(256) void realm_gemm_tiled_reduce(GemmArgs g, int grows,
+                                                                          int gtok)
+{
+    const int tile = blockIdx.x, e = blockIdx.y * 256 + threadIdx.x, TILE = grows * gtok;
+    if (e >= TILE)
+        return;
+    const ReduceSite r = reduce_site(g, grows, gtok, tile, e);
+    if (r.row >= r.N || r.tok >= g.M)
+        return;
+    r.y[(size_t)r.tok * r.N + r.row] = reduce_base(g, r, tile, e, TILE);
+}
+
+// The same, plus the multi-LoRA delta of the fused small-batch path:
+//   y[t][n] = base + scale_a * sum_j u[t][j] B_a[n][j],  a = ids[t]
+// (no delta for a = -1 or a slot past the projection's set), with u the sum
+// of the fused shrink's parts.  A workgroup's 256 elements cover at most 3
+// tokens (tiles have at least 128 rows); their u rows are summed into LDS,
+// and each element takes its row of B_a in f32 FMAs.  Every global load (the
+// base product's parts, the ids, the table entries, u and the first 256
+// bytes of the B row) is issued before the one LDS barrier.  (An MFMA form,
+// B staged once per tile and adapter, ran slower: its 125 KB of LDS left one
+// 4-wave workgroup per CU and nothing to hide its dependent loads and
+// barriers behind.)
+extern "C" __global__ __launch_bounds__(256) void realm_gemm_tiled_reduce_lora(GemmArgs g,
+                                                                               int grows, int gtok,
+                                                                               LoraGroupArgs L)
+{
+    __shared__ float us[3][LORA_FUSED_RMAX];
+    const int tile = blockIdx.x, e = blockIdx.y * 256 + threadIdx.x, TILE = grows * gtok;
+    const ReduceSite r = reduce_site(g, grows, gtok, tile, e);
+    const bool live = e < TILE && r.row < r.N && r.tok < g.M;
+    auto lpick = [&](auto a0, auto a1, auto a2, auto a3) {
+        return r.seg == 0 ? a0 : r.seg == 1 ? a1 : r.seg == 2 ? a2 : a3;
+    };
+    const LoraEntry *table = lpick(L.table[0], L.table[1], L.table[2], L.table[3]);
+    const float *u = lpick(L.u[0], L.u[1], L.u[2], L.u[3]);
+    const int rmax = lpick(L.rmax[0], L.rmax[1], L.rmax[2], L.rmax[3]);
+    const int pstride = lpick(L.pstride[0], L.pstride[1], L.pstride[2], L.pstride[3]);
+    const int nad = lpick(L.a_start[1], L.a_start[2], L.a_start[3], L.a_start[4]) -
+                    lpick(L.a_start[0], L.a_start[1], L.a_start[2], L.a_start[3]);
+    // the base product's parts
+    float sum = 0.f;
+    if (live) {
+        const float *pp = g.part + (size_t)tile * g.ksplit * TILE + e;
+        sum = pp[0];
+        for (int c = 1; c < g.ksplit; ++c)
+            sum += pp[(size_t)c * TILE];
+    }
+    // this element's adapter and its B row: up to 256 bytes in registers
+    // when the row is 16-byte aligned (f16: ranks to 128, f32: to 64)
+    const int a = live ? L.ids[r.tok] : -1;
+    const bool has = a >= 0 && a < nad;
+    LoraEntry en = {};
+    uint4 braw[16];
+    int nb = 0;
+    if (has) {
+        en = table[a];
+        const size_t esz = en.dtype ? 2 : 4, rowbytes = (size_t)en.rank * esz;
+        const uint8_t *bp = (const uint8_t *)en.b + (size_t)r.row * rowbytes;
+        if ((rowbytes & 15) == 0 && ((uintptr_t)bp & 15) == 0)
+            nb = (int)min(rowbytes >> 4, (size_t)16);
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            if (i < nb)
+                braw[i] = ((gu4_t *)bp)[i];
+    }
+    // the u rows of the workgroup's tokens: tile-local tl0 .. tl0 + 2
+    const int tl0 = (int)(blockIdx.y * 256) / grows;
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+        const int tq = r.tt * gtok + tl0 + q;
+        const int aq = tl0 + q < gtok && tq < g.M ? L.ids[tq] : -1;
+        if (aq < 0 || aq >= nad)
+            continue;
+        const int rank = table[aq].rank;
+        for (int j = threadIdx.x; j < rank; j += 256) {
+            const float *up = u + (size_t)tq * rmax + j;
+            float s = up[0];
+            for (int c = 1; c < L.nparts; ++c)
+                s += up[(size_t)c * pstride];
+            us[q][j] = s;
+        }
+    }
+    lds_barrier();
+    if (!live)
+        return;
+    if (__builtin_expect(__builtin_isnan(g.tscale[r.tok]), 0)) // flagged by xprep
+        sum = reduce_base(g, r, tile, e, TILE);
+    if (has) {
+        const float *uq = us[r.tl - tl0];
+        float d = 0.f;
+        if (en.dtype) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+                if (i < nb) {
+                    const half8_t h = __builtin_bit_cast(half8_t, braw[i]);
+#pragma unroll
+                    for (int q = 0; q < 8; ++q)
+                        d = fmaf(uq[8 * i + q], (float)h[q], d);
+                }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+                if (i < nb) {
+                    const float4 f = __builtin_bit_cast(float4, braw[i]);
+                    d = fmaf(uq[4 * i], f.x, d);
+                    d = fmaf(uq[4 * i + 1], f.y, d);
+                    d = fmaf(uq[4 * i + 2], f.z, d);
+                    d = fmaf(uq[4 * i + 3], f.w, d);
+                }
+        }
+        // the rest of the row (unaligned rows, f32 ranks past 64)
+        int j = nb * (en.dtype ? 8 : 4);
+        if (en.dtype) {
+            gf16_t *bp = (gf16_t *)en.b + (size_t)r.row * en.rank;
+            for (; j < en.rank; ++j)
+                d = fmaf(uq[j], (float)bp[j], d);
+        } else {
+            gf32_t *bp = (gf32_t *)en.b + (size_t)r.row * en.rank;
+            for (; j < en.rank; ++j)
+                d = fmaf(uq[j], bp[j], d);
+        }
+        sum += en.scale * d;
+    }
+    r.y[(size_t)r.tok * r.N + r.row] = sum;
 }

@@ -19,6 +19,15 @@ struct LoraEntry {
     int32_t pad;
 };
 
+// One 16-row chunk of one adapter's A (the fused shrink's unit of work):
+// the set lists the chunks that exist (rc * 16 < rank), with their entry.
+struct LoraChunk {
+    LoraEntry e;
+    int32_t a;  // adapter slot
+    int32_t rc; // rows 16 rc .. 16 rc + 15
+    int32_t pad[2];
+};
+
 #define REALM_GEMM_MAX_SEGS 4
 
 // Arguments of the LoRA shrink and expand kernels: one launch covers up to
@@ -34,8 +43,13 @@ struct LoraGroupArgs {
     const int32_t *ids;        // adapter slot per token (-1 none)
     int32_t xbf16;             // x is bf16 (else f32)
     int32_t M, K, KX;
-    int32_t nparts;            // shrink K parts (512 positions each)
+    int32_t nparts;            // shrink K parts (512 positions each; fused: LORA_FUSED_KP)
     int32_t a_start[REALM_GEMM_MAX_SEGS + 1];
+    // fused shrink (workgroups of the xprep launch past its token rows):
+    // projection p owns shrink workgroups wg_start[p] .. wg_start[p + 1] - 1,
+    // one per (entry of its set's chunk list, K part)
+    int32_t wg_start[REALM_GEMM_MAX_SEGS + 1];
+    const LoraChunk *chunks[REALM_GEMM_MAX_SEGS];
     const LoraEntry *table[REALM_GEMM_MAX_SEGS];
     float *u[REALM_GEMM_MAX_SEGS];        // shrink output [part][token][rmax]
     float *y[REALM_GEMM_MAX_SEGS];        // expand: outputs [M][N] (hold the base product)
@@ -43,6 +57,12 @@ struct LoraGroupArgs {
     int32_t rmax[REALM_GEMM_MAX_SEGS];    // largest rank of the set, rounded up to 8
     int32_t pstride[REALM_GEMM_MAX_SEGS]; // floats per part of u
 };
+
+// K positions per part of the fused shrink (the expand, folded into the
+// K-split reduce, adds the parts in order); ranks up to LORA_FUSED_RMAX.
+#define LORA_FUSED_KP 2048
+#define LORA_FUSED_RMAX 128
+#define LORA_FUSED_MAX_M 64 // tokens per call
 
 // Arguments of the realm_gemm_* kernels.
 struct GemmArgs {

@@ -73,6 +73,16 @@ REALM_DEV half2_t splat2(float v)
     return r;
 }
 
+// Pointers read from device tables (adapter factors): cast to the global
+// address space so that their loads are global loads (a flat load also
+// counts against the LDS/scalar counter and makes every LDS wait wait for it
+// too).
+typedef __attribute__((address_space(1))) const _Float16 gf16_t;
+typedef __attribute__((address_space(1))) const float gf32_t;
+typedef __attribute__((address_space(1))) const uint4 gu4_t;
+typedef __attribute__((address_space(1))) const uint2 gu2_t;
+typedef __attribute__((address_space(1))) const float4 gf4_t;
+
 REALM_DEV floatx4 mfma(half8_t a, half8_t b, floatx4 c)
 {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);

@@ -602,16 +602,21 @@ def test_multi_lora_activation_range(backend, oracle, scale, dtype):
 
 @pytest.mark.parametrize("t", [GGML_Q4_K, GGML_Q6_K])
 @pytest.mark.parametrize("m", [4, 37])
-@pytest.mark.parametrize("rt", ["", "2", "4", "8"])
+@pytest.mark.parametrize("rt", ["fused", "", "2", "4", "8"])
 def test_multi_lora_group(backend, oracle, monkeypatch, t, m, rt):
     """q/k/v-like projections with their own adapter sets in one grouped
     call (ragged rows; ranks 3 to 100; f16 and f32 factors), against the
     oracle per projection: per-matrix launches at 4 tokens, one tiled base
-    launch for the group at 37; one shrink and one expand launch for the
-    group, the expand with its default row tile and each of 128, 256 and
-    512 rows per workgroup forced (600 rows: several row groups, the last
-    one partial; shorter projections skip the groups past their rows)."""
-    if rt:
+    launch for the group at 37.  At 37 tokens, "fused" (the default): the
+    shrink runs in the xprep launch and the expand in the K-split reduce
+    (the last kernel); otherwise (REALM_LORA_FUSED=0) one shrink and one
+    expand launch for the group, the expand with its default row tile and
+    each of 128, 256 and 512 rows per workgroup forced (600 rows: several
+    row groups, the last one partial; shorter projections skip the groups
+    past their rows)."""
+    if rt != "fused":
+        monkeypatch.setenv("REALM_LORA_FUSED", "0")
+    if rt not in ("fused", ""):
         monkeypatch.setenv("REALM_LORA_EXPAND_RT", rt)
     g = synth.rng(zlib.crc32(f"lgroup{t}{m}".encode()) % 100000)
     k = 1536
@@ -651,7 +656,9 @@ def test_multi_lora_group(backend, oracle, monkeypatch, t, m, rt):
             backend.release_weights(wh)
         for d in [dx, d_ids] + dys:
             d.close()
-    if m > 4:  # one expand launch for the group is the last kernel
+    if m > 4 and rt == "fused":  # the expand is in the reduce
+        assert kernel == "realm_gemm_tiled_reduce_lora", kernel
+    elif m > 4:  # one expand launch for the group is the last kernel
         assert kernel.startswith("realm_lora_expand"), kernel
         if rt:
             assert kernel.endswith("expand" if rt == "8" else f"_rt{rt}"), kernel
