@@ -17,9 +17,12 @@ After the timed region, bench.py reports the roofline of the dominant Q4_K
 kernel (the grouped gate/up GEMV: its launches replayed from a graph of their
 own, HIP events on its stream) and, in "extra": the same step at batch 4 and
 16, 16-tenant multi-LoRA overhead (config 3), prefill TFLOP/s (config 2,
-Q4_K and Q8_0 with bf16 activations) and the CPU baseline (the oracle's
-restatement of realm-compute-cpu, timed on this host).  All inputs are
-synthetic and seeded (realm_amd/synth.py).
+Q4_K and Q8_0 with bf16 activations), the config-4 70B-shape layer, the dense
+f32 product, the reference's own criterion workloads for the Q4_K fused
+kernel (fused_kernels.rs:96-211, with the same shapes timed on the CPU
+restatement) and the CPU baseline (the oracle's restatement of
+realm-compute-cpu, timed on this host).  All inputs are synthetic and seeded
+(realm_amd/synth.py).
 """
 from __future__ import annotations
 
@@ -474,6 +477,45 @@ def dense(be, stream: int, reps: int) -> dict:
     return out
 
 
+CRITERION = ([("qkv_proj", 1, 6144, 2048), ("attention_out", 1, 2048, 2048),
+              ("ffn_gate_up", 1, 11264, 2048), ("ffn_down", 1, 2048, 5632),
+              ("lm_head", 1, 32000, 2048)]
+             + [(f"batch{b}_2048", b, 2048, 2048) for b in (1, 4, 8, 16, 32)]
+             + [(f"square{z}", 1, z, z) for z in (256, 512, 1024, 2048, 4096)])
+
+
+def criterion_shapes(be, stream: int, reps: int) -> tuple[dict, list]:
+    """The reference's own criterion workloads for the Q4_K fused kernel
+    (crates/realm-compute-cpu/benches/fused_kernels.rs:96-211: the five
+    transformer shapes at batch 1 including lm_head 32000 x 2048, batch sizes
+    1-32 on 2048 x 2048, square matrices 256-4096), on resident weights: 20
+    calls on the same weights and input per graph, as criterion's loop calls
+    the same data, so the weights are cache-warm for the smaller shapes.
+    Returns the GPU figures and the host data for the CPU leg."""
+    g = synth.rng(11)
+    out, host = {}, []
+    for name, m, n, k in CRITERION:
+        blocks = synth.q4k_blocks(g, n, k)
+        x_host = synth.activations(g, m, k)
+        h = be.register_weights(GGML_Q4_K, blocks, n, k)
+        x = be.alloc(m * k * 4).upload(x_host)
+        y = be.alloc(m * n * 4)
+        gr = capture(be, stream, lambda: [be.matmul_dev(h, x.ptr, m, y.ptr, stream=stream)
+                                          for _ in range(20)])
+        time_graph(be, gr, stream, 2)
+        us = time_graph(be, gr, stream, reps) / 20 * 1e3
+        be.graph_release(gr)
+        kern = be.last_kernel()
+        out[name] = {"m": m, "n": n, "k": k, "us": round(us, 3),
+                     "gb_per_s": round(alg_bytes(GGML_Q4_K, n, k, m) / (us * 1e-6) / 1e9, 1),
+                     "kernel": kern}
+        host.append((name, m, n, k, blocks, x_host))
+        be.release_weights(h)
+        x.close()
+        y.close()
+    return out, host
+
+
 def cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -498,6 +540,23 @@ def median_rate(fn, nbytes: int, seconds: float, trials: int = 10) -> tuple[floa
         rates.append(nbytes * reps / (time.perf_counter() - t0) / 1e9)
         calls += reps
     return float(np.median(rates)), calls
+
+
+def cpu_criterion(crit_host: list, gpu: dict) -> None:
+    """The criterion workloads on the oracle's restatement of fused.rs (the
+    function the reference's criterion benchmark times, one thread): median
+    of 3 calls each, added to the GPU figures with the ratio."""
+    from oracle import oracle as o  # checker/baseline only
+    for name, m, n, k, blocks, x in crit_host:
+        o.fused(GGML_Q4_K, blocks, x, m, n, k)
+        ts = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            o.fused(GGML_Q4_K, blocks, x, m, n, k)
+            ts.append(time.perf_counter() - t0)
+        cpu_us = float(np.median(ts)) * 1e6
+        gpu[name]["cpu_1thread_us"] = round(cpu_us, 1)
+        gpu[name]["gpu_over_cpu"] = round(cpu_us / gpu[name]["us"], 1)
 
 
 def cpu_baseline(seconds: float, blocks, x, gpu_y) -> tuple[dict, dict]:
@@ -544,7 +603,8 @@ def main() -> int:
                     help="no timing: one 256 MiB device copy (the counter reference) then "
                          "one gate/up GEMV launch per layer, for rocprofv3 --pmc runs")
     ap.add_argument("--extra-only",
-                    choices=("batched", "lora", "prefill", "config4", "dense", "layer"),
+                    choices=("batched", "lora", "prefill", "config4", "dense", "layer",
+                             "criterion"),
                     help="run one of the extra measurements alone (for kernel profiles) and "
                          "print its result; no decode step, no JSON line")
     args = ap.parse_args()
@@ -567,6 +627,9 @@ def main() -> int:
         return 0
     if args.extra_only == "dense":
         log(f"dense: {dense(be, stream, 10)}")
+        return 0
+    if args.extra_only == "criterion":
+        log(f"criterion shapes: {criterion_shapes(be, stream, 10)[0]}")
         return 0
     log(f"registering {args.layers} LLaMA-7B layers")
     model = Model7B(be, args.layers, 16)
@@ -647,6 +710,9 @@ def main() -> int:
         log(f"config4: {extra['config4_70b_layer']}")
         extra["dense_f32"] = dense(be, stream, 10)
         log(f"dense: {extra['dense_f32']}")
+        extra["criterion_q4k"], crit_host = criterion_shapes(be, stream, 10)
+        cpu_criterion(crit_host, extra["criterion_q4k"])
+        log(f"criterion shapes: {extra['criterion_q4k']}")
         cpu, cpu1 = cpu_baseline(args.cpu_seconds, wq_host, x_host, wq_out)
         extra["cpu_baseline_1thread"] = cpu1
         log(f"cpu baseline: {cpu}")
