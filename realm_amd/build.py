@@ -34,6 +34,9 @@ HSACO_UNITS = [("realm_kernels", "realm_kernels.hip", ()),
                ("realm_gemv_q4k_t4", "gemv_fmt.hip", ("REALM_GEMV_FMT=0", "REALM_GEMV_NT=4")),
                ("realm_gemv_q6k_t4", "gemv_fmt.hip", ("REALM_GEMV_FMT=1", "REALM_GEMV_NT=4")),
                ("realm_gemv_q80_t4", "gemv_fmt.hip", ("REALM_GEMV_FMT=2", "REALM_GEMV_NT=4")),
+               ("realm_gemv_q8m", "gemv_fmt.hip", ("REALM_GEMV_FMT=3",)),
+               ("realm_gemv_q8m_t2", "gemv_fmt.hip", ("REALM_GEMV_FMT=3", "REALM_GEMV_NT=2")),
+               ("realm_gemv_q8m_t4", "gemv_fmt.hip", ("REALM_GEMV_FMT=3", "REALM_GEMV_NT=4")),
                ("realm_gemm_tiled", "gemm_tiled.hip", ())]
 HSACO = os.path.join(LIB_DIR, "realm_kernels.hsaco")
 LIBSO = os.path.join(LIB_DIR, "librealm_hip.so")

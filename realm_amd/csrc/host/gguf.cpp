@@ -473,15 +473,21 @@ REALM_API int realm_hip_gguf_register(uint64_t model, const void *bytes, size_t 
             todo.emplace_back(i, t);
         }
     }
-    // the device footprint of all of them first (the 32-element formats stay
-    // resident dequantized, 4 bytes per weight): an image that cannot fit is
-    // refused before anything is registered
+    // the device footprint of all of them first (the reference's Q2_K / Q3_K
+    // / Q5_K / Q8_K stay resident dequantized, 4 bytes per weight; the
+    // 32-element formats take the q8m layout, 1.125 bytes per weight plus
+    // padding): an image that cannot fit is refused before anything is
+    // registered
     size_t need = 0, free_bytes = 0;
     for (auto &it : todo) {
         const Tensor &t = it.second;
-        const bool f32res = t.type != REALM_GGML_Q4_K && t.type != REALM_GGML_Q6_K &&
-                            t.type != REALM_GGML_Q8_0;
-        need += f32res ? (size_t)(t.dims[0] * t.dims[1] * 4) : (size_t)t.nbytes + (size_t)t.nbytes / 8;
+        const size_t elems = (size_t)(t.dims[0] * t.dims[1]);
+        const bool kq = t.type == REALM_GGML_Q2_K || t.type == REALM_GGML_Q3_K ||
+                        t.type == REALM_GGML_Q5_K || t.type == REALM_GGML_Q8_K;
+        const bool q8m = t.type == REALM_GGML_Q4_0 || t.type == REALM_GGML_Q4_1 ||
+                         t.type == REALM_GGML_Q5_0 || t.type == REALM_GGML_Q5_1 ||
+                         t.type == REALM_GGML_Q8_1;
+        need += kq ? elems * 4 : q8m ? elems + elems / 8 + 4096 : (size_t)t.nbytes + (size_t)t.nbytes / 8;
     }
     GG_TRY(realm_device_free_bytes(&free_bytes));
     if (need > free_bytes)

@@ -53,10 +53,14 @@ REALM_EMBED(7, REALM_HSACO_FILE7)
 REALM_EMBED(8, REALM_HSACO_FILE8)
 REALM_EMBED(9, REALM_HSACO_FILE9)
 REALM_EMBED(10, REALM_HSACO_FILE10)
-static_assert(REALM_HSACO_COUNT == 11, "the build embeds eleven code objects");
+REALM_EMBED(11, REALM_HSACO_FILE11)
+REALM_EMBED(12, REALM_HSACO_FILE12)
+REALM_EMBED(13, REALM_HSACO_FILE13)
+static_assert(REALM_HSACO_COUNT == 14, "the build embeds fourteen code objects");
 static const unsigned char *const realm_hsacos[REALM_HSACO_COUNT] = {
-    realm_hsaco0, realm_hsaco1, realm_hsaco2, realm_hsaco3, realm_hsaco4,  realm_hsaco5,
-    realm_hsaco6, realm_hsaco7, realm_hsaco8, realm_hsaco9, realm_hsaco10};
+    realm_hsaco0, realm_hsaco1, realm_hsaco2,  realm_hsaco3,  realm_hsaco4,
+    realm_hsaco5, realm_hsaco6, realm_hsaco7,  realm_hsaco8,  realm_hsaco9,
+    realm_hsaco10, realm_hsaco11, realm_hsaco12, realm_hsaco13};
 
 #define REALM_API extern "C" __attribute__((visibility("default")))
 
@@ -138,7 +142,12 @@ const char *dq_name(int t)
 }
 size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 size_t round_up(size_t v, size_t m) { return (v + m - 1) / m * m; }
-const char *fmt_name(int t) { return t == GGML_Q4_K ? "q4k" : t == GGML_Q6_K ? "q6k" : "q80"; }
+// kernel-name stem of a resident format ("q8m": the 32-element formats as
+// int8 q', f16 scale, f16 delta)
+const char *fmt_name(int t)
+{
+    return t == GGML_Q4_K ? "q4k" : t == GGML_Q6_K ? "q6k" : t == GGML_Q8_0 ? "q80" : "q8m";
+}
 
 // ------------------------------------------------------------------ device
 
@@ -397,12 +406,18 @@ size_t layout(int type, size_t n, size_t k, size_t off[3], size_t *kx)
         *kx = k;
         return off[2] + np * B * 192;
     }
+    // Q8_0, and the 32-element formats as q8m (the Q8_0 streams plus a delta
+    // stream shaped like the scales)
     size_t kp = round_up(k, 64);
     off[0] = 0;
     off[1] = align256(np * (kp / 32) * 2);
-    off[2] = 0;
     *kx = kp;
-    return off[1] + np * kp;
+    if (type == GGML_Q8_0) {
+        off[2] = 0;
+        return off[1] + np * kp;
+    }
+    off[2] = align256(off[1] + np * kp);
+    return off[2] + np * (kp / 32) * 2;
 }
 
 bool q6k_wide(const uint8_t *blocks, size_t nblocks)
@@ -432,7 +447,7 @@ int upload_repack(int type, const void *blocks, size_t n, size_t k, void *dst, W
     uint8_t *base = (uint8_t *)dst;
     w->w0 = base + off[0];
     w->w1 = base + off[1];
-    w->w2 = type == GGML_Q6_K ? base + off[2] : nullptr;
+    w->w2 = type == GGML_Q6_K || is_block32(type) ? base + off[2] : nullptr;
     w->wide = type == GGML_Q6_K && q6k_wide((const uint8_t *)blocks, nblocks);
     // zeroes the row padding (and the Q8_0 K padding) of every stream
     HIP_TRY(hipMemsetAsync(dst, 0, total, s));
@@ -454,11 +469,17 @@ int upload_repack(int type, const void *blocks, size_t n, size_t k, void *dst, W
         void *args[] = {&raw, &dq, &scq, &qq, &nb, &bpr};
         CHECK(launch("realm_repack_q6k", dim3((unsigned)((nblocks * 64 + 255) / 256)),
                      dim3(256), 0, s, args));
-    } else {
+    } else if (type == GGML_Q8_0) {
         void *dq = (void *)w->w0, *qq = (void *)w->w1;
         int kbr = (int)(k / 32), kp = (int)kx;
         void *args[] = {&raw, &dq, &qq, &nb, &kbr, &kp};
         CHECK(launch("realm_repack_q80", dim3((unsigned)((nblocks * 32 + 255) / 256)),
+                     dim3(256), 0, s, args));
+    } else { // the 32-element formats: q8m
+        void *dq = (void *)w->w0, *qq = (void *)w->w1, *mq = (void *)w->w2;
+        int kbr = (int)(k / 32), kp = (int)kx, it = type;
+        void *args[] = {&raw, &dq, &qq, &mq, &nb, &kbr, &kp, &it};
+        CHECK(launch("realm_repack_q32", dim3((unsigned)((nblocks * 32 + 255) / 256)),
                      dim3(256), 0, s, args));
     }
     return REALM_OK;
@@ -582,11 +603,13 @@ int run_gemv(const Weight *const *ws, int count, const float *d_x, int M, float 
     }
     if (w.type == GGML_Q8_0 && d > 8) // its 12-deep ring does not fit the registers
         d = 8;
+    if (is_block32(w.type) && d > 3) // q8m (one more dword per unit) spills from depth 4
+        d = 3;
     d = std::min(d, ds[nd - 1]);
     if (const char *env = getenv("REALM_GEMV_D")) { // tuning override
         int v = atoi(env);
         for (int i = 0; i < nd; ++i)
-            if (ds[i] == v)
+            if (ds[i] == v && !(is_block32(w.type) && v > 3))
                 d = v;
     }
     const int threads = threads_of(d);
@@ -1109,10 +1132,50 @@ int run_gemm(const Weight &w, const void *d_x, bool bf16, size_t M, float *d_y, 
 int dense_launch(const float *da, const float *db, float *dc, size_t m, size_t k, size_t n,
                  int bt, hipStream_t s);
 
+// The 32-element formats (q8m layout): the int8-dot GEMV for up to 4
+// tokens, 4 tokens per launch up to Q8M_GEMV_MAX_M, and beyond that the
+// matrix dequantized into the stream's workspace (bit-exact,
+// realm_dequant_q8m) for the dense f32 GEMM.  Measured on 4096 x 4096: one
+// token 5.6 us (the dense product over f32 weights took 88 us), 4 tokens
+// 8.1 us, 16 tokens 30 us (98 us dense), 64 tokens 124-132 us dequantized +
+// dense, about what 16 four-token launches take.
+constexpr size_t Q8M_GEMV_MAX_M = 48;
+
+int run_q8m(const Weight &w, const float *d_x, size_t M, float *d_y, hipStream_t s)
+{
+    if (M <= Q8M_GEMV_MAX_M) {
+        int rc = REALM_OK;
+        for (size_t t0 = 0; t0 < M && rc == REALM_OK; t0 += 4) {
+            const Weight *ws[1] = {&w};
+            float *ys[1] = {d_y + t0 * w.n};
+            rc = run_gemv(ws, 1, d_x + t0 * w.k, (int)std::min<size_t>(4, M - t0), ys, s);
+        }
+        if (rc != REALM_BACKEND_UNSUPPORTED) // (rows too long for the GEMV: dense)
+            return rc;
+    }
+    void *wf = nullptr;
+    CHECK(ws_get(s, WS_WEIGHT, w.n * w.k * sizeof(float), &wf));
+    long long ln = (long long)w.n;
+    int ik = (int)w.k, ikp = (int)w.kx, it = w.type;
+    const void *dq = w.w0, *qq = w.w1, *mq = w.w2;
+    void *args[] = {(void *)&dq, (void *)&qq, (void *)&mq, &wf, &ln, &ik, &ikp, &it};
+    CHECK(launch("realm_dequant_q8m", dim3((unsigned)((w.n * w.k + 255) / 256)), dim3(256), 0,
+                 s, args));
+    return dense_launch(d_x, (const float *)wf, d_y, M, w.k, w.n, 1, s);
+}
+
 int run_matmul(const Weight &w, const void *d_x, bool bf16, size_t M, float *d_y,
                hipStream_t s, const LoraCall *lora)
 {
-    if (is_dq(w.type)) { // resident as dequantized f32 [n][k]: y = x W^T
+    if (is_block32(w.type)) {
+        if (bf16 || lora)
+            return fail(REALM_BACKEND_UNSUPPORTED,
+                        "bf16 input and LoRA take Q4_K, Q6_K or Q8_0 weights");
+        if (M == 0 || w.n == 0)
+            return REALM_OK;
+        return run_q8m(w, (const float *)d_x, M, d_y, s);
+    }
+    if (is_kq(w.type)) { // resident as dequantized f32 [n][k]: y = x W^T
         if (bf16 || lora)
             return fail(REALM_BACKEND_UNSUPPORTED,
                         "bf16 input and LoRA take Q4_K, Q6_K or Q8_0 weights");
@@ -1963,10 +2026,10 @@ REALM_API int realm_hip_weights_register(int type, const void *blocks, size_t nb
     CHECK(ensure_init());
     hipStream_t s;
     CHECK(thread_stream(&s));
-    if (is_dq(type)) {
-        // the 32-element formats and the reference's own Q2_K / Q3_K / Q5_K /
-        // Q8_K stay resident dequantized (f32 [n][k], 4 bytes per weight),
-        // their products on the f32 GEMM
+    if (is_kq(type)) {
+        // the reference's own Q2_K / Q3_K / Q5_K / Q8_K stay resident
+        // dequantized (f32 [n][k], 4 bytes per weight), their products on the
+        // f32 GEMM (the 32-element formats are repacked as q8m below)
         void *dev = nullptr, *raw = nullptr;
         CHECK(ws_get(s, WS_RAW, nbytes, &raw));
         HIP_TRY(hipMalloc(&dev, n * k * 4));
@@ -2127,7 +2190,9 @@ REALM_API int realm_hip_weights_matmul_group_dev(const uint64_t *handles, size_t
         return fail(REALM_INVALID_ARGUMENT, "batch exceeds 2^31-1");
     hipStream_t s;
     CHECK(pick_stream(stream, &s));
-    if (is_dq(w[0].type)) { // dequantized f32 weights: one dense product each
+    // dequantized f32 weights, and q8m batches past the GEMV's 4 tokens: one
+    // product each (q8m groups of 1-4 tokens take the grouped GEMV below)
+    if (is_kq(w[0].type) || (is_block32(w[0].type) && batch > 4)) {
         for (size_t i = 0; i < count; ++i)
             CHECK(run_matmul(w[i], d_input, false, batch, d_outs[i], s, nullptr));
         return REALM_OK;
@@ -2136,6 +2201,11 @@ REALM_API int realm_hip_weights_matmul_group_dev(const uint64_t *handles, size_t
         int rc = run_gemv(wp, (int)count, d_input, (int)batch, d_outs, s);
         if (rc != REALM_BACKEND_UNSUPPORTED)
             return rc;
+    }
+    if (is_block32(w[0].type)) { // q8m rows too long for the GEMV: dense, one each
+        for (size_t i = 0; i < count; ++i)
+            CHECK(run_matmul(w[i], d_input, false, batch, d_outs[i], s, nullptr));
+        return REALM_OK;
     }
     // batched: one activation prep for the whole group (the matrices share
     // format and K, so the prepared layout is the same), then one MFMA launch

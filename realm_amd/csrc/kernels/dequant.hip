@@ -195,10 +195,34 @@ extern "C" __global__ __launch_bounds__(256) void realm_repack_q80(
 }
 
 // The 32-element block formats of the reference (crates/realm-core/src/
-// quant.rs:10-70, 226-370), one thread per output element: Q4_0 (type 2,
-// 18 B), Q4_1 (3, 20 B), Q5_0 (6, 22 B), Q5_1 (7, 24 B), Q8_1 (9, 36 B).
-// Products and sums are separate f32 roundings (__fmul_rn / __fadd_rn), as
-// the reference's mul-then-add, so the output is bit-exact.
+// quant.rs:10-70, 226-370): Q4_0 (type 2, 18 B), Q4_1 (3, 20 B), Q5_0 (6,
+// 22 B), Q5_1 (7, 24 B), Q8_1 (9, 36 B).  Element i of a block is q' s
+// (+ delta for Q4_1, Q5_1, Q8_1) with s, delta the block's f16 fields and q'
+// the small integer block32_q returns.
+REALM_DEV int block32_bytes(int type)
+{
+    return type == 2 ? 18 : type == 3 ? 20 : type == 6 ? 22 : type == 7 ? 24 : 36;
+}
+REALM_DEV bool block32_delta(int type) { return type == 3 || type == 7 || type == 9; }
+REALM_DEV int block32_q(int type, const uint8_t *b, int i)
+{
+    const bool delta = block32_delta(type);
+    if (type == 2 || type == 3) {
+        const uint8_t byte = b[(delta ? 4 : 2) + (i & 15)];
+        return (i < 16 ? (byte & 0x0F) : (byte >> 4)) - 8;
+    }
+    if (type == 6 || type == 7) {
+        const uint8_t *qh = b + (delta ? 4 : 2), *ql = qh + 4;
+        const int lo = (i & 1) ? (ql[i >> 1] >> 4) : (ql[i >> 1] & 0x0F);
+        const int sh = 4 * ((i & 3) >= 2) + (type == 6 ? 2 * ((i >> 2) & 1) : 0);
+        return (lo | (((qh[i >> 3] >> sh) & 1) << 4)) - 16;
+    }
+    return (int8_t)b[4 + i];
+}
+
+// Bit-exact dequantization, one thread per output element.  Products and
+// sums are separate f32 roundings (__fmul_rn / __fadd_rn), as the
+// reference's mul-then-add.
 extern "C" __global__ __launch_bounds__(256) void realm_dequant_q32(const uint8_t *raw, float *y,
                                                                    long long nb, int type)
 {
@@ -206,25 +230,62 @@ extern "C" __global__ __launch_bounds__(256) void realm_dequant_q32(const uint8_
     if (e >= nb * 32)
         return;
     const int i = (int)(e & 31);
-    const int bb = type == 2 ? 18 : type == 3 ? 20 : type == 6 ? 22 : type == 7 ? 24 : 36;
-    const uint8_t *b = raw + (e >> 5) * bb;
+    const uint8_t *b = raw + (e >> 5) * block32_bytes(type);
     const float s = realm::f16_bits_to_f32(b[0] | (b[1] << 8));
-    const bool delta = type == 3 || type == 7 || type == 9;
+    const bool delta = block32_delta(type);
     const float d = delta ? realm::f16_bits_to_f32(b[2] | (b[3] << 8)) : 0.f;
-    int q;
-    if (type == 2 || type == 3) {
-        const uint8_t byte = b[(delta ? 4 : 2) + (i & 15)];
-        q = (i < 16 ? (byte & 0x0F) : (byte >> 4)) - 8;
-    } else if (type == 6 || type == 7) {
-        const uint8_t *qh = b + (delta ? 4 : 2), *ql = qh + 4;
-        const int lo = (i & 1) ? (ql[i >> 1] >> 4) : (ql[i >> 1] & 0x0F);
-        const int sh = 4 * ((i & 3) >= 2) + (type == 6 ? 2 * ((i >> 2) & 1) : 0);
-        q = (lo | (((qh[i >> 3] >> sh) & 1) << 4)) - 16;
-    } else {
-        q = (int8_t)b[4 + i];
-    }
-    const float t = __fmul_rn((float)q, s);
+    const float t = __fmul_rn((float)block32_q(type, b, i), s);
     y[e] = delta ? __fadd_rn(t, d) : t;
+}
+
+// Registration of a 32-element format as resident weights ("q8m"): q' as
+// int8 in the Q8_0 layout (realm_repack_q80: row n, block kb, byte i in
+// plane (32 (kb & 1) + i) / 16 of unit kb / 2), the f16 scale in the Q8_0
+// scale stream and the f16 delta (zero for Q4_0 and Q5_0) in a stream of the
+// same shape.  1.125 bytes per weight against 4 for f32; q' s + delta
+// reproduces the reference's values exactly.  The destination is zeroed
+// beforehand (padding: zero quants, scales and deltas).
+extern "C" __global__ __launch_bounds__(256) void realm_repack_q32(
+    const uint8_t *__restrict__ raw, uint8_t *__restrict__ dq, int8_t *__restrict__ qq,
+    uint8_t *__restrict__ mq, long long nblocks, int kb_per_row, int kp, int type)
+{
+    const long long gid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long long b = gid >> 5;
+    if (b >= nblocks)
+        return;
+    const int i = (int)(gid & 31);
+    const long long n = b / kb_per_row;
+    const int kb = (int)(b - n * kb_per_row);
+    const uint8_t *blk = raw + b * block32_bytes(type);
+    const int ub = 32 * (kb & 1) + i;
+    const long long U = kp / 64;
+    qq[n * kp + (ub >> 4) * (U * 16) + (kb >> 1) * 16 + (ub & 15)] = (int8_t)block32_q(type, blk, i);
+    const long long si = (n * (kp / 32) + kb) * 2;
+    if (i < 2)
+        dq[si + i] = blk[i];
+    else if (i < 4 && block32_delta(type))
+        mq[si + i - 2] = blk[i];
+}
+
+// A q8m matrix back to f32 W [n][k] for the dense products of larger
+// batches: q' s (+ delta), the reference's roundings, so bit-exact with
+// realm_dequant_q32 on the raw blocks.
+extern "C" __global__ __launch_bounds__(256) void realm_dequant_q8m(
+    const uint8_t *__restrict__ dq, const int8_t *__restrict__ qq, const uint8_t *__restrict__ mq,
+    float *__restrict__ y, long long n, int k, int kp, int type)
+{
+    const long long e = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (e >= n * k)
+        return;
+    const long long row = e / k;
+    const int kk = (int)(e - row * k), qi = kk & 63;
+    const long long U = kp / 64;
+    const int q = qq[row * kp + (qi >> 4) * (U * 16) + (kk >> 6) * 16 + (qi & 15)];
+    const long long si = (row * (kp / 32) + (kk >> 5)) * 2;
+    const float s = realm::f16_bits_to_f32(dq[si] | (dq[si + 1] << 8));
+    const float t = __fmul_rn((float)q, s);
+    y[e] = block32_delta(type) ? __fadd_rn(t, realm::f16_bits_to_f32(mq[si] | (mq[si + 1] << 8)))
+                               : t;
 }
 
 // The reference's own 256-element Q2_K (type 10, 116 B), Q3_K (11, 196 B),

@@ -73,11 +73,13 @@ REALM_DEV float dev_weight(const uint8_t *__restrict__ w0, const uint8_t *__rest
         const uint32_t lo = t < 2 ? (qa & 15u) : (qa >> 4);
         const int q = (int)(lo | (((qh >> (2 * t)) & 3u) << 4)) - 32;
         return d * (float)sc * (float)q;
-    } else { // Q8_0
-        const float d = f16_bits_to_f32(
-            *reinterpret_cast<const uint16_t *>(w0 + ((size_t)row * (KX >> 5) + (k >> 5)) * 2));
+    } else { // Q8_0; 3: the 32-element formats as int8 q, f16 scale, f16 delta (q8m)
+        const size_t bi = (size_t)row * (KX >> 5) + (k >> 5);
+        const float d = f16_bits_to_f32(*reinterpret_cast<const uint16_t *>(w0 + bi * 2));
         const int qi = k & 63;
         const int8_t q = (int8_t)w1[(size_t)row * U * 64 + (qi >> 4) * U * 16 + u * 16 + (qi & 15)];
+        if constexpr (FMT == 3)
+            return (float)q * d + f16_bits_to_f32(*reinterpret_cast<const uint16_t *>(w2 + bi * 2));
         return (float)q * d;
     }
 }

@@ -33,6 +33,9 @@ using realm::GemvArgs;
 #define FMT_Q4K 0
 #define FMT_Q6K 1
 #define FMT_Q80 2
+#define FMT_Q8M 3 // Q4_0, Q4_1, Q5_0, Q5_1, Q8_1: int8 q, f16 scale and delta per 32
+// one metadata float4 per unit (two 32-element x blocks)
+#define ONE_META(FMT) ((FMT) == FMT_Q80 || (FMT) == FMT_Q8M)
 
 namespace {
 
@@ -288,6 +291,35 @@ struct Unit<FMT_Q80> {
     }
 };
 
+// The reference's 32-element formats (quant.rs:10-70, 226-370), each
+// element q' s + delta with a small integer q' (Q4_0/Q4_1: nibble - 8,
+// Q5_0/Q5_1: 5-bit value - 16, Q8_1: int8), repacked at registration into
+// the Q8_0 layout plus a delta stream (zero for Q4_0 and Q5_0): the Q8_0
+// unit and the two f16 deltas of its blocks.
+template <>
+struct Unit<FMT_Q8M> {
+    uint4 q[4];
+    uint32_t d, m;
+    struct Off {
+        uint32_t q, d;
+    };
+    static __device__ __forceinline__ Off offsets(int slot, int u, int U)
+    {
+        return {(uint32_t)(slot * U * 64 + u * 16), (uint32_t)(slot * U * 4 + u * 4)};
+    }
+    static __device__ __forceinline__ size_t stride0(int U) { return (size_t)U * 4; }
+    static __device__ __forceinline__ size_t stride1(int U) { return (size_t)U * 64; }
+    static __device__ __forceinline__ size_t stride2(int U) { return (size_t)U * 4; }
+    __device__ __forceinline__ void load(const Bases &b, const Off &o, int U)
+    {
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            q[c] = ldg16(b.b1 + o.q + (uint32_t)(c * U * 16));
+        d = ldg4(b.b0 + o.d);
+        m = ldg4(b.b2 + o.d);
+    }
+};
+
 REALM_DEV float combine(int ph, int pl, float s)
 {
     return s * ((float)ph + (float)pl * (1.f / 254.f));
@@ -385,6 +417,11 @@ REALM_DEV void unit_dot(const Unit<FMT> &w, const XR &xr, const XM &xm, int u, i
         }
     } else {
         const float da = f16_bits_to_f32(w.d), db = f16_bits_to_f32(w.d >> 16);
+        float ma = 0.f, mb = 0.f;
+        if constexpr (FMT == FMT_Q8M) {
+            ma = f16_bits_to_f32(w.m);
+            mb = f16_bits_to_f32(w.m >> 16);
+        }
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             if (t > 0)
@@ -402,6 +439,8 @@ REALM_DEV void unit_dot(const Unit<FMT> &w, const XR &xr, const XM &xm, int u, i
             }
             const float4 m = xm(t, 0);
             acc[t] += da * combine(ha, la, m.x) + db * combine(hb, lb, m.y);
+            if constexpr (FMT == FMT_Q8M) // sum of (q' s + delta) x: + delta * sum x per block
+                acc[t] += fmaf(ma, m.z, mb * m.w);
         }
     }
 }
@@ -532,7 +571,7 @@ REALM_DEV void gemv(const GemvArgs &a)
             } else {
                 auto xr = [&](int t, int p) { return rec[t * TS + p * U + uc]; };
                 auto xm = [&](int t, int q) {
-                    return mt[t * TS + (FMT == FMT_Q80 ? uc : 2 * uc + q)];
+                    return mt[t * TS + (ONE_META(FMT) ? uc : 2 * uc + q)];
                 };
                 unit_dot<FMT, NT>(w[j], xr, xm, uc, nan_fb, part);
             }
@@ -644,7 +683,7 @@ REALM_DEV void gemv(const GemvArgs &a)
                 xreg[t][p] = rec[t * TS + p * U + uc];
 #pragma unroll
             for (int q = 0; q < 2; ++q)
-                mreg[t][q] = meta[t * TS + (FMT == FMT_Q80 ? uc : 2 * uc + q)];
+                mreg[t][q] = meta[t * TS + (ONE_META(FMT) ? uc : 2 * uc + q)];
         }
     }
     // The rest of the ring is issued only now: a larger burst ahead of the
@@ -709,8 +748,10 @@ REALM_DEV void gemv(const GemvArgs &a)
 #define DEF_GEMV2(LPR, UPL, D, NM, NT, SUF) DEF_GEMV1(q4k, FMT_Q4K, LPR, UPL, D, NM, NT, SUF)
 #elif REALM_GEMV_FMT == FMT_Q6K
 #define DEF_GEMV2(LPR, UPL, D, NM, NT, SUF) DEF_GEMV1(q6k, FMT_Q6K, LPR, UPL, D, NM, NT, SUF)
-#else
+#elif REALM_GEMV_FMT == FMT_Q80
 #define DEF_GEMV2(LPR, UPL, D, NM, NT, SUF) DEF_GEMV1(q80, FMT_Q80, LPR, UPL, D, NM, NT, SUF)
+#else
+#define DEF_GEMV2(LPR, UPL, D, NM, NT, SUF) DEF_GEMV1(q8m, FMT_Q8M, LPR, UPL, D, NM, NT, SUF)
 #endif
 
 #if !defined(REALM_GEMV_NT) || REALM_GEMV_NT == 1

@@ -1,5 +1,6 @@
 // Translation unit of the GEMV variants of one weight format, selected with
-// -DREALM_GEMV_FMT=0 (Q4_K), 1 (Q6_K) or 2 (Q8_0), and one token count,
+// -DREALM_GEMV_FMT=0 (Q4_K), 1 (Q6_K), 2 (Q8_0) or 3 (the 32-element formats in
+// the q8m layout), and one token count,
 // -DREALM_GEMV_NT=1 (default), 2 or 4.
 #ifndef REALM_GEMV_FMT
 #error "REALM_GEMV_FMT must be defined"

@@ -64,5 +64,7 @@ def test_code_object_is_embedded_for_gfx950():
               b"realm_lora_shrink_q4k_f32", b"realm_lora_shrink_q6k_f32_o1", b"realm_dense_f32",
               b"realm_gemm_q4k_t4112b2", b"realm_gemm_q6kw_t4112p2", b"realm_xprep_q4k_o1",
               b"realm_gemm_tiled_reduce", b"realm_gemm_tiled_reduce_lora",
-              b"realm_xprep_lora_q4k_o1", b"realm_xprep_lora_q6k"):
+              b"realm_xprep_lora_q4k_o1", b"realm_xprep_lora_q6k",
+              b"realm_gemv_q8m_l64_u1_d1_m1", b"realm_gemv_q8m_l32_u1_d2_m4_t4",
+              b"realm_repack_q32", b"realm_dequant_q8m"):
         assert k in blobs

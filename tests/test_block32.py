@@ -116,20 +116,25 @@ def test_fused_validation(backend):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("t", [2, 3, 6, 7, 9])
-def test_resident_weights(backend, oracle, t):
-    """Registered once (kept dequantized on the device), then products at 1,
-    3 and 20 tokens, alone and in a grouped call, against the oracle; LoRA
-    on such a base is refused."""
+@pytest.mark.parametrize("n,k", [(96, 512), (200, 4128)])
+def test_resident_weights(backend, oracle, t, n, k):
+    """Registered once (repacked as int8 q', f16 scale, f16 delta: 1.125
+    bytes per weight), then products at 1-4 tokens (int8-dot GEMV), 7 and 20
+    (4 tokens per GEMV launch) and 50 (dequantized bit-exactly into the
+    workspace, dense f32 GEMM), alone and in a grouped call, against the
+    oracle; K = 4128 is not a multiple of 64 (padded layout); LoRA on such a
+    base is refused."""
     from realm_amd.backend import BackendError
-    g = np.random.default_rng(500 + t)
-    n, k = 96, 512
+    g = np.random.default_rng(500 + t + n)
     raw = _random_blocks(g, t, n * k // 32)
     h = backend.register_weights(t, raw, n, k)
     h2 = backend.register_weights(t, raw, n, k)
     try:
-        for m in (1, 3, 20):
+        for m in (1, 2, 3, 4, 7, 20, 50):
             x = g.standard_normal(m * k).astype(np.float32)
             got = backend.weights_matmul(h, x.reshape(m, k))
+            kern = backend.last_kernel()
+            assert kern.startswith("realm_gemv_q8m" if m <= 48 else "realm_dense"), (m, kern)
             rc, want = oracle.candle_fused(t, raw, x, m, n, k)
             assert rc == 0 and rel_l2(got, want.reshape(m, n)) < 1e-3, m
             dx = backend.alloc(x.nbytes).upload(x)
