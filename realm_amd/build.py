@@ -37,7 +37,8 @@ HSACO_UNITS = [("realm_kernels", "realm_kernels.hip", ()),
                ("realm_gemv_q8m", "gemv_fmt.hip", ("REALM_GEMV_FMT=3",)),
                ("realm_gemv_q8m_t2", "gemv_fmt.hip", ("REALM_GEMV_FMT=3", "REALM_GEMV_NT=2")),
                ("realm_gemv_q8m_t4", "gemv_fmt.hip", ("REALM_GEMV_FMT=3", "REALM_GEMV_NT=4")),
-               ("realm_gemm_tiled", "gemm_tiled.hip", ())]
+               ("realm_gemm_tiled", "gemm_tiled.hip", ()),
+               ("realm_gemm_tiled_q80", "gemm_tiled.hip", ("REALM_TILED_Q80",))]
 HSACO = os.path.join(LIB_DIR, "realm_kernels.hsaco")
 LIBSO = os.path.join(LIB_DIR, "librealm_hip.so")
 

@@ -56,11 +56,12 @@ REALM_EMBED(10, REALM_HSACO_FILE10)
 REALM_EMBED(11, REALM_HSACO_FILE11)
 REALM_EMBED(12, REALM_HSACO_FILE12)
 REALM_EMBED(13, REALM_HSACO_FILE13)
-static_assert(REALM_HSACO_COUNT == 14, "the build embeds fourteen code objects");
+REALM_EMBED(14, REALM_HSACO_FILE14)
+static_assert(REALM_HSACO_COUNT == 15, "the build embeds fifteen code objects");
 static const unsigned char *const realm_hsacos[REALM_HSACO_COUNT] = {
     realm_hsaco0, realm_hsaco1, realm_hsaco2,  realm_hsaco3,  realm_hsaco4,
     realm_hsaco5, realm_hsaco6, realm_hsaco7,  realm_hsaco8,  realm_hsaco9,
-    realm_hsaco10, realm_hsaco11, realm_hsaco12, realm_hsaco13};
+    realm_hsaco10, realm_hsaco11, realm_hsaco12, realm_hsaco13, realm_hsaco14};
 
 #define REALM_API extern "C" __attribute__((visibility("default")))
 
@@ -662,16 +663,16 @@ bool tiled_tile(const std::string &name, bool bf16, int ks, GemmTile *t)
 // Kernel choice for a batched product with M tokens against w:
 //  * M <= 8 (f32) or M <= 32 (bf16): gemm.hip's small-batch tiles (16 rows x
 //    8..32 tokens, K split over the workgroup's waves);
-//  * otherwise, Q4_K / Q6_K (K a multiple of 256): the LDS-tiled kernel on
-//    32x32x16 MFMAs (gemm_tiled.hip) -- packed f32 (16 or 32 tokens per
-//    workgroup) or bf16 (64 tokens) -- with the K range split so that a
-//    launch has at least 256 workgroups;
-//  * Q8_0: gemm.hip's decode (16 rows x 16..64 tokens) or prefill (128 rows
-//    x 64 tokens) tiles.
+//  * otherwise, Q4_K / Q6_K / Q8_0 (K a multiple of 256): the LDS-tiled
+//    kernel on 32x32x16 MFMAs (gemm_tiled.hip) -- packed f32 (16 or 32
+//    tokens per workgroup) or bf16 (64 tokens) -- with the K range split so
+//    that a launch has at least 256 workgroups;
+//  * Q8_0 with K not a multiple of 256: gemm.hip's decode (16 rows x 16..64
+//    tokens) or prefill (128 rows x 64 tokens) tiles.
 // The tiled kernel's formats; its per-lane weight offsets are 32-bit.
 bool tiled_ok(const Weight &w)
 {
-    return (w.type == GGML_Q4_K || w.type == GGML_Q6_K) && w.kx % 256 == 0 &&
+    return (w.type == GGML_Q4_K || w.type == GGML_Q6_K || w.type == GGML_Q8_0) && w.kx % 256 == 0 &&
            w.bytes < ((size_t)1 << 32);
 }
 
@@ -690,7 +691,7 @@ GemmTile gemm_tile(const Weight &w, size_t M, bool bf16)
         return M <= 16 ? GemmTile{"s1", 16, 16, 1024} : GemmTile{"s2", 16, 32, 512};
     if (tiled_ok(w)) {
         GemmTile t;
-        const char *name = bf16 ? (w.type == GGML_Q4_K ? "t4112b2" : "t4112b3")
+        const char *name = bf16 ? (w.type == GGML_Q6_K ? "t4112b3" : "t4112b2")
                                 : (M <= 16 ? "t4111p2" : "t4112p2");
         tiled_tile(name, bf16, 1, &t);
         const size_t tiles = ((w.n + t.rows_per_wg - 1) / t.rows_per_wg) *

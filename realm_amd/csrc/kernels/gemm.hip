@@ -660,7 +660,11 @@ REALM_DEV void shrink_body(const _Float16 *__restrict__ xh, const _Float16 *__re
     half8_t bh[SHRINK_NS], bl[SHRINK_NS];
 #pragma unroll
     for (int s = 0; s < SHRINK_NS; ++s) {
-        const int k0 = kwin<FMT, ORD>(4 * (s0 + min(s, ns - 1)) + c);
+        // a window at or past K (Q8_0 rows padded to KX) reads nothing: the
+        // adapter row has K entries
+        const int kw = kwin<FMT, ORD>(4 * (s0 + min(s, ns - 1)) + c);
+        const bool inrow = kw < K;
+        const int k0 = inrow ? kw : 0;
         float v[8];
         if (F16A) {
             gf16_t *src = (gf16_t *)e.a + (size_t)jr * K + k0;
@@ -678,7 +682,7 @@ REALM_DEV void shrink_body(const _Float16 *__restrict__ xh, const _Float16 *__re
         }
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
-            const float vv = s < ns ? v[pi8(q)] : 0.f;
+            const float vv = s < ns && inrow ? v[pi8(q)] : 0.f;
             const _Float16 hq = (_Float16)vv;
             bh[s][q] = hq;
             bl[s][q] = (_Float16)(vv - (float)hq);
@@ -1003,6 +1007,7 @@ REALM_DEV void lora_shrink_fused(const LoraGroupArgs &g, int wg)
     }
 DEF_XPREP_LORA(q4k, FMT_Q4K)
 DEF_XPREP_LORA(q6k, FMT_Q6K)
+DEF_XPREP_LORA(q80, FMT_Q80)
 
 // ------------------------------------------------------------ LoRA expand
 //

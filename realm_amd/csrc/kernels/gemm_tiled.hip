@@ -50,7 +50,7 @@ struct Mat {
 
 // Raw weight bytes of one 32-row tile and one 256-k block as lane
 // (r32 = row within the tile, h = lane half) needs them: k 128h .. 128h+127
-// of the block (Q4_K, Q6_K), or bytes 8h..8h+7 of every 16-byte chunk (Q8_0).
+// of the block (Q4_K, Q6_K), or (Q8_0) units 2(i&1) + h of plane i/2, i < 8.
 template <int FMT>
 struct Raw;
 template <>
@@ -66,8 +66,8 @@ struct Raw<FMT_Q6K> {
 };
 template <>
 struct Raw<FMT_Q80> {
-    uint2 q[16]; // k-step s: block 8 blk + s/2, bytes 16(s&1) + 8h .. +8
-    uint4 d;     // the eight f16 block scales
+    uint4 q[8]; // load i: plane i/2 of unit 4 blk + 2(i&1) + h, k-steps 2i, 2i+1
+    uint4 d;    // the eight f16 block scales
 };
 
 // Byte offsets of a lane's weights (its row, lane half h) in the weight
@@ -88,7 +88,7 @@ REALM_DEV LaneOff lane_off(const Mat &g, int row, int h)
         return {r * (uint32_t)(g.K >> 8) * 2u, r * (uint32_t)(g.K >> 8) * 16u + 8u * h,
                 r * (uint32_t)(g.K >> 6) * 48u + 32u * h};
     else // Q8_0: w0 d [row][KX/32] 2 B; w1 q planes, KX B per row
-        return {r * (uint32_t)(g.KX >> 5) * 2u, r * (uint32_t)g.KX + 8u * h, 0u};
+        return {r * (uint32_t)(g.KX >> 5) * 2u, r * (uint32_t)g.KX + 16u * h, 0u};
 }
 
 REALM_DEV void load_raw(Raw<FMT_Q4K> &r, const Mat &g, const LaneOff &o, int blk)
@@ -120,8 +120,8 @@ REALM_DEV void load_raw(Raw<FMT_Q80> &r, const Mat &g, const LaneOff &o, int blk
     const size_t U = (size_t)(g.KX >> 6);
     const uint8_t *q = (const uint8_t *)g.w1 + (size_t)blk * 64;
 #pragma unroll
-    for (int s = 0; s < 16; ++s) // Q8_0 block 8 blk + s/2: unit 4 blk + s/4, plane s & 3
-        r.q[s] = ldg8(q + (s & 3) * (U * 16) + (s >> 2) * 16 + o.o1);
+    for (int i = 0; i < 8; ++i) // plane i/2 of unit 4 blk + 2(i&1) + h (h in o1)
+        r.q[i] = ldg16(q + (i >> 1) * (U * 16) + (i & 1) * 32 + o.o1);
     r.d = ldg16((const uint8_t *)g.w0 + (size_t)blk * 16 + o.o0);
 }
 
@@ -255,6 +255,37 @@ REALM_DEV half8_t q80_frag(uint2 q)
     return h8(u32(q0), u32(q1), u32(q2), u32(q3));
 }
 
+// A Q8_0 k-step fragment with its block scale d folded in, as an exact f16
+// pair: hi = RN(d q) and lo = d q - hi.  d q has at most 19 significant bits
+// and is a multiple of ulp(d); hi is a multiple of ulp(d) too, so lo is a
+// multiple of ulp(d) no larger than half an ulp of hi (at most 8 bits): the
+// fused multiply-add computes it exactly.  hi is finite while |d| < 512
+// (|q| <= 128); rows with a larger or non-finite scale are flagged
+// (q80_big_scale) and take the exact f32 path.
+REALM_DEV void q80_split(uint2 q, uint32_t d2bits, half8_t &hi, half8_t &lo)
+{
+#pragma clang fp contract(off)
+    const uint4 u = __builtin_bit_cast(uint4, q80_frag(q));
+    const uint32_t qv[4] = {u.x, u.y, u.z, u.w};
+    const half2_t d2 = h2(d2bits);
+    uint32_t hv[4], lv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const half2_t p = h2(qv[i]) * d2;
+        hv[i] = u32(p);
+        lv[i] = u32(__builtin_elementwise_fma(h2(qv[i]), d2, -p));
+    }
+    hi = h8(hv[0], hv[1], hv[2], hv[3]);
+    lo = h8(lv[0], lv[1], lv[2], lv[3]);
+}
+
+// Nonzero when one of the two f16 scales in w has |d| >= 512 or is not
+// finite ((bits & 0x7FFF) >= 0x6000, tested per half without carries).
+REALM_DEV uint32_t q80_big_scale(uint32_t w)
+{
+    return ((w & 0x7FFF7FFFu) + 0x20002000u) & 0x80008000u;
+}
+
 REALM_DEV half8_t lds_h8(const uint8_t *p)
 {
     return __builtin_bit_cast(half8_t, *reinterpret_cast<const uint4 *>(p));
@@ -278,6 +309,9 @@ REALM_DEV void gemm_tiled(const GemmArgs &g)
     constexpr int GTOK = WT * TM * TOK;     // tokens per workgroup
     constexpr int SROWS = WT * TM * 32;     // LDS slot rows per part
     constexpr int NPART = SEP ? 2 : 1;
+    // Q8_0 and wide Q6_K run two MFMAs per k-step on two weight fragments
+    // (Q8_0: the hi and lo parts of d q, summed straight into acc)
+    constexpr bool TWO = WIDE || FMT == FMT_Q80;
     constexpr int RS = 528;                 // bytes per slot row: 256 f16 + 16 pad
     constexpr int MRS = 32;                 // bytes per Q4_K min-term row
     constexpr int XB = NPART * SROWS * RS;
@@ -416,7 +450,12 @@ REALM_DEV void gemm_tiled(const GemmArgs &g)
     // the next block's weights load into wnxt and its activations into nbuf.
     // vector-memory instructions one stage issues in every wave (at least):
     // its share of the direct-to-LDS loads plus its weight loads
-    constexpr int GMIN = (XINS + MINS) / NW + TN * (FMT == FMT_Q4K ? 5 : FMT == FMT_Q6K ? 8 : 17);
+    constexpr int GMIN = (XINS + MINS) / NW + TN * (FMT == FMT_Q4K ? 5 : FMT == FMT_Q6K ? 8 : 9);
+    // Q8_0: rows (lane's tile a) with a scale that d q in f16 cannot hold
+    uint32_t bad[TN];
+#pragma unroll
+    for (int a = 0; a < TN; ++a)
+        bad[a] = 0u;
     // wait until at most k stages' loads are in flight (k < NS - 1), i.e.
     // everything issued before them has landed
     auto wait_stages = [&](int k) {
@@ -464,6 +503,18 @@ REALM_DEV void gemm_tiled(const GemmArgs &g)
             for (int a = 0; a < TN; ++a)
                 dec[a].init(wcur[a], h, g.nan_fb);
         }
+        // Q8_0: the scales of this lane's blocks, 2h, 2h+1 (dlo) and 4+2h,
+        // 5+2h (dhi) of the eight
+        uint32_t dlo[TN], dhi[TN];
+        if constexpr (FMT == FMT_Q80) {
+#pragma unroll
+            for (int a = 0; a < TN; ++a) {
+                bad[a] |= q80_big_scale(wcur[a].d.x) | q80_big_scale(wcur[a].d.y) |
+                          q80_big_scale(wcur[a].d.z) | q80_big_scale(wcur[a].d.w);
+                dlo[a] = h ? wcur[a].d.y : wcur[a].d.x;
+                dhi[a] = h ? wcur[a].d.w : wcur[a].d.z;
+            }
+        }
         auto afrag = [&](int s, half8_t (&A)[TM], half8_t (&AL)[TM]) {
 #pragma unroll
             for (int bb = 0; bb < TM; ++bb) {
@@ -476,7 +527,16 @@ REALM_DEV void gemm_tiled(const GemmArgs &g)
 #pragma unroll
             for (int a = 0; a < TN; ++a) {
                 if constexpr (FMT == FMT_Q80) {
-                    Bf[a] = q80_frag(wcur[a].q[s]);
+                    // k-step s = 2i + t: bytes 8t..8t+7 of load i, in Q8_0
+                    // block 4(i&1) + 2h + i/4 of the eight, whose scale is
+                    // splat to both halves
+                    const int i = s >> 1;
+                    const uint4 &qi = wcur[a].q[i];
+                    const uint2 qq = (s & 1) ? make_uint2(qi.z, qi.w) : make_uint2(qi.x, qi.y);
+                    const uint32_t dw = (i & 1) ? dhi[a] : dlo[a];
+                    const uint32_t d2 = __builtin_amdgcn_perm(dw, dw, (i >> 2) ? 0x03020302u
+                                                                               : 0x01000100u);
+                    q80_split(qq, d2, Bf[a], Bh[a]);
                 } else if constexpr (FMT == FMT_Q4K) {
                     Bf[a] = dec[a].frag(s);
                 } else {
@@ -524,23 +584,25 @@ REALM_DEV void gemm_tiled(const GemmArgs &g)
             for (int a = 0; a < TN; ++a)
 #pragma unroll
                 for (int bb = 0; bb < TM; ++bb) {
-                    P[a][bb] = mfma32(A[cu][bb], Bf[cu][a], P[a][bb]);
+                    // Q8_0's fragments carry d: its sums go straight into acc
+                    floatx16 &T = FMT == FMT_Q80 ? acc[a][bb] : P[a][bb];
+                    T = mfma32(A[cu][bb], Bf[cu][a], T);
                     if (SEP)
-                        P[a][bb] = mfma32(AL[cu][bb], Bf[cu][a], P[a][bb]);
-                    if (WIDE) {
-                        P[a][bb] = mfma32(A[cu][bb], Bh[cu][a], P[a][bb]);
+                        T = mfma32(AL[cu][bb], Bf[cu][a], T);
+                    if (TWO) {
+                        T = mfma32(A[cu][bb], Bh[cu][a], T);
                         if (SEP)
-                            P[a][bb] = mfma32(AL[cu][bb], Bh[cu][a], P[a][bb]);
+                            T = mfma32(AL[cu][bb], Bh[cu][a], T);
                     }
                 }
 #ifndef REALM_TILED_NO_SCHED
             // interleave: each MFMA of step s is followed by a share of the
             // LDS reads and the decode work of step s+1
             if (s + 1 < 16) {
-                constexpr int NMF = TN * TM * (SEP ? 2 : 1) * (WIDE ? 2 : 1);
+                constexpr int NMF = TN * TM * (SEP ? 2 : 1) * (TWO ? 2 : 1);
                 constexpr int NRD = TM * (SEP ? 2 : 1);
                 constexpr int RPM = (NRD + NMF - 1) / NMF;
-                constexpr int NVA = (FMT == FMT_Q4K ? 9 : FMT == FMT_Q6K ? 22 : 9) * TN;
+                constexpr int NVA = (FMT == FMT_Q4K ? 9 : 22) * TN;
                 constexpr int VPM = (NVA + NMF - 1) / NMF;
 #pragma unroll
                 for (int m = 0; m < NMF; ++m) {
@@ -550,23 +612,6 @@ REALM_DEV void gemm_tiled(const GemmArgs &g)
                 }
             }
 #endif
-            if constexpr (FMT == FMT_Q80) {
-                if (s & 1) { // Q8_0 block 8 blk + s/2 complete: apply its scale
-#pragma unroll
-                    for (int a = 0; a < TN; ++a) {
-                        const uint32_t dw = (s >> 2) == 0 ? wcur[a].d.x : (s >> 2) == 1 ? wcur[a].d.y
-                                          : (s >> 2) == 2 ? wcur[a].d.z : wcur[a].d.w;
-                        const float d = f16_bits_to_f32(dw >> (16 * ((s >> 1) & 1)));
-#pragma unroll
-                        for (int bb = 0; bb < TM; ++bb)
-#pragma unroll
-                            for (int v = 0; v < 16; ++v) {
-                                acc[a][bb][v] = __builtin_fmaf(d, P[a][bb][v], acc[a][bb][v]);
-                                P[a][bb][v] = 0.f;
-                            }
-                    }
-                }
-            }
         }
         if constexpr (FMT != FMT_Q80) {
 #pragma unroll
@@ -657,7 +702,9 @@ REALM_DEV void gemm_tiled(const GemmArgs &g)
             for (int v = 0; v < 16; v += VS)
 #pragma unroll
                 for (int a = 0; a < TN; ++a)
-                    pt[tloc(bb, v) * GROWS + rl0 + 32 * a] = vals[bb][v / VS][a];
+                    // a flagged Q8_0 row leaves NaN: the reduce recomputes it
+                    pt[tloc(bb, v) * GROWS + rl0 + 32 * a] =
+                        (FMT == FMT_Q80 && bad[a]) ? __builtin_nanf("") : vals[bb][v / VS][a];
         return;
     }
 #pragma unroll
@@ -673,7 +720,8 @@ REALM_DEV void gemm_tiled(const GemmArgs &g)
                 if (row >= mat.N)
                     continue;
                 float out = vals[bb][v / VS][a];
-                if (__builtin_expect(__builtin_isnan(ts[bb][v]), 0)) // flagged by xprep
+                // flagged by xprep, or a Q8_0 row with a scale d q in f16 cannot hold
+                if (__builtin_expect(__builtin_isnan(ts[bb][v]) || (FMT == FMT_Q80 && bad[a]), 0))
                     out = exact_dot<FMT>(mat.w0, mat.w1, mat.w2, row, g.K, g.KX,
                                          (const uint8_t *)g.x +
                                              (size_t)tok * g.K * (g.xbf16 ? 2 : 4),
@@ -706,6 +754,11 @@ REALM_DEV void gemm_tiled(const GemmArgs &g)
     GEMM_TILED(FNAME, FMT, WIDE, 4, 1, 1, 4, MODE_B, b, 1, 2)                              \
     GEMM_TILED(FNAME, FMT, WIDE, 8, 1, 1, 1, MODE_B, b, 1, 4)
 
+// Q8_0 is compiled as a code object of its own (REALM_TILED_Q80), in
+// parallel with the rest
+#ifdef REALM_TILED_Q80
+GEMM_TILED_SET(q80, FMT_Q80, false)
+#else
 GEMM_TILED_SET(q4k, FMT_Q4K, false)
 GEMM_TILED_SET(q6k, FMT_Q6K, false)
 GEMM_TILED_SET(q6kw, FMT_Q6K, true)
@@ -739,14 +792,15 @@ REALM_DEV ReduceSite reduce_site(const GemmArgs &g, int grows, int gtok, int til
 }
 
 // The base product of one element: the parts in split order, or the exact
-// f32 dot product for a token xprep flagged.
+// f32 dot product for a token xprep flagged and for a NaN sum (a Q8_0 row
+// the tiled kernel flagged, or a NaN that the exact product reproduces).
 REALM_DEV float reduce_base(const GemmArgs &g, const ReduceSite &r, int tile, int e, int TILE)
 {
     const float *p = g.part + (size_t)tile * g.ksplit * TILE + e;
     float sum = p[0];
     for (int c = 1; c < g.ksplit; ++c)
         sum += p[(size_t)c * TILE];
-    if (__builtin_expect(__builtin_isnan(g.tscale[r.tok]), 0)) { // flagged by xprep
+    if (__builtin_expect(__builtin_isnan(g.tscale[r.tok]) || __builtin_isnan(sum), 0)) {
         auto pick = [&](auto a0, auto a1, auto a2, auto a3) {
             return r.seg == 0 ? a0 : r.seg == 1 ? a1 : r.seg == 2 ? a2 : a3;
         };
@@ -754,10 +808,12 @@ REALM_DEV float reduce_base(const GemmArgs &g, const ReduceSite &r, int tile, in
         const void *w1 = pick(g.seg_w1[0], g.seg_w1[1], g.seg_w1[2], g.seg_w1[3]);
         const void *w2 = pick(g.seg_w2[0], g.seg_w2[1], g.seg_w2[2], g.seg_w2[3]);
         const uint8_t *x = (const uint8_t *)g.x + (size_t)r.tok * g.K * (g.xbf16 ? 2 : 4);
-        // the reduce serves Q4_K and Q6_K launches: the format from the layout
+        // the reduce serves Q4_K, Q6_K and Q8_0 launches: the format from the layout
         sum = g.fmt == FMT_Q4K
                   ? exact_dot<FMT_Q4K>(w0, w1, w2, r.row, g.K, g.KX, x, g.xbf16, g.nan_fb, 0, 1)
-                  : exact_dot<FMT_Q6K>(w0, w1, w2, r.row, g.K, g.KX, x, g.xbf16, g.nan_fb, 0, 1);
+              : g.fmt == FMT_Q6K
+                  ? exact_dot<FMT_Q6K>(w0, w1, w2, r.row, g.K, g.KX, x, g.xbf16, g.nan_fb, 0, 1)
+                  : exact_dot<FMT_Q80>(w0, w1, w2, r.row, g.K, g.KX, x, g.xbf16, g.nan_fb, 0, 1);
     }
     return sum;
 }
@@ -848,8 +904,8 @@ extern "C" __global__ __launch_bounds__(256) void realm_gemm_tiled_reduce_lora(G
     lds_barrier();
     if (!live)
         return;
-    if (__builtin_expect(__builtin_isnan(g.tscale[r.tok]), 0)) // flagged by xprep
-        sum = reduce_base(g, r, tile, e, TILE);
+    if (__builtin_expect(__builtin_isnan(g.tscale[r.tok]) || __builtin_isnan(sum), 0))
+        sum = reduce_base(g, r, tile, e, TILE); // flagged: the exact product
     if (has) {
         const float *uq = us[r.tl - tl0];
         float d = 0.f;
@@ -888,3 +944,4 @@ extern "C" __global__ __launch_bounds__(256) void realm_gemm_tiled_reduce_lora(G
     }
     r.y[(size_t)r.tok * r.N + r.row] = sum;
 }
+#endif // REALM_TILED_Q80

@@ -35,8 +35,16 @@ REALM_DEV int pi8(int e) { return (e & 4) | ((e & 1) << 1) | ((e >> 1) & 1); }
 template <int FMT, int ORD>
 REALM_DEV int kwin(int pg)
 {
-    if (FMT == FMT_Q80)
-        return 8 * pg;
+    if (FMT == FMT_Q80) {
+        if (ORD == 0)
+            return 8 * pg;
+        // k-step s = 2i + t of block b, lane half h: 8 k of the 16 that
+        // load i of gemm_tiled.hip brings (plane i/2 of unit 2(i&1) + h), so
+        // that a lane's weight loads are 16 bytes and a row's two lanes read
+        // 32 contiguous bytes
+        const int b = pg >> 5, s = (pg >> 1) & 15, h = pg & 1, i = s >> 1;
+        return 256 * b + 64 * (2 * (i & 1) + h) + 16 * (i >> 1) + 8 * (s & 1);
+    }
     if (ORD == 0) {
         const int b = pg >> 5, i = (pg >> 2) & 7, c = pg & 3;
         if (FMT == FMT_Q4K)

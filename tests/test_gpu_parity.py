@@ -281,12 +281,13 @@ TILED = [("t4111p2", 1), ("t4111p2", 3), ("t4112p2", 1), ("t4112p2", 4), ("t4112
 
 
 @pytest.mark.parametrize("tile,ks", TILED)
-@pytest.mark.parametrize("t", [GGML_Q4_K, GGML_Q6_K])
+@pytest.mark.parametrize("t", [GGML_Q4_K, GGML_Q6_K, GGML_Q8_0])
 def test_tiled_variants(backend, oracle, monkeypatch, tile, ks, t):
     """Every LDS-tiled kernel variant (forced through the tuning override):
     ragged rows (N = 300) and tokens, six 256-blocks split unevenly over K
     splits, the packed / separate-lo / bf16 activation modes; Q6_K once
-    with sub-scales over the full int8 range (the split-scale decode)."""
+    with sub-scales over the full int8 range (the split-scale decode); Q8_0
+    with quants over the full int8 range (-128 included)."""
     monkeypatch.setenv("REALM_GEMM_TILE", tile)
     monkeypatch.setenv("REALM_GEMM_KS", str(ks))
     bf16 = tile.endswith(("b2", "b3", "b4"))
@@ -295,6 +296,8 @@ def test_tiled_variants(backend, oracle, monkeypatch, tile, ks, t):
     blocks = synth.blocks(g, t, n, k)
     if t == GGML_Q6_K and ks > 1:
         blocks["scales"] = g.integers(-128, 128, blocks["scales"].shape, dtype=np.int8)
+    if t == GGML_Q8_0:
+        blocks["quants"] = g.integers(-128, 128, blocks["quants"].shape, dtype=np.int8)
     for m in (37, 70):
         if bf16:
             xb = synth.activations_bf16(g, m, k)

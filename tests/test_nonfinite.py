@@ -143,7 +143,10 @@ CASES = [  # (format, m, k, group, bf16, forced tile, forced K split, kernel pre
     (GGML_Q4_K, 37, 2048, 1, False, "t4112p2", "1", "realm_gemm_q4k_t4112p2"),
     (GGML_Q6_K, 37, 2048, 2, False, "t4112p2", "4", "realm_gemm_tiled_reduce"),
     (GGML_Q4_K, 64, 2048, 1, True, "t4112b2", "1", "realm_gemm_q4k_t4112b2"),
-    (GGML_Q8_0, 37, 2048, 1, False, None, None, "realm_gemm_q80"),
+    (GGML_Q8_0, 37, 2048, 1, False, None, None, "realm_gemm_tiled_reduce"),
+    (GGML_Q8_0, 37, 2048, 1, False, "t4112p2", "1", "realm_gemm_q80_t4112p2"),
+    (GGML_Q8_0, 64, 2048, 1, True, "t4112b2", "1", "realm_gemm_q80_t4112b2"),
+    (GGML_Q8_0, 37, 2112, 1, False, None, None, "realm_gemm_q80_d4"),
 ]
 
 
@@ -203,3 +206,54 @@ def test_attention_nonfinite_scores(backend, monkeypatch, splits):
     assert np.array_equal(np.isnan(got), np.isnan(want))
     fin = np.isfinite(want)
     assert rel_l2(got[fin], want[fin]) < 1e-5
+
+
+Q80_SCALE_CASES = [  # (m, bf16, forced tile, forced K split, kernel)
+    (37, False, "t4112p2", "1", "realm_gemm_q80_t4112p2"),
+    (37, False, "t4112p2", "4", "realm_gemm_tiled_reduce"),
+    (64, True, "t4112b2", "1", "realm_gemm_q80_t4112b2"),
+    (64, True, "t4112b2", "2", "realm_gemm_tiled_reduce"),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", Q80_SCALE_CASES, ids=[f"m{c[0]}-{c[2]}-ks{c[3]}" for c in Q80_SCALE_CASES])
+def test_q80_tiled_scales(backend, oracle, monkeypatch, case):
+    """Q8_0 scales the tiled kernel's f16 (d q) split cannot hold: rows with
+    a block scale of magnitude 512 or more, NaN or +-Inf are computed by the
+    exact f32 path (direct epilogue, or the reduce after a K split); a row
+    whose scale is 511.75 with q = -128 (d q = -65504, the largest f16) stays
+    on the MFMA path.  NaN and Inf positions match the oracle's f32 product,
+    finite entries within 1e-3 per token."""
+    m, bf16, tile, ks, kernel = case
+    monkeypatch.setenv("REALM_GEMM_TILE", tile)
+    monkeypatch.setenv("REALM_GEMM_KS", ks)
+    g = synth.rng(zlib.crc32(repr(case).encode()) % 100000)
+    n, k = 200, 2048
+    blocks = synth.blocks(g, GGML_Q8_0, n, k)
+    blocks["quants"] = g.integers(-128, 128, blocks["quants"].shape, dtype=np.int8)
+    kb = k // 32
+    f16 = lambda v: np.array([v], np.float16).view(np.uint16)[0]
+    blocks["scale"][5 * kb + 3] = f16(600.0)
+    blocks["scale"][6 * kb + 40] = f16(-512.0)
+    blocks["scale"][7 * kb + 63] = f16(65504.0)
+    blocks["scale"][9 * kb + 10] = f16(511.75)
+    blocks["quants"][9 * kb + 10] = -128
+    blocks["scale"][150 * kb + 2] = f16(np.nan)
+    blocks["scale"][151 * kb + 20] = f16(np.inf)
+    blocks["scale"][152 * kb + 33] = f16(-np.inf)
+    if bf16:
+        xb = synth.activations_bf16(g, m, k)
+        xin, xf = xb, synth.bf16_bits_to_f32(xb)
+    else:
+        xin = xf = synth.activations(g, m, k)
+    (got,), ran = _run(backend, GGML_Q8_0, blocks, n, k, xin, bf16)
+    assert ran == kernel, ran
+    rc, ref = oracle.candle_fused(GGML_Q8_0, blocks, xf, m, n, k)
+    assert rc == 0
+    ref = ref.reshape(m, n)
+    assert np.isnan(ref[:, 150]).all() and not np.isfinite(ref[:, 151:153]).any()
+    assert_same_class(got, ref, ran)
+    for r in (5, 6, 7, 9):  # the planted rows, each on its own
+        err = rel_l2(got[:, r], ref[:, r])
+        assert err < REL_TOL, f"row {r}: rel_l2 {err:.3e}"
