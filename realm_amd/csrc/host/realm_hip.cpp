@@ -691,7 +691,7 @@ GemmTile gemm_tile(const Weight &w, size_t M, bool bf16)
         return M <= 16 ? GemmTile{"s1", 16, 16, 1024} : GemmTile{"s2", 16, 32, 512};
     if (tiled_ok(w)) {
         GemmTile t;
-        const char *name = bf16 ? (w.type == GGML_Q6_K ? "t4112b3" : "t4112b2")
+        const char *name = bf16 ? "t4112b2"
                                 : (M <= 16 ? "t4111p2" : "t4112p2");
         tiled_tile(name, bf16, 1, &t);
         const size_t tiles = ((w.n + t.rows_per_wg - 1) / t.rows_per_wg) *

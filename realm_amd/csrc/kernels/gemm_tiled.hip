@@ -244,14 +244,18 @@ struct Dec<FMT_Q6K, WIDE> {
 template <bool WIDE>
 struct Dec<FMT_Q80, WIDE> {}; // Q8_0 decodes straight from the raw bytes
 
+// Eight Q8_0 quants as f16, in the order bytes 0, 2, 1, 3, 4, 6, 5, 7: each
+// byte XOR 0x80 (u = q + 128) placed under 0x64 by one byte permute is the
+// f16 1152 + q; minus 1152 gives q exactly.
 REALM_DEV half8_t q80_frag(uint2 q)
 {
     const half2_t off2 = splat2(-1152.f);
-    const uint32_t ua = q.x ^ 0x80808080u, ub = q.y ^ 0x80808080u;
-    const half2_t q0 = h2((ua & 0x00FF00FFu) | 0x64006400u) + off2;
-    const half2_t q1 = h2(((ua >> 8) & 0x00FF00FFu) | 0x64006400u) + off2;
-    const half2_t q2 = h2((ub & 0x00FF00FFu) | 0x64006400u) + off2;
-    const half2_t q3 = h2(((ub >> 8) & 0x00FF00FFu) | 0x64006400u) + off2;
+    const uint32_t ua = q.x ^ 0x80808080u, ub = q.y ^ 0x80808080u, c = 0x64646464u;
+    // selector bytes 0-3 pick from the second operand, 4-7 from the first
+    const half2_t q0 = h2(__builtin_amdgcn_perm(c, ua, 0x04020400u)) + off2;
+    const half2_t q1 = h2(__builtin_amdgcn_perm(c, ua, 0x04030401u)) + off2;
+    const half2_t q2 = h2(__builtin_amdgcn_perm(c, ub, 0x04020400u)) + off2;
+    const half2_t q3 = h2(__builtin_amdgcn_perm(c, ub, 0x04030401u)) + off2;
     return h8(u32(q0), u32(q1), u32(q2), u32(q3));
 }
 

@@ -109,7 +109,7 @@ def test_gemv_ring_depths_grouped(backend, oracle, monkeypatch, depth):
 
 @pytest.mark.parametrize("name,t,n,k,kernel", [
     ("w_gate", GGML_Q4_K, 28672, 8192, "realm_gemm_q4k_t4112b2"),
-    ("w_down", GGML_Q6_K, 8192, 28672, "realm_gemm_q6k_t4112b3"),
+    ("w_down", GGML_Q6_K, 8192, 28672, "realm_gemm_q6k_t4112b2"),
 ])
 def test_config4_prefill_1024(backend, oracle, name, t, n, k, kernel):
     """The config-4 1024-token bf16 prefill on the full 70B-shape W_gate

@@ -209,8 +209,9 @@ def _row_subset(t, blocks, n, k, rows):
 
 @pytest.mark.parametrize("t", [GGML_Q4_K, GGML_Q8_0])
 def test_config2_prefill_bf16(backend, oracle, t):
-    """Prefill M=512, K=4096 -> N=11008 with bf16 activations, checked on a
-    seeded subset of 96 output rows for all 512 tokens."""
+    """Prefill M=512, K=4096 -> N=11008 with bf16 activations (the launch
+    bench.py times: the LDS-tiled MFMA kernel for both formats), checked on
+    a seeded subset of 96 output rows for all 512 tokens."""
     g = synth.rng(2)
     m, n, k = 512, 11008, 4096
     blocks = synth.blocks(g, t, n, k)
@@ -221,6 +222,7 @@ def test_config2_prefill_bf16(backend, oracle, t):
     try:
         backend.matmul_dev(h, dx.ptr, m, dy.ptr, bf16=True)
         backend.synchronize()
+        ran = backend.last_kernel()
         got = dy.download(np.float32, m * n).reshape(m, n)
     finally:
         backend.release_weights(h)
@@ -231,7 +233,8 @@ def test_config2_prefill_bf16(backend, oracle, t):
                                   synth.bf16_bits_to_f32(xb), m, rows.size, k)
     assert rc == 0
     err = rel_l2(got[:, rows], ref.reshape(m, rows.size))
-    print(f"prefill {NAMES[t]} rel_l2={err:.3e}")
+    print(f"prefill {NAMES[t]} {ran} rel_l2={err:.3e}")
+    assert ran == f"realm_gemm_{'q4k' if t == GGML_Q4_K else 'q80'}_t4112b2", ran
     assert err < REL_TOL
     assert np.isfinite(got).all()
 
