@@ -606,7 +606,7 @@ def test_multi_lora_activation_range(backend, oracle, scale, dtype):
         backend.release_weights(wh)
 
 
-@pytest.mark.parametrize("t", [GGML_Q4_K, GGML_Q6_K])
+@pytest.mark.parametrize("t", [GGML_Q4_K, GGML_Q6_K, GGML_Q8_0])
 @pytest.mark.parametrize("m", [4, 37])
 @pytest.mark.parametrize("rt", ["fused", "", "2", "4", "8"])
 def test_multi_lora_group(backend, oracle, monkeypatch, t, m, rt):
