@@ -1330,15 +1330,23 @@ int fused_host(int type, const void *blocks, size_t n_blocks, const float *input
 }
 
 // Dense f32 C = A @ B (or A @ B^T, bt = 1) on device pointers; m, n, k >= 1
-// and below 2^31.  One workgroup per 128 x 128 tile of C.
+// and below 2^31.  One workgroup per TMR x 128 tile of C: TMR = 32 or 64 for
+// up to 32 or 64 rows (skinny products), 128 otherwise.
 int dense_launch(const float *da, const float *db, float *dc, size_t m, size_t k, size_t n,
                  int bt, hipStream_t s)
 {
+    const size_t tmr = m <= 32 ? 32 : m <= 64 ? 64 : 128;
+    const char *kname = m <= 32 ? "realm_dense_f32_m32" : m <= 64 ? "realm_dense_f32_m64"
+                                                                   : "realm_dense_f32";
     // K splits (parts summed in split order) until the launch has 256
-    // workgroups, keeping at least 256 positions of K per split
-    const size_t tiles = ((n + 127) / 128) * ((m + 127) / 128);
+    // workgroups, keeping at least 256 positions of K per split; skinny
+    // tiles until 1024 workgroups and 128 positions (a skinny product streams
+    // B once, and a workgroup holds one 16-position slice of it in flight:
+    // 32 x 4096 x 4096 B^T took 58 us at 8 splits, 41 us at 32)
+    const size_t tiles = ((n + 127) / 128) * ((m + tmr - 1) / tmr);
+    const size_t want = tmr < 128 ? 1024 : 256, kmin = tmr < 128 ? 128 : 256;
     int ks = 1;
-    while (tiles * ks < 256 && k / (2 * (size_t)ks) >= 256 && ks < 32)
+    while (tiles * ks < want && k / (2 * (size_t)ks) >= kmin && ks < 32)
         ks *= 2;
     if (const char *env = getenv("REALM_DENSE_KS")) // tuning override
         ks = std::max(1, std::min(64, atoi(env)));
@@ -1350,8 +1358,8 @@ int dense_launch(const float *da, const float *db, float *dc, size_t m, size_t k
         CHECK(ws_get(s, WS_PART, (size_t)ks * m * n * sizeof(float), &part));
     int M = (int)m, N = (int)n, K = (int)k;
     void *args[] = {(void *)&da, (void *)&db, (void *)&dc, &M, &N, &K, &bt, &ks, &part};
-    CHECK(launch("realm_dense_f32",
-                 dim3((unsigned)((n + 127) / 128), (unsigned)((m + 127) / 128), (unsigned)ks),
+    CHECK(launch(kname,
+                 dim3((unsigned)((n + 127) / 128), (unsigned)((m + tmr - 1) / tmr), (unsigned)ks),
                  dim3(256), 0, s, args));
     if (ks > 1) {
         long long total = (long long)(m * n);

@@ -748,12 +748,13 @@ def test_dense_random(backend, m, k, n):
 
 @pytest.mark.parametrize("transposed", [False, True])
 @pytest.mark.parametrize("m,k,n", [(1, 1, 1), (2, 3, 2), (31, 17, 129), (128, 256, 128),
-                                   (130, 515, 257), (32, 2048, 300), (5, 4099, 70)])
+                                   (130, 515, 257), (32, 2048, 300), (5, 4099, 70),
+                                   (33, 1024, 200), (64, 700, 130), (65, 300, 129)])
 def test_dense_dev(backend, m, k, n, transposed):
     """Device-pointer dense product, both B layouts, ragged tile edges in m,
-    n and k, skinny products with K splits (parts summed in split order): f32
-    products and sums, so within f32 rounding of an f64 product; small-integer
-    inputs give exact results."""
+    n and k, skinny products with K splits (parts summed in split order) on
+    the 32- and 64-row tiles: f32 products and sums, so within f32 rounding
+    of an f64 product; small-integer inputs give exact results."""
     g = synth.rng(m * 131 + k * 7 + n + transposed)
     for ints in (False, True):
         if ints:
@@ -777,7 +778,8 @@ def test_dense_dev(backend, m, k, n, transposed):
             assert np.array_equal(got, ref.astype(np.float32))
         else:  # f32 sums over k: relative error about 2^-24 sqrt(k)
             assert rel_l2(got, ref) < 1e-5
-    assert backend.last_kernel() in ("realm_dense_f32", "realm_dense_reduce")
+    tile = "realm_dense_f32" + ("_m32" if m <= 32 else "_m64" if m <= 64 else "")
+    assert backend.last_kernel() in (tile, "realm_dense_reduce"), backend.last_kernel()
 
 
 def test_candle_matmul_host_function(backend, kat):
