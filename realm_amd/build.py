@@ -37,6 +37,9 @@ HSACO_UNITS = [("realm_kernels", "realm_kernels.hip", ()),
                ("realm_gemv_q8m", "gemv_fmt.hip", ("REALM_GEMV_FMT=3",)),
                ("realm_gemv_q8m_t2", "gemv_fmt.hip", ("REALM_GEMV_FMT=3", "REALM_GEMV_NT=2")),
                ("realm_gemv_q8m_t4", "gemv_fmt.hip", ("REALM_GEMV_FMT=3", "REALM_GEMV_NT=4")),
+               ("realm_gemv_q4k_pre", "gemv_fmt.hip", ("REALM_GEMV_FMT=0", "REALM_GEMV_PRE")),
+               ("realm_gemv_q6k_pre", "gemv_fmt.hip", ("REALM_GEMV_FMT=1", "REALM_GEMV_PRE")),
+               ("realm_gemv_q80_pre", "gemv_fmt.hip", ("REALM_GEMV_FMT=2", "REALM_GEMV_PRE")),
                ("realm_gemm_tiled", "gemm_tiled.hip", ()),
                ("realm_gemm_tiled_q80", "gemm_tiled.hip", ("REALM_TILED_Q80",))]
 HSACO = os.path.join(LIB_DIR, "realm_kernels.hsaco")

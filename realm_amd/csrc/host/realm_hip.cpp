@@ -57,11 +57,15 @@ REALM_EMBED(11, REALM_HSACO_FILE11)
 REALM_EMBED(12, REALM_HSACO_FILE12)
 REALM_EMBED(13, REALM_HSACO_FILE13)
 REALM_EMBED(14, REALM_HSACO_FILE14)
-static_assert(REALM_HSACO_COUNT == 15, "the build embeds fifteen code objects");
+REALM_EMBED(15, REALM_HSACO_FILE15)
+REALM_EMBED(16, REALM_HSACO_FILE16)
+REALM_EMBED(17, REALM_HSACO_FILE17)
+static_assert(REALM_HSACO_COUNT == 18, "the build embeds eighteen code objects");
 static const unsigned char *const realm_hsacos[REALM_HSACO_COUNT] = {
     realm_hsaco0, realm_hsaco1, realm_hsaco2,  realm_hsaco3,  realm_hsaco4,
     realm_hsaco5, realm_hsaco6, realm_hsaco7,  realm_hsaco8,  realm_hsaco9,
-    realm_hsaco10, realm_hsaco11, realm_hsaco12, realm_hsaco13, realm_hsaco14};
+    realm_hsaco10, realm_hsaco11, realm_hsaco12, realm_hsaco13, realm_hsaco14,
+    realm_hsaco15, realm_hsaco16, realm_hsaco17};
 
 #define REALM_API extern "C" __attribute__((visibility("default")))
 
@@ -512,14 +516,28 @@ struct LoraCall {
 
 // --------------------------------------------------------------- dispatch
 
+// The decoder layer's step before a one-token product, fused into the
+// GEMV's x staging (gemv.hip "_n" and "_s" kernels): mode 1, RMSNorm of
+// x + a (a may be null) times w, x + a written to sum by workgroup 0 (sum
+// may be null); mode 2, SwiGLU of gate = x and up = a.
+struct GemvPre {
+    int mode = 0;
+    const float *a = nullptr;
+    const float *w = nullptr;
+    float *sum = nullptr;
+    float eps = 0.f;
+};
+
 // M = 1..4 tokens, f32 activations: the integer-dot GEMV over 1..4
 // matrices of one format that share x (rows concatenated); 2 tokens run the
 // 2-token kernels, 3 and 4 the 4-token ones (every weight load serves all of
 // them).  Returns BACKEND_UNSUPPORTED when the row is too long for the
 // kernel's register budget or the quantized x of all tokens does not fit in
-// LDS (the caller then uses the MFMA path).
+// LDS (the caller then uses the MFMA path), and, with a fused pre-step
+// (one token of Q4_K, Q6_K or Q8_0, SwiGLU on one matrix), before any
+// launch when the fused kernels cannot take the call.
 int run_gemv(const Weight *const *ws, int count, const float *d_x, int M, float *const *d_y,
-             hipStream_t s)
+             hipStream_t s, const GemvPre *pre = nullptr)
 {
     const Weight &w = *ws[0];
     int U = (int)(w.kx / 64);
@@ -527,12 +545,22 @@ int run_gemv(const Weight *const *ws, int count, const float *d_x, int M, float 
     int upl = (U + lpr - 1) / lpr;
     const int rpp = 64 / lpr;
     const int nt = M <= 1 ? 1 : (M == 2 ? 2 : 4);
+    const int pmode = pre ? pre->mode : 0;
     // per token: 8 x records + up to 2 meta float4 per unit; then one flag
     // word per token (its x needs the exact path)
     size_t lds = (size_t)U * 16 * 10 * nt + 16;
-    if (M < 1 || M > 4 || upl > 8 || lds > g_dev.max_lds || count < 1 ||
+    if (M < 1 || M > 4 || upl > 8 || lds + (pmode ? 64 : 0) > g_dev.max_lds || count < 1 ||
         count > REALM_GEMV_MAX_MATS)
         return REALM_BACKEND_UNSUPPORTED;
+    if (pmode) {
+        bool ok = M == 1 && (pmode == 1 || count == 1);
+        for (int i = 0; i < count; ++i)
+            ok = ok && (ws[i]->type == GGML_Q4_K || ws[i]->type == GGML_Q6_K ||
+                        ws[i]->type == GGML_Q8_0) &&
+                 ws[i]->type == w.type && ws[i]->n % rpp == 0;
+        if (!ok)
+            return REALM_BACKEND_UNSUPPORTED;
+    }
     // A grouped launch needs every matrix to start on a pass boundary;
     // otherwise the matrices go one launch each.
     for (int i = 0; count > 1 && i < count; ++i)
@@ -560,6 +588,12 @@ int run_gemv(const Weight *const *ws, int count, const float *d_x, int M, float 
     a.KX = (int)w.kx;
     a.nan_fb = g_nan_fb.load();
     a.m = M;
+    if (pmode) {
+        a.pre_a = pre->a;
+        a.pre_w = pre->w;
+        a.pre_sum = pre->sum;
+        a.pre_eps = pre->eps;
+    }
     // At most one workgroup per CU (each stages x in its LDS); each wave
     // keeps a ring of D passes in flight, D the smallest variant that holds
     // all of the wave's passes (so the whole weight stream is requested
@@ -613,7 +647,14 @@ int run_gemv(const Weight *const *ws, int count, const float *d_x, int M, float 
             if (ds[i] == v && !(is_block32(w.type) && v > 3))
                 d = v;
     }
+    if (pmode) // the fused kernels' ring depths (gemv.hip DEF_GEMV_PRE)
+        d = std::min(d, upl == 1 ? 3 : upl <= 3 ? 2 : 1);
     const int threads = threads_of(d);
+    if (pmode == 1) { // the norm needs every round of x in registers (GEMV_XR)
+        const int xr = std::min((512 * upl + threads - 1) / threads, 8);
+        if ((8 * U + threads - 1) / threads > xr)
+            return REALM_BACKEND_UNSUPPORTED;
+    }
     const int wpb = threads / 64;
     long wgs = std::min<long>(cu, (npass + wpb - 1) / wpb);
     if (const char *env = getenv("REALM_GEMV_WGS")) { // tuning override
@@ -621,10 +662,14 @@ int run_gemv(const Weight *const *ws, int count, const float *d_x, int M, float 
         if (v >= 1 && v <= 16 * cu)
             wgs = v;
     }
+    // the fused norm kernels take the grouped form (any count), SwiGLU the
+    // single one
+    const bool m4 = pmode == 1 || (pmode == 0 && count > 1);
     std::string name = std::string("realm_gemv_") + fmt_name(w.type) + "_l" +
                        std::to_string(lpr) + "_u" + std::to_string(upl) + "_d" +
-                       std::to_string(d) + "_m" + (count == 1 ? "1" : "4") +
-                       (nt == 1 ? "" : "_t" + std::to_string(nt));
+                       std::to_string(d) + "_m" + (m4 ? "4" : "1") +
+                       (nt == 1 ? "" : "_t" + std::to_string(nt)) +
+                       (pmode == 1 ? "_n" : pmode == 2 ? "_s" : "");
     void *args[] = {&a};
     return launch(name, dim3((unsigned)std::max<long>(wgs, 1)), dim3(threads), lds, s, args);
 }
@@ -1732,15 +1777,36 @@ int layer_steps(const realm_layer *L, const int type[7], const float *x, const f
     float *normed = ws, *q = ws + sh, *att = ws + 2 * sh, *o = ws + 3 * sh, *gate = ws + 4 * sh,
           *up = ws + 4 * sh + si;
     float *k_rows = kc + position * kv_dim, *v_rows = vc + position * kv_dim;
-    const float *h = x;
-    if (x_res) {
-        CHECK(realm_hip_rms_norm_dev(x, x_res, L->attn_norm, L->rms_norm_eps, seq_len, H, h_in,
-                                     normed, s));
-        h = h_in;
-    } else {
-        CHECK(realm_hip_rms_norm_dev(x, nullptr, L->attn_norm, L->rms_norm_eps, seq_len, H,
-                                     nullptr, normed, s));
-    }
+    const float *h = x_res ? h_in : x;
+    // One-token calls fuse each RMSNorm into the x staging of the grouped
+    // GEMV after it (Q/K/V, gate/up) and SwiGLU into W_down's, for
+    // projections without adapters whose matrices share a Q4_K, Q6_K or Q8_0
+    // format (REALM_LAYER_FUSE=0 keeps the separate launches).  run_gemv
+    // refuses before launching anything when its fused kernels cannot take
+    // the call; then the separate launches run.
+    const char *fenv = getenv("REALM_LAYER_FUSE");
+    const bool fuse = seq_len == 1 && !(fenv && fenv[0] == '0') && aligned16(L->attn_norm) &&
+                      aligned16(L->ffn_norm);
+    auto fused = [&](const uint64_t *hs, const uint64_t *sets, int n, const float *in,
+                     float *const *out, const GemvPre &pre, bool *done) {
+        *done = false;
+        if (!fuse || !aligned16(in) || (pre.a && !aligned16(pre.a)) ||
+            (pre.sum && !aligned16(pre.sum)))
+            return (int)REALM_OK;
+        Weight w[REALM_GEMV_MAX_MATS];
+        const Weight *wp[REALM_GEMV_MAX_MATS];
+        for (int i = 0; i < n; ++i) {
+            if (sets[i])
+                return (int)REALM_OK;
+            CHECK(get_weight(hs[i], &w[i]));
+            wp[i] = &w[i];
+        }
+        const int rc = run_gemv(wp, n, in, 1, out, s, &pre);
+        if (rc == REALM_BACKEND_UNSUPPORTED)
+            return (int)REALM_OK;
+        *done = rc == REALM_OK;
+        return rc;
+    };
     // matrices of one format share a grouped product (GGUF quant mixes
     // often keep V or up in Q6_K: then separate products); with adapter sets
     // on every member, one grouped multi-LoRA product, on some of them, one
@@ -1770,7 +1836,19 @@ int layer_steps(const realm_layer *L, const int type[7], const float *x, const f
     const uint64_t qkv[3] = {L->wq, L->wk, L->wv};
     const uint64_t qkv_sets[3] = {L->lora_q, L->lora_k, L->lora_v};
     float *const qkv_out[3] = {q, k_rows, v_rows};
-    CHECK(products(qkv, qkv_sets, type, qkv_out, 3));
+    bool done = false;
+    GemvPre norm1;
+    norm1.mode = 1;
+    norm1.a = x_res;
+    norm1.w = L->attn_norm;
+    norm1.sum = x_res ? h_in : nullptr;
+    norm1.eps = L->rms_norm_eps;
+    CHECK(fused(qkv, qkv_sets, 3, x, qkv_out, norm1, &done));
+    if (!done) {
+        CHECK(realm_hip_rms_norm_dev(x, x_res, L->attn_norm, L->rms_norm_eps, seq_len, H,
+                                     x_res ? h_in : nullptr, normed, s));
+        CHECK(products(qkv, qkv_sets, type, qkv_out, 3));
+    }
     { // RoPE of Q and of this call's K rows in one launch
         int iq = (int)heads, ik = (int)kvh, is = (int)seq_len, id = (int)hd, ip = (int)position;
         float theta = L->rope_theta;
@@ -1782,11 +1860,29 @@ int layer_steps(const realm_layer *L, const int type[7], const float *x, const f
     CHECK(realm_hip_attention_dev(q, kc, vc, seq_len, position + seq_len, position, heads, kvh,
                                   hd, att, s));
     CHECK(one(L->wo, L->lora_o, att, o));
-    CHECK(realm_hip_rms_norm_dev(h, o, L->ffn_norm, L->rms_norm_eps, seq_len, H, h2, normed, s));
     const uint64_t gu[2] = {L->w_gate, L->w_up};
     const uint64_t gu_sets[2] = {L->lora_gate, L->lora_up};
     float *const gu_out[2] = {gate, up};
-    CHECK(products(gu, gu_sets, type + 4, gu_out, 2));
+    GemvPre norm2;
+    norm2.mode = 1;
+    norm2.a = o;
+    norm2.w = L->ffn_norm;
+    norm2.sum = h2;
+    norm2.eps = L->rms_norm_eps;
+    CHECK(fused(gu, gu_sets, 2, h, gu_out, norm2, &done));
+    if (!done) {
+        CHECK(realm_hip_rms_norm_dev(h, o, L->ffn_norm, L->rms_norm_eps, seq_len, H, h2, normed,
+                                     s));
+        CHECK(products(gu, gu_sets, type + 4, gu_out, 2));
+    }
+    const uint64_t dn[1] = {L->w_down}, dn_sets[1] = {L->lora_down};
+    float *const dn_out[1] = {down};
+    GemvPre act;
+    act.mode = 2;
+    act.a = up;
+    CHECK(fused(dn, dn_sets, 1, gate, dn_out, act, &done));
+    if (done)
+        return REALM_OK;
     CHECK(realm_hip_swiglu_dev(gate, up, seq_len * I, gate, s));
     return one(L->w_down, L->lora_down, gate, down);
 }

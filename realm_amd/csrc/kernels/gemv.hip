@@ -454,9 +454,55 @@ REALM_DEV void unit_dot(const Unit<FMT> &w, const XR &xr, const XM &xm, int u, i
 // weight a lane loads is used for all NT tokens; token t's quantized x is
 // the LDS region of TS = 10 U int4 starting at t TS (8 U records, then up
 // to 2 U metadata float4).
-template <int FMT, int LPR, int UPL, int D, int XR, int TH, int NM, int NT>
+// The fused pre-steps of the one-token "_n" / "_s" kernels (GemvArgs):
+// element k of x' from the inputs, in the operation order of realm_rms_norm
+// ((x + r) * inv * w) and realm_swiglu (g * (1 / (1 + exp(-g))) * u), so a
+// fused product sees the values the separate launches would have written.
+#define PRE_NONE 0
+#define PRE_NORM 1
+#define PRE_SWIGLU 2
+REALM_DEV float4 pre_swiglu(float4 g, float4 u)
+{
+    return make_float4(g.x * (1.f / (1.f + expf(-g.x))) * u.x, g.y * (1.f / (1.f + expf(-g.y))) * u.y,
+                       g.z * (1.f / (1.f + expf(-g.z))) * u.z, g.w * (1.f / (1.f + expf(-g.w))) * u.w);
+}
+REALM_DEV float4 pre_norm(float4 v, float inv, float4 w)
+{
+    return make_float4(v.x * inv * w.x, v.y * inv * w.y, v.z * inv * w.z, v.w * inv * w.w);
+}
+REALM_DEV float4 f4add(float4 a, float4 b)
+{
+    return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+}
+
+// exact_dot over x' of a fused kernel (the exact f32 path of a flagged row)
+template <int FMT, int PRE>
+REALM_DEV float exact_dot_pre(const void *w0, const void *w1, const void *w2, int row, int K,
+                              int KX, const float *x, const float *pa, const float *pw, float inv,
+                              int nan_fb, int k0, int step)
+{
+#pragma clang fp contract(off)
+    float acc = 0.f;
+    for (int k = k0; k < K; k += step) {
+        float v;
+        if constexpr (PRE == PRE_NORM) {
+            const float h = pa ? x[k] + pa[k] : x[k];
+            v = h * inv * pw[k];
+        } else {
+            const float g = x[k];
+            v = g * (1.f / (1.f + expf(-g))) * pa[k];
+        }
+        acc += dev_weight<FMT>((const uint8_t *)w0, (const uint8_t *)w1, (const uint8_t *)w2, row,
+                               k, KX, nan_fb) *
+               v;
+    }
+    return acc;
+}
+
+template <int FMT, int LPR, int UPL, int D, int XR, int TH, int NM, int NT, int PRE = PRE_NONE>
 REALM_DEV void gemv(const GemvArgs &a)
 {
+    static_assert(PRE == PRE_NONE || NT == 1, "the fused pre-steps are one-token kernels");
     using W = Unit<FMT>;
     extern __shared__ int4 lds[];
     const int K = a.K, KX = a.KX;
@@ -487,6 +533,7 @@ REALM_DEV void gemv(const GemvArgs &a)
     const float *const xp = a.x;
     const int nan_fb = a.nan_fb;
     int xbad = 0; // bit t: token t's x needs the exact path (set after staging)
+    float pre_inv = 0.f; // _n: 1 / sqrt(mean((x + r)^2) + eps) (workgroup-uniform)
     // Every kernel argument is read here, in one batch of scalar loads ahead
     // of the first vector load (one statement, so all are live at once):
     // left alone, the compiler sinks some of these loads next to their uses,
@@ -599,10 +646,15 @@ REALM_DEV void gemv(const GemvArgs &a)
             const void *e2 = m == 0 ? w2[0] : (m == 1 ? w2[1] : (m == 2 ? w2[2] : w2[3]));
 #pragma unroll
             for (int t = 0; t < NT; ++t)
-                if ((xbad >> t) & 1)
-                    v[t] = group_total<LPR>(exact_dot<FMT>(e0, e1, e2, lr, K, KX,
-                                                           xp + (size_t)min(t, M - 1) * K, 0,
-                                                           nan_fb, l, LPR));
+                if ((xbad >> t) & 1) {
+                    if constexpr (PRE == PRE_NONE)
+                        v[t] = group_total<LPR>(exact_dot<FMT>(e0, e1, e2, lr, K, KX,
+                                                               xp + (size_t)min(t, M - 1) * K, 0,
+                                                               nan_fb, l, LPR));
+                    else
+                        v[t] = group_total<LPR>(exact_dot_pre<FMT, PRE>(
+                            e0, e1, e2, lr, K, KX, xp, a.pre_a, a.pre_w, pre_inv, nan_fb, l, LPR));
+                }
         }
         if (l == LPR - 1 && row < rows) {
             float *y = yv[0];
@@ -635,6 +687,19 @@ REALM_DEV void gemv(const GemvArgs &a)
 #pragma unroll
         for (int rd = 0; rd < XH; ++rd)
             x_round<TH>(xp + (size_t)min(t, M - 1) * K, K, U, rd, xv[t][rd]);
+    // the fused pre-step's other inputs (residual or up; the norm weight),
+    // loaded with x (the host only fuses a norm whose rounds all fit XH)
+    constexpr int PXH = PRE == PRE_NONE ? 1 : XH;
+    float4 pav[PXH][2], pwv[PXH][2];
+    if constexpr (PRE != PRE_NONE) {
+#pragma unroll
+        for (int rd = 0; rd < XH; ++rd) {
+            if (PRE == PRE_SWIGLU || a.pre_a)
+                x_round<TH>(a.pre_a, K, U, rd, pav[rd]);
+            if (PRE == PRE_NORM)
+                x_round<TH>(a.pre_w, K, U, rd, pwv[rd]);
+        }
+    }
     if (threadIdx.x < NT)
         xflag[threadIdx.x] = 0;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
@@ -649,6 +714,51 @@ REALM_DEV void gemv(const GemvArgs &a)
     __builtin_amdgcn_sched_barrier(0);
     W w[D][UPL];
     load_pass(w[0], 0);
+    if constexpr (PRE == PRE_SWIGLU) {
+#pragma unroll
+        for (int rd = 0; rd < XH; ++rd)
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+                xv[0][rd][c] = pre_swiglu(xv[0][rd][c], pav[rd][c]);
+    } else if constexpr (PRE == PRE_NORM) {
+        // h = x + r (written out once, by workgroup 0), its sum of squares
+        // over the workgroup (every workgroup the same), then h inv w
+        float ss = 0.f;
+#pragma unroll
+        for (int rd = 0; rd < XH; ++rd) {
+            const int e0 = 8 * (rd * TH + (int)threadIdx.x);
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                float4 hv = xv[0][rd][c];
+                if (a.pre_a)
+                    hv = f4add(hv, pav[rd][c]);
+                xv[0][rd][c] = hv;
+                ss += hv.x * hv.x + hv.y * hv.y + hv.z * hv.z + hv.w * hv.w;
+            }
+            if (a.pre_sum && blockIdx.x == 0 && rd < rounds && e0 < K) {
+                float4 *o = reinterpret_cast<float4 *>(a.pre_sum + e0);
+                o[0] = xv[0][rd][0];
+                o[1] = xv[0][rd][1];
+            }
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1)
+            ss += __shfl_xor(ss, off, 64);
+        __shared__ float pre_red[TH / 64];
+        if ((threadIdx.x & 63) == 0)
+            pre_red[threadIdx.x >> 6] = ss;
+        lds_barrier();
+        float total = 0.f;
+#pragma unroll
+        for (int wv = 0; wv < TH / 64; ++wv)
+            total += pre_red[wv];
+        pre_inv = 1.f / sqrtf(total / (float)K + a.pre_eps);
+#pragma unroll
+        for (int rd = 0; rd < XH; ++rd)
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+                xv[0][rd][c] = pre_norm(xv[0][rd][c], pre_inv, pwv[rd][c]);
+    }
 #pragma unroll
     for (int t = 0; t < NT; ++t)
 #pragma unroll
@@ -660,6 +770,12 @@ REALM_DEV void gemv(const GemvArgs &a)
         for (int rd = XH; rd < rounds; ++rd) {
             float4 v[2];
             x_round<TH>(xp + (size_t)min(t, M - 1) * K, K, U, rd, v);
+            if constexpr (PRE == PRE_SWIGLU) { // (a fused norm has no rounds here)
+                float4 u[2];
+                x_round<TH>(a.pre_a, K, U, rd, u);
+                v[0] = pre_swiglu(v[0], u[0]);
+                v[1] = pre_swiglu(v[1], u[1]);
+            }
             quant_round<FMT, TH>(rec + t * TS, meta + t * TS, xflag + t, v, U, rd);
         }
     lds_barrier();
@@ -737,24 +853,42 @@ REALM_DEV void gemv(const GemvArgs &a)
 
 // Variant: lanes per row, units per lane, ring depth, matrices (1 or 4),
 // tokens (the one-token kernels carry no token suffix).
-#define DEF_GEMV1(NAME, FMT, LPR, UPL, D, NM, NT, SUF)                                       \
+#define DEF_GEMV1P(NAME, FMT, LPR, UPL, D, NM, NT, SUF, PRE)                                 \
     extern "C" __global__ __launch_bounds__(GEMV_THN(UPL, D, NT)) void                       \
         realm_gemv_##NAME##_l##LPR##_u##UPL##_d##D##_m##NM##SUF(GemvArgs a)                  \
     {                                                                                        \
         gemv<FMT, LPR, UPL, D, GEMV_XR(UPL, GEMV_THN(UPL, D, NT)), GEMV_THN(UPL, D, NT), NM,  \
-             NT>(a);                                                                          \
+             NT, PRE>(a);                                                                     \
     }
+#define DEF_GEMV1(NAME, FMT, LPR, UPL, D, NM, NT, SUF)                                       \
+    DEF_GEMV1P(NAME, FMT, LPR, UPL, D, NM, NT, SUF, PRE_NONE)
 #if REALM_GEMV_FMT == FMT_Q4K
 #define DEF_GEMV2(LPR, UPL, D, NM, NT, SUF) DEF_GEMV1(q4k, FMT_Q4K, LPR, UPL, D, NM, NT, SUF)
+#define DEF_GEMVP(LPR, UPL, D, NM, SUF, PRE) DEF_GEMV1P(q4k, FMT_Q4K, LPR, UPL, D, NM, 1, SUF, PRE)
 #elif REALM_GEMV_FMT == FMT_Q6K
 #define DEF_GEMV2(LPR, UPL, D, NM, NT, SUF) DEF_GEMV1(q6k, FMT_Q6K, LPR, UPL, D, NM, NT, SUF)
+#define DEF_GEMVP(LPR, UPL, D, NM, SUF, PRE) DEF_GEMV1P(q6k, FMT_Q6K, LPR, UPL, D, NM, 1, SUF, PRE)
 #elif REALM_GEMV_FMT == FMT_Q80
 #define DEF_GEMV2(LPR, UPL, D, NM, NT, SUF) DEF_GEMV1(q80, FMT_Q80, LPR, UPL, D, NM, NT, SUF)
+#define DEF_GEMVP(LPR, UPL, D, NM, SUF, PRE) DEF_GEMV1P(q80, FMT_Q80, LPR, UPL, D, NM, 1, SUF, PRE)
 #else
 #define DEF_GEMV2(LPR, UPL, D, NM, NT, SUF) DEF_GEMV1(q8m, FMT_Q8M, LPR, UPL, D, NM, NT, SUF)
 #endif
 
-#if !defined(REALM_GEMV_NT) || REALM_GEMV_NT == 1
+#if defined(REALM_GEMV_PRE)
+// The decoder layer's fused one-token kernels: "_n" (RMSNorm before the
+// product; grouped Q/K/V and gate/up, NM = 4) and "_s" (SwiGLU; W_down,
+// NM = 1), in the ring depths the host picks for them (1-3 for one unit per
+// lane, 1-2 for two or three, 1 beyond).
+#define DEF_GEMV_PRE(LPR, UPL, D) DEF_GEMVP(LPR, UPL, D, 4, _n, PRE_NORM) DEF_GEMVP(LPR, UPL, D, 1, _s, PRE_SWIGLU)
+DEF_GEMV_PRE(16, 1, 1) DEF_GEMV_PRE(16, 1, 2) DEF_GEMV_PRE(16, 1, 3)
+DEF_GEMV_PRE(32, 1, 1) DEF_GEMV_PRE(32, 1, 2) DEF_GEMV_PRE(32, 1, 3)
+DEF_GEMV_PRE(64, 1, 1) DEF_GEMV_PRE(64, 1, 2) DEF_GEMV_PRE(64, 1, 3)
+DEF_GEMV_PRE(64, 2, 1) DEF_GEMV_PRE(64, 2, 2)
+DEF_GEMV_PRE(64, 3, 1) DEF_GEMV_PRE(64, 3, 2)
+DEF_GEMV_PRE(64, 4, 1) DEF_GEMV_PRE(64, 5, 1) DEF_GEMV_PRE(64, 6, 1) DEF_GEMV_PRE(64, 7, 1)
+DEF_GEMV_PRE(64, 8, 1)
+#elif !defined(REALM_GEMV_NT) || REALM_GEMV_NT == 1
 #define DEF_GEMV(LPR, UPL, D) DEF_GEMV2(LPR, UPL, D, 1, 1, ) DEF_GEMV2(LPR, UPL, D, 4, 1, )
 
 // The one-token variants the host chooses from (ring depths per

@@ -115,6 +115,15 @@ struct GemvArgs {
     int32_t K, KX;
     int32_t nan_fb;
     int32_t m; // tokens (rows of x and of each y); 1 for the one-token kernels
+    // The decoder layer's step before the product, fused into the x staging
+    // of the one-token "_n" and "_s" kernels (unused by the others):
+    //   _n: x' = RMSNorm(x + pre_a) * pre_w (pre_a may be null), with
+    //       x + pre_a written to pre_sum by workgroup 0 when pre_sum is set;
+    //   _s: x' = SwiGLU(gate = x, up = pre_a).
+    const float *pre_a;
+    const float *pre_w;
+    float *pre_sum;
+    float pre_eps;
 };
 
 #ifdef __cplusplus

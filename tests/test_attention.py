@@ -159,13 +159,17 @@ def test_kv_append_then_attention(backend):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("fuse", ["1", "0"])
 @pytest.mark.parametrize("mixed", [False, True])
-def test_forward_layer(backend, oracle, mixed):
+def test_forward_layer(backend, oracle, monkeypatch, mixed, fuse):
     """realm_hip_forward_layer_dev against the oracle's composition of the
     reference's steps: a 5-token prefill from an empty cache, a 1-token and
     a 3-token decode after it (the GEMV and MFMA product paths), and a call
     that would overflow the cache.  mixed: V and up in Q6_K (separate
-    products), otherwise every projection in Q4_K (grouped products)."""
+    products), otherwise every projection in Q4_K (grouped products).  The
+    1-token call runs with the norms and SwiGLU fused into the GEMVs
+    (fuse "1", where the formats allow) and as separate launches ("0")."""
+    monkeypatch.setenv("REALM_LAYER_FUSE", fuse)
     from realm_amd import synth
     from realm_amd.backend import RealmError, RealmLayer
     from realm_amd.formats import GGML_Q4_K, GGML_Q6_K
@@ -238,10 +242,14 @@ def test_forward_layer(backend, oracle, mixed):
 
 
 @pytest.mark.gpu
-def test_forward_layers_chain(backend, oracle):
+@pytest.mark.parametrize("fuse", ["1", "0"])
+def test_forward_layers_chain(backend, oracle, monkeypatch, fuse):
     """Three layers in one realm_hip_forward_layers_dev call (the residual add
     fused into the next layer's first norm) against three oracle layers
-    applied in turn, for a 4-token prefill and a 1-token decode after it."""
+    applied in turn, for a 4-token prefill and a 1-token decode after it
+    (fuse "1": the decode's norms, residual adds and SwiGLU inside the
+    GEMVs; "0": separate launches)."""
+    monkeypatch.setenv("REALM_LAYER_FUSE", fuse)
     from realm_amd import synth
     from realm_amd.backend import RealmLayer
     from realm_amd.formats import GGML_Q4_K, GGML_Q6_K
@@ -430,3 +438,76 @@ def test_attention_long_cache(backend, seq, kv):
             b.close()
     want = oa.attention(q, k, v, seq, kv, pos, heads, kvh, hd)
     assert rel_l2(got, want) < 1e-5
+
+
+@pytest.mark.gpu
+def test_forward_layer_7b_decode_fused(backend, oracle, monkeypatch):
+    """One LLaMA-7B-shape layer (hidden 4096, 32 heads of 128, intermediate
+    11008; Q4_K projections, Q6_K W_down), the decode step bench.py times:
+    a 2-token prefill, then one token with the norms and SwiGLU fused into
+    the GEMVs' x staging (the l64 u1 "_n" kernels for Q/K/V and gate/up, the
+    u3 "_s" kernel for W_down) and the same token through the separate
+    launches, both against the oracle's composition."""
+    from realm_amd import synth
+    from realm_amd.backend import RealmLayer
+    from realm_amd.formats import GGML_Q4_K, GGML_Q6_K
+    H, heads, kvh, hd, inter, max_len = 4096, 32, 32, 128, 11008, 4
+    kv_dim = kvh * hd
+    cfg = {"hidden": H, "heads": heads, "kv_heads": kvh, "head_dim": hd, "eps": 1e-5,
+           "theta": 10000.0}
+    shapes = {"wq": (H, H), "wk": (kv_dim, H), "wv": (kv_dim, H), "wo": (H, H),
+              "w_gate": (inter, H), "w_up": (inter, H), "w_down": (H, inter)}
+    types = {n: (GGML_Q6_K if n == "w_down" else GGML_Q4_K) for n in shapes}
+    g = synth.rng(4096)
+    blocks = {n: synth.blocks(g, types[n], *shapes[n]) for n in shapes}
+    for b in blocks.values():
+        b["d"] = (b["d"].view(np.float16) * np.float16(8)).view(np.uint16)
+    hs = {n: backend.register_weights(types[n], blocks[n], *shapes[n]) for n in shapes}
+    norms = {"attn": (1 + 0.1 * g.standard_normal(H)).astype(np.float32),
+             "ffn": (1 + 0.1 * g.standard_normal(H)).astype(np.float32)}
+    dn = {k: backend.alloc(v.nbytes).upload(v) for k, v in norms.items()}
+    layer = RealmLayer(wq=hs["wq"], wk=hs["wk"], wv=hs["wv"], wo=hs["wo"], w_gate=hs["w_gate"],
+                       w_up=hs["w_up"], w_down=hs["w_down"], attn_norm=dn["attn"].ptr,
+                       ffn_norm=dn["ffn"].ptr, hidden=H, num_heads=heads, num_kv_heads=kvh,
+                       head_dim=hd, intermediate=inter, rms_norm_eps=1e-5, rope_theta=10000.0)
+
+    def matmul(name, x, m):
+        n, k = shapes[name]
+        rc, y = oracle.candle_fused(types[name], blocks[name], np.ascontiguousarray(x), m, n, k)
+        assert rc == 0
+        return y.reshape(m, n)
+
+    kc_ref = np.zeros(max_len * kv_dim, np.float32)
+    vc_ref = np.zeros(max_len * kv_dim, np.float32)
+    dkc, dvc = backend.alloc(kc_ref.nbytes), backend.alloc(vc_ref.nbytes)
+    bufs = []
+    try:
+        x0 = g.standard_normal((2, H)).astype(np.float32)
+        dx = backend.alloc(x0.nbytes).upload(x0)
+        dy = backend.alloc(x0.nbytes)
+        bufs += [dx, dy]
+        backend.forward_layer_dev(layer, dx.ptr, 2, 0, dkc.ptr, dvc.ptr, max_len, dy.ptr)
+        oa.forward_layer(matmul, x0, blocks, norms, cfg, kc_ref, vc_ref, 0, 2)
+        x1 = g.standard_normal((1, H)).astype(np.float32)
+        want = oa.forward_layer(matmul, x1, blocks, norms, cfg, kc_ref.copy(), vc_ref.copy(), 2, 1)
+        d1 = backend.alloc(x1.nbytes).upload(x1)
+        bufs.append(d1)
+        outs = {}
+        for fuse in ("1", "0"):
+            monkeypatch.setenv("REALM_LAYER_FUSE", fuse)
+            do = backend.alloc(x1.nbytes)
+            bufs.append(do)
+            # the same cache position both times: the step rewrites its K/V row
+            backend.forward_layer_dev(layer, d1.ptr, 1, 2, dkc.ptr, dvc.ptr, max_len, do.ptr)
+            backend.synchronize()
+            outs[fuse] = do.download(np.float32, H).reshape(1, H)
+            err = rel_l2(outs[fuse], want)
+            delta = rel_l2(outs[fuse] - x1, want - x1)
+            print(f"7b decode fuse={fuse} rel_l2={err:.3e} delta={delta:.3e}")
+            assert err < 1e-3 and delta < 1e-3, fuse
+        assert rel_l2(outs["1"], outs["0"]) < 1e-5
+    finally:
+        for h in hs.values():
+            backend.release_weights(h)
+        for b in list(dn.values()) + [dkc, dvc] + bufs:
+            b.close()
