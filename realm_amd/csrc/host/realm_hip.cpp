@@ -1598,6 +1598,58 @@ REALM_API int realm_hip_rope_dev(float *d_x, size_t seq_len, size_t num_heads, s
     return launch("realm_rope", dim3((unsigned)((pairs + 255) / 256)), dim3(256), 0, s, args);
 }
 
+namespace {
+// Key splits of a decode attention: small grids split the keys of each
+// (token, head) over up to 16 workgroups of at least 64 keys; any cache
+// length takes at least as many splits as keep a chunk's scores in LDS.
+size_t att_splits(size_t seq_len, size_t kv_len, size_t num_heads, size_t head_dim)
+{
+    size_t splits = 1;
+    if (seq_len * num_heads < 2 * (size_t)g_dev.cu_count && kv_len >= 256)
+        splits = std::min<size_t>({16, (2 * (size_t)g_dev.cu_count + seq_len * num_heads - 1) /
+                                           (seq_len * num_heads),
+                                   (kv_len + 63) / 64});
+    if (const char *env = getenv("REALM_ATT_SPLITS")) { // tuning / test override
+        const long v = atol(env);
+        if (v >= 1 && v <= 64)
+            splits = (size_t)v;
+    }
+    const size_t att_threads = 1024; // ATT_TH in layer_ops.hip
+    const size_t max_chunk = g_dev.max_lds / sizeof(float) - head_dim - 256 - 16;
+    if ((head_dim + kv_len + att_threads) * sizeof(float) + 64 > g_dev.max_lds)
+        splits = std::max(splits, (kv_len + max_chunk - 1) / max_chunk);
+    return splits;
+}
+
+// The split attention of a one-token decode step with RoPE fused in
+// (realm_attention_split_rope): q and this step's key row k_new arrive
+// unrotated; the kernel rotates them by the (cos, sin) table of the step's
+// position (realm_rope_table) and writes the rotated row into the cache at
+// `position`.  The caller checked the arguments and that att_splits() > 1.
+int attention_rope_run(const float *d_q, float *d_k_cache, const float *d_v_cache,
+                       const float *k_new, size_t kv_len, size_t position, size_t num_heads,
+                       size_t num_kv_heads, size_t head_dim, const void *rope_cs, float *d_out,
+                       hipStream_t s)
+{
+    const size_t splits = att_splits(1, kv_len, num_heads, head_dim);
+    const size_t chunk = (kv_len + splits - 1) / splits;
+    const size_t lds = (head_dim + chunk + 256) * sizeof(float);
+    if (splits < 2 || lds + 64 > g_dev.max_lds)
+        return fail(REALM_BACKEND_UNSUPPORTED, "attention: no split form for fused RoPE");
+    void *part = nullptr;
+    CHECK(ws_get(s, WS_ATT, num_heads * splits * (head_dim + 2) * sizeof(float), &part));
+    int ikv = (int)kv_len, ipos = (int)position, ih = (int)num_heads, ikh = (int)num_kv_heads,
+        id = (int)head_dim, isp = (int)splits, ich = (int)chunk;
+    float scale = 1.0f / std::sqrt((float)head_dim);
+    void *args[] = {(void *)&d_q, (void *)&d_k_cache, (void *)&d_v_cache, &ikv, &ipos, &ih,
+                    &ikh, &id, &scale, &isp, &ich, &part, (void *)&k_new, (void *)&rope_cs};
+    CHECK(launch("realm_attention_split_rope", dim3((unsigned)(num_heads * splits)), dim3(256),
+                 lds, s, args));
+    void *cargs[] = {&part, &isp, &id, &d_out};
+    return launch("realm_attention_combine", dim3((unsigned)num_heads), dim3(256), 0, s, cargs);
+}
+} // namespace
+
 REALM_API int realm_hip_attention_dev(const float *d_q, const float *d_k_cache,
                                       const float *d_v_cache, size_t seq_len, size_t kv_len,
                                       size_t position, size_t num_heads, size_t num_kv_heads,
@@ -1617,25 +1669,10 @@ REALM_API int realm_hip_attention_dev(const float *d_q, const float *d_k_cache,
         kv_len > (size_t)INT32_MAX || num_heads > (size_t)INT32_MAX)
         return fail(REALM_INVALID_ARGUMENT, "attention: sizes exceed 2^31-1");
     CHECK(ensure_init());
-    // Small grids (decode): split the keys of each (token, head) over up to
-    // 16 workgroups of at least 64 keys, then combine the partials.
-    size_t splits = 1;
-    if (seq_len * num_heads < 2 * (size_t)g_dev.cu_count && kv_len >= 256)
-        splits = std::min<size_t>({16, (2 * (size_t)g_dev.cu_count + seq_len * num_heads - 1) /
-                                           (seq_len * num_heads),
-                                   (kv_len + 63) / 64});
-    if (const char *env = getenv("REALM_ATT_SPLITS")) { // tuning / test override
-        const long v = atol(env);
-        if (v >= 1 && v <= 64)
-            splits = (size_t)v;
-    }
-    // Any cache length: when the scores of all visible keys do not fit in
-    // one workgroup's LDS, at least as many splits as keep every chunk's
-    // scores (plus q and the reduction slots) inside it.
+    // Small grids (decode) and long caches: the keys split over workgroups,
+    // then the partials combined (att_splits)
     const size_t att_threads = 1024; // ATT_TH in layer_ops.hip
-    const size_t max_chunk = g_dev.max_lds / sizeof(float) - head_dim - 256 - 16;
-    if ((head_dim + kv_len + att_threads) * sizeof(float) + 64 > g_dev.max_lds)
-        splits = std::max(splits, (kv_len + max_chunk - 1) / max_chunk);
+    const size_t splits = att_splits(seq_len, kv_len, num_heads, head_dim);
     if (splits > 1) {
         const size_t chunk = (kv_len + splits - 1) / splits;
         const size_t lds = (head_dim + chunk + 256) * sizeof(float);
@@ -1769,7 +1806,7 @@ int check_layer(const realm_layer *L, size_t seq_len, size_t position, size_t ma
 // the buffers x and x_res came in (both are consumed by the first norm).
 int layer_steps(const realm_layer *L, const int type[7], const float *x, const float *x_res,
                 size_t seq_len, size_t position, float *kc, float *vc, float *ws, float *h_in,
-                float *h2, float *down, hipStream_t s)
+                float *h2, float *down, const void *rope_cs, hipStream_t s)
 {
     const size_t H = L->hidden, heads = L->num_heads, kvh = L->num_kv_heads, hd = L->head_dim,
                  I = L->intermediate, kv_dim = kvh * hd;
@@ -1836,6 +1873,11 @@ int layer_steps(const realm_layer *L, const int type[7], const float *x, const f
     const uint64_t qkv[3] = {L->wq, L->wk, L->wv};
     const uint64_t qkv_sets[3] = {L->lora_q, L->lora_k, L->lora_v};
     float *const qkv_out[3] = {q, k_rows, v_rows};
+    // With the fused norm, `normed` is free: the new key row goes there
+    // unrotated and the split attention applies RoPE itself (and writes the
+    // rotated row into the cache), when the step runs the split form
+    const bool rope_fuse = fuse && rope_cs && att_splits(1, position + 1, heads, hd) > 1;
+    float *const qkv_fout[3] = {q, rope_fuse ? normed : k_rows, v_rows};
     bool done = false;
     GemvPre norm1;
     norm1.mode = 1;
@@ -1843,22 +1885,28 @@ int layer_steps(const realm_layer *L, const int type[7], const float *x, const f
     norm1.w = L->attn_norm;
     norm1.sum = x_res ? h_in : nullptr;
     norm1.eps = L->rms_norm_eps;
-    CHECK(fused(qkv, qkv_sets, 3, x, qkv_out, norm1, &done));
-    if (!done) {
-        CHECK(realm_hip_rms_norm_dev(x, x_res, L->attn_norm, L->rms_norm_eps, seq_len, H,
-                                     x_res ? h_in : nullptr, normed, s));
-        CHECK(products(qkv, qkv_sets, type, qkv_out, 3));
+    CHECK(fused(qkv, qkv_sets, 3, x, qkv_fout, norm1, &done));
+    if (done && rope_fuse) {
+        CHECK(attention_rope_run(q, kc, vc, normed, position + 1, position, heads, kvh, hd,
+                                 rope_cs, att, s));
+    } else {
+        if (!done) {
+            CHECK(realm_hip_rms_norm_dev(x, x_res, L->attn_norm, L->rms_norm_eps, seq_len, H,
+                                         x_res ? h_in : nullptr, normed, s));
+            CHECK(products(qkv, qkv_sets, type, qkv_out, 3));
+        }
+        { // RoPE of Q and of this call's K rows in one launch
+            int iq = (int)heads, ik = (int)kvh, is = (int)seq_len, id = (int)hd,
+                ip = (int)position;
+            float theta = L->rope_theta;
+            const size_t pairs = seq_len * (heads + kvh) * (hd / 2);
+            void *args[] = {&q, &iq, &k_rows, &ik, &is, &id, &ip, &theta};
+            CHECK(launch("realm_rope_qk", dim3((unsigned)((pairs + 255) / 256)), dim3(256), 0, s,
+                         args));
+        }
+        CHECK(realm_hip_attention_dev(q, kc, vc, seq_len, position + seq_len, position, heads,
+                                      kvh, hd, att, s));
     }
-    { // RoPE of Q and of this call's K rows in one launch
-        int iq = (int)heads, ik = (int)kvh, is = (int)seq_len, id = (int)hd, ip = (int)position;
-        float theta = L->rope_theta;
-        const size_t pairs = seq_len * (heads + kvh) * (hd / 2);
-        void *args[] = {&q, &iq, &k_rows, &ik, &is, &id, &ip, &theta};
-        CHECK(launch("realm_rope_qk", dim3((unsigned)((pairs + 255) / 256)), dim3(256), 0, s,
-                     args));
-    }
-    CHECK(realm_hip_attention_dev(q, kc, vc, seq_len, position + seq_len, position, heads, kvh,
-                                  hd, att, s));
     CHECK(one(L->wo, L->lora_o, att, o));
     const uint64_t gu[2] = {L->w_gate, L->w_up};
     const uint64_t gu_sets[2] = {L->lora_gate, L->lora_up};
@@ -1920,17 +1968,35 @@ REALM_API int realm_hip_forward_layers_dev(const realm_layer *layers, size_t n_l
     CHECK(ensure_init());
     hipStream_t s;
     CHECK(pick_stream(stream, &s));
-    // per-layer intermediates, then the chained h_in, h2 and down [seq][H]
+    // per-layer intermediates, then the chained h_in, h2 and down [seq][H],
+    // then the one-token step's rotation table
     const size_t sh = align256(seq_len * layers[0].hidden * 4);
+    const size_t hd0 = layers[0].head_dim;
     void *ws = nullptr;
-    CHECK(ws_get(s, WS_LAYER, wsize + 3 * sh, &ws));
+    CHECK(ws_get(s, WS_LAYER, wsize + 3 * sh + align256(hd0 * 4), &ws));
     uint8_t *base = static_cast<uint8_t *>(ws);
     float *h_in = (float *)(base + wsize), *h2 = (float *)(base + wsize + sh),
           *down = (float *)(base + wsize + 2 * sh);
-    for (size_t l = 0; l < n_layers; ++l)
+    // One token: the (cos, sin) of its position's rotary angles, once for
+    // every layer that shares layer 0's head_dim and theta (the fused
+    // decode attention reads them instead of evaluating them per layer)
+    void *rope_tab = nullptr;
+    const char *fenv = getenv("REALM_LAYER_FUSE");
+    if (seq_len == 1 && !(fenv && fenv[0] == '0') &&
+        att_splits(1, position + 1, layers[0].num_heads, hd0) > 1) {
+        rope_tab = base + wsize + 3 * sh;
+        int ihd = (int)hd0, ipos = (int)position;
+        float th = layers[0].rope_theta;
+        void *args[] = {&rope_tab, &ihd, &ipos, &th};
+        CHECK(launch("realm_rope_table", dim3((unsigned)((hd0 / 2 + 255) / 256)), dim3(256), 0, s,
+                     args));
+    }
+    for (size_t l = 0; l < n_layers; ++l) {
+        const bool same = layers[l].head_dim == hd0 && layers[l].rope_theta == layers[0].rope_theta;
         CHECK(layer_steps(&layers[l], &types[7 * l], l ? h2 : d_hidden, l ? down : nullptr,
                           seq_len, position, d_k_caches[l], d_v_caches[l], (float *)base, h_in,
-                          h2, down, s));
+                          h2, down, same ? rope_tab : nullptr, s));
+    }
     return realm_hip_add_dev(h2, down, seq_len * layers[0].hidden, d_out, s);
 }
 

@@ -96,6 +96,24 @@ extern "C" __global__ __launch_bounds__(256) void realm_swiglu(const float4 *gat
 // freq, in the reference's f32 operation order.  One thread per pair.
 namespace {
 
+// (cos, sin) of the angle of pair (x_i, x_{i+1}) at absolute position pos,
+// and the rotation by them: every rotation here goes through these two
+// functions, so the fused and separate forms agree.
+__device__ __forceinline__ float2 rope_cs(int i, int pos, int head_dim, float theta)
+{
+    const float freq = 1.0f / powf(theta, (float)i / (float)head_dim);
+    const float angle = (float)pos * freq;
+    return make_float2(cosf(angle), sinf(angle));
+}
+__device__ __forceinline__ float2 rope_apply(float2 a, float2 cs)
+{
+    return make_float2(a.x * cs.x - a.y * cs.y, a.x * cs.y + a.y * cs.x);
+}
+__device__ __forceinline__ float2 rope_rot(float2 a, int i, int pos, int head_dim, float theta)
+{
+    return rope_apply(a, rope_cs(i, pos, head_dim, theta));
+}
+
 // Pair p of x [seq][heads][head_dim] rotated in place.
 __device__ __forceinline__ void rope_pair(float *x, size_t p, int heads, int head_dim, int start,
                                           float theta)
@@ -103,12 +121,8 @@ __device__ __forceinline__ void rope_pair(float *x, size_t p, int heads, int hea
     const int half = head_dim >> 1;
     const int i = 2 * (int)(p % half);
     const int s = (int)(p / ((size_t)heads * half));
-    const float freq = 1.0f / powf(theta, (float)i / (float)head_dim);
-    const float angle = (float)(start + s) * freq;
-    const float c = cosf(angle), sn = sinf(angle);
     float2 *v = reinterpret_cast<float2 *>(x) + p;
-    const float2 a = *v;
-    *v = make_float2(a.x * c - a.y * sn, a.x * sn + a.y * c);
+    *v = rope_rot(*v, i, start + s, head_dim, theta);
 }
 
 } // namespace
@@ -123,6 +137,16 @@ extern "C" __global__ __launch_bounds__(256) void realm_rope(float *x, int seq, 
 }
 
 // Q and K of one layer in one launch: pairs of q first, then of k.
+// (cos, sin) of the head_dim / 2 pair angles at position pos (the fused
+// decode attention's rotations, once per step for every layer)
+extern "C" __global__ __launch_bounds__(256) void realm_rope_table(float2 *cs, int head_dim,
+                                                                   int pos, float theta)
+{
+    const int p = (int)(blockIdx.x * 256 + threadIdx.x);
+    if (p < (head_dim >> 1))
+        cs[p] = rope_cs(2 * p, pos, head_dim, theta);
+}
+
 extern "C" __global__ __launch_bounds__(256) void realm_rope_qk(float *q, int q_heads, float *k,
                                                                 int k_heads, int seq, int head_dim,
                                                                 int start, float theta)
@@ -284,9 +308,18 @@ extern "C" __global__ __launch_bounds__(256) void realm_add(const float4 *a, con
 // realm_attention_combine then forms m = max m_s, l = sum l_s e^(m_s - m),
 // out = sum acc_s e^(m_s - m) / l, splits in order.  256 threads; the
 // chunk's scores live in LDS.
-extern "C" __global__ __launch_bounds__(256) void realm_attention_split(
-    const float *q, const float *kc, const float *vc, int kv_len, int position, int heads,
-    int kv_heads, int head_dim, float scale, int splits, int chunk, float *part)
+// ROPE (the one-token decode step of the device layer): q arrives without
+// its rotary embedding and the new key row (absolute position `position`)
+// in k_new, also unrotated; both are rotated here by the (cos, sin) table of
+// that position (realm_rope_table: rope_pair's values), and the workgroup of
+// the first head of each KV group whose split holds that row writes the
+// rotated row into the cache.  No workgroup of the launch reads that cache
+// row: the row's keys come from k_new.
+template <bool ROPE>
+__device__ void attention_split(const float *q, float *kc, const float *vc, int kv_len,
+                                int position, int heads, int kv_heads, int head_dim, float scale,
+                                int splits, int chunk, float *part, const float *k_new,
+                                const float2 *rcs)
 {
     extern __shared__ float smem[];
     __shared__ float red[8];
@@ -298,19 +331,42 @@ extern "C" __global__ __launch_bounds__(256) void realm_attention_split(
     const int j0 = s * chunk, j1 = min(vis, j0 + chunk);
     const int n = max(j1 - j0, 0);
     const float *qr = q + ((size_t)t * heads + h) * head_dim;
-    for (int d = threadIdx.x; d < head_dim; d += 256)
-        qs[d] = qr[d];
+    if constexpr (ROPE) {
+        const int half = head_dim >> 1;
+        for (int pi = threadIdx.x; pi < half; pi += 256) { // (one token: t = 0)
+            const int i = 2 * pi;
+            const float2 r = rope_apply(make_float2(qr[i], qr[i + 1]), rcs[pi]);
+            qs[i] = r.x;
+            qs[i + 1] = r.y;
+        }
+        // the new key row: rotated into the cache once per KV head
+        if (t == 0 && h % (heads / kv_heads) == 0 && position >= j0 && position < j1) {
+            const float *kn = k_new + (size_t)kvh * head_dim;
+            float *kw = kc + (size_t)position * kv_dim + (size_t)kvh * head_dim;
+            for (int pi = threadIdx.x; pi < half; pi += 256) {
+                const int i = 2 * pi;
+                const float2 r = rope_apply(make_float2(kn[i], kn[i + 1]), rcs[pi]);
+                kw[i] = r.x;
+                kw[i + 1] = r.y;
+            }
+        }
+    } else {
+        for (int d = threadIdx.x; d < head_dim; d += 256)
+            qs[d] = qr[d];
+    }
     __syncthreads();
     const int lpk = head_dim >> 2, kpw = 64 / lpk;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int c = lane % lpk, sub = lane / lpk;
     const float4 q4 = reinterpret_cast<const float4 *>(qs)[c];
     float mx = -INFINITY;
-    for (int base = wave * kpw; base < n; base += 32 * kpw) {
+    // the cached keys (ROPE: all but the step's new row, scored below)
+    const int nc = ROPE ? max(min(j1, position) - j0, 0) : n;
+    for (int base = wave * kpw; base < nc; base += 32 * kpw) {
         float4 k4[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-            const int jc = j0 + min(base + u * 4 * kpw + sub, n - 1);
+            const int jc = j0 + min(base + u * 4 * kpw + sub, nc - 1);
             k4[u] = *reinterpret_cast<const float4 *>(kc + (size_t)jc * kv_dim +
                                                       (size_t)kvh * head_dim + 4 * c);
         }
@@ -321,10 +377,29 @@ extern "C" __global__ __launch_bounds__(256) void realm_attention_split(
             for (int off = lpk >> 1; off > 0; off >>= 1)
                 dot += __shfl_xor(dot, off, 64);
             const float sv = dot * scale;
-            if (c == 0 && jl < n) {
+            if (c == 0 && jl < nc) {
                 sc[jl] = sv;
                 mx = fmaxf(mx, sv);
             }
+        }
+    }
+    if (ROPE && wave == 0 && position >= j0 && position < j1) {
+        // the new row's score: its key from k_new, rotated; the same float4
+        // grouping and shuffle order as the cached keys'
+        float dot = 0.f;
+        if (lane < lpk) {
+            const float4 r = *reinterpret_cast<const float4 *>(
+                k_new + (size_t)kvh * head_dim + 4 * lane);
+            const float2 lo = rope_apply(make_float2(r.x, r.y), rcs[2 * lane]);
+            const float2 hi = rope_apply(make_float2(r.z, r.w), rcs[2 * lane + 1]);
+            dot = q4.x * lo.x + q4.y * lo.y + q4.z * hi.x + q4.w * hi.y;
+        }
+        for (int off = lpk >> 1; off > 0; off >>= 1)
+            dot += __shfl_xor(dot, off, 64);
+        if (lane == 0) {
+            const float sv = dot * scale;
+            sc[position - j0] = sv;
+            mx = fmaxf(mx, sv);
         }
     }
     __syncthreads();
@@ -372,6 +447,23 @@ extern "C" __global__ __launch_bounds__(256) void realm_attention_split(
         pr[0] = n > 0 ? mx : -INFINITY;
         pr[1] = n > 0 ? sum : 0.f;
     }
+}
+
+extern "C" __global__ __launch_bounds__(256) void realm_attention_split(
+    const float *q, const float *kc, const float *vc, int kv_len, int position, int heads,
+    int kv_heads, int head_dim, float scale, int splits, int chunk, float *part)
+{
+    attention_split<false>(q, const_cast<float *>(kc), vc, kv_len, position, heads, kv_heads,
+                           head_dim, scale, splits, chunk, part, nullptr, nullptr);
+}
+
+extern "C" __global__ __launch_bounds__(256) void realm_attention_split_rope(
+    const float *q, float *kc, const float *vc, int kv_len, int position, int heads,
+    int kv_heads, int head_dim, float scale, int splits, int chunk, float *part,
+    const float *k_new, const float2 *rope_cs_tab)
+{
+    attention_split<true>(q, kc, vc, kv_len, position, heads, kv_heads, head_dim, scale, splits,
+                          chunk, part, k_new, rope_cs_tab);
 }
 
 // One workgroup of head_dim threads per (token, head).

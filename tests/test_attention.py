@@ -159,7 +159,7 @@ def test_kv_append_then_attention(backend):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("fuse", ["1", "0"])
+@pytest.mark.parametrize("fuse", ["1", "0", "rope"])
 @pytest.mark.parametrize("mixed", [False, True])
 def test_forward_layer(backend, oracle, monkeypatch, mixed, fuse):
     """realm_hip_forward_layer_dev against the oracle's composition of the
@@ -168,8 +168,13 @@ def test_forward_layer(backend, oracle, monkeypatch, mixed, fuse):
     that would overflow the cache.  mixed: V and up in Q6_K (separate
     products), otherwise every projection in Q4_K (grouped products).  The
     1-token call runs with the norms and SwiGLU fused into the GEMVs
-    (fuse "1", where the formats allow) and as separate launches ("0")."""
-    monkeypatch.setenv("REALM_LAYER_FUSE", fuse)
+    (fuse "1", where the formats allow), as separate launches ("0"), and
+    fused with the split attention forced ("rope": RoPE of q and of the new
+    key row inside the attention kernel, which writes the rotated row into
+    the cache)."""
+    monkeypatch.setenv("REALM_LAYER_FUSE", "0" if fuse == "0" else "1")
+    if fuse == "rope":
+        monkeypatch.setenv("REALM_ATT_SPLITS", "2")
     from realm_amd import synth
     from realm_amd.backend import RealmError, RealmLayer
     from realm_amd.formats import GGML_Q4_K, GGML_Q6_K
@@ -242,14 +247,17 @@ def test_forward_layer(backend, oracle, monkeypatch, mixed, fuse):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("fuse", ["1", "0"])
+@pytest.mark.parametrize("fuse", ["1", "0", "rope"])
 def test_forward_layers_chain(backend, oracle, monkeypatch, fuse):
     """Three layers in one realm_hip_forward_layers_dev call (the residual add
     fused into the next layer's first norm) against three oracle layers
     applied in turn, for a 4-token prefill and a 1-token decode after it
     (fuse "1": the decode's norms, residual adds and SwiGLU inside the
-    GEMVs; "0": separate launches)."""
-    monkeypatch.setenv("REALM_LAYER_FUSE", fuse)
+    GEMVs; "0": separate launches; "rope": fused, with the split attention
+    forced, RoPE inside it)."""
+    monkeypatch.setenv("REALM_LAYER_FUSE", "0" if fuse == "0" else "1")
+    if fuse == "rope":
+        monkeypatch.setenv("REALM_ATT_SPLITS", "2")
     from realm_amd import synth
     from realm_amd.backend import RealmLayer
     from realm_amd.formats import GGML_Q4_K, GGML_Q6_K
@@ -446,8 +454,10 @@ def test_forward_layer_7b_decode_fused(backend, oracle, monkeypatch):
     11008; Q4_K projections, Q6_K W_down), the decode step bench.py times:
     a 2-token prefill, then one token with the norms and SwiGLU fused into
     the GEMVs' x staging (the l64 u1 "_n" kernels for Q/K/V and gate/up, the
-    u3 "_s" kernel for W_down) and the same token through the separate
-    launches, both against the oracle's composition."""
+    u3 "_s" kernel for W_down), the same with the split attention forced
+    (RoPE fused into it), and the same token through the separate launches,
+    all against the oracle's composition; the K cache row each run writes
+    against the oracle's."""
     from realm_amd import synth
     from realm_amd.backend import RealmLayer
     from realm_amd.formats import GGML_Q4_K, GGML_Q6_K
@@ -493,19 +503,28 @@ def test_forward_layer_7b_decode_fused(backend, oracle, monkeypatch):
         d1 = backend.alloc(x1.nbytes).upload(x1)
         bufs.append(d1)
         outs = {}
-        for fuse in ("1", "0"):
-            monkeypatch.setenv("REALM_LAYER_FUSE", fuse)
+        kc_want = kc_ref.copy()
+        oa.forward_layer(matmul, x1, blocks, norms, cfg, kc_want, vc_ref.copy(), 2, 1)
+        for fuse in ("1", "rope", "0"):
+            monkeypatch.setenv("REALM_LAYER_FUSE", "0" if fuse == "0" else "1")
+            if fuse == "rope":
+                monkeypatch.setenv("REALM_ATT_SPLITS", "2")
+            else:
+                monkeypatch.delenv("REALM_ATT_SPLITS", raising=False)
             do = backend.alloc(x1.nbytes)
             bufs.append(do)
-            # the same cache position both times: the step rewrites its K/V row
+            # the same cache position every time: the step rewrites its K/V row
             backend.forward_layer_dev(layer, d1.ptr, 1, 2, dkc.ptr, dvc.ptr, max_len, do.ptr)
             backend.synchronize()
             outs[fuse] = do.download(np.float32, H).reshape(1, H)
+            krow = dkc.download(np.float32, 3 * kv_dim)[2 * kv_dim:]
+            assert rel_l2(krow, kc_want[2 * kv_dim:3 * kv_dim]) < 1e-3, fuse
             err = rel_l2(outs[fuse], want)
             delta = rel_l2(outs[fuse] - x1, want - x1)
             print(f"7b decode fuse={fuse} rel_l2={err:.3e} delta={delta:.3e}")
             assert err < 1e-3 and delta < 1e-3, fuse
         assert rel_l2(outs["1"], outs["0"]) < 1e-5
+        assert rel_l2(outs["rope"], outs["0"]) < 1e-5
     finally:
         for h in hs.values():
             backend.release_weights(h)
