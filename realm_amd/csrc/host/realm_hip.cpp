@@ -1669,6 +1669,53 @@ REALM_API int realm_hip_attention_dev(const float *d_q, const float *d_k_cache,
         kv_len > (size_t)INT32_MAX || num_heads > (size_t)INT32_MAX)
         return fail(REALM_INVALID_ARGUMENT, "attention: sizes exceed 2^31-1");
     CHECK(ensure_init());
+    // Chunks of many query tokens (prefill): the tiled kernel stages each
+    // block of 32 keys once for 32 queries and takes any cache length; its
+    // keys split over workgroups when the query tiles alone leave the chip
+    // idle (partials combined by realm_attention_combine).
+    // REALM_ATT_TILED=1 / 0 forces it on / off (a forced split count,
+    // REALM_ATT_SPLITS, turns it off); REALM_ATT_TSPLITS forces its splits.
+    bool tiled = seq_len >= 4 && !getenv("REALM_ATT_SPLITS");
+    if (const char *env = getenv("REALM_ATT_TILED"))
+        tiled = env[0] == '1';
+    if (tiled && head_dim % 32 == 0 && num_heads <= 65535 && seq_len <= ((size_t)1 << 26) &&
+        aligned16(d_q) && aligned16(d_out)) {
+        hipStream_t s;
+        CHECK(pick_stream(stream, &s));
+        const size_t tiles = (seq_len + 31) / 32;
+        const size_t kvis = std::min(kv_len, position + seq_len); // keys the last token sees
+        size_t splits = 1;
+        if (tiles * num_heads < 2 * (size_t)g_dev.cu_count)
+            splits = std::min<size_t>({32, (2 * (size_t)g_dev.cu_count + tiles * num_heads - 1) /
+                                               (tiles * num_heads),
+                                       (kvis + 63) / 64});
+        if (const char *env = getenv("REALM_ATT_TSPLITS")) {
+            const long v = atol(env);
+            if (v >= 1 && v <= 64)
+                splits = (size_t)v;
+        }
+        splits = std::max<size_t>(splits, 1);
+        // chunks of whole 32-key blocks; the split count that covers kvis
+        size_t chunk = ((std::max<size_t>(kvis, 1) + splits - 1) / splits + 31) / 32 * 32;
+        splits = std::max<size_t>((kvis + chunk - 1) / chunk, 1);
+        void *part = nullptr;
+        if (splits > 1)
+            CHECK(ws_get(s, WS_ATT, seq_len * num_heads * splits * (head_dim + 2) * sizeof(float),
+                         &part));
+        int is = (int)seq_len, ikv = (int)kv_len, ipos = (int)position, ih = (int)num_heads,
+            ikh = (int)num_kv_heads, isp = (int)splits, ich = (int)chunk, id = (int)head_dim;
+        float scale = 1.0f / std::sqrt((float)head_dim);
+        void *args[] = {(void *)&d_q, (void *)&d_k_cache, (void *)&d_v_cache, &is, &ikv, &ipos,
+                        &ih, &ikh, &scale, &isp, &ich, &d_out, &part};
+        const std::string kname = "realm_attention_tiled_h" + std::to_string(head_dim);
+        CHECK(launch(kname.c_str(), dim3((unsigned)tiles, (unsigned)num_heads, (unsigned)splits),
+                     dim3(256), 0, s, args));
+        if (splits == 1)
+            return REALM_OK;
+        void *cargs[] = {&part, &isp, &id, &d_out};
+        return launch("realm_attention_combine", dim3((unsigned)(seq_len * num_heads)),
+                      dim3(256), 0, s, cargs);
+    }
     // Small grids (decode) and long caches: the keys split over workgroups,
     // then the partials combined (att_splits)
     const size_t att_threads = 1024; // ATT_TH in layer_ops.hip
@@ -1697,12 +1744,12 @@ REALM_API int realm_hip_attention_dev(const float *d_q, const float *d_k_cache,
         return launch("realm_attention_combine", dim3((unsigned)(seq_len * num_heads)),
                       dim3(256), 0, s, cargs);
     }
+    hipStream_t s;
+    CHECK(pick_stream(stream, &s));
     const size_t lds = (head_dim + kv_len + att_threads) * sizeof(float);
     if (lds + 64 > g_dev.max_lds)
         return fail(REALM_BACKEND_UNSUPPORTED,
                     "attention: " + std::to_string(kv_len) + " cached keys exceed the LDS");
-    hipStream_t s;
-    CHECK(pick_stream(stream, &s));
     int ikv = (int)kv_len, ipos = (int)position, ih = (int)num_heads, ikh = (int)num_kv_heads,
         id = (int)head_dim;
     float scale = 1.0f / std::sqrt((float)head_dim);

@@ -287,6 +287,226 @@ extern "C" __global__ __launch_bounds__(ATT_TH) void realm_attention(
     }
 }
 
+// Causal attention for many query tokens (prefill), tiled: one workgroup
+// of 4 waves per (32 query tokens, head, key split) walks its visible keys
+// in blocks of 32, each block's K and V staged once in LDS for all 32
+// queries (the one-workgroup-per-token kernel reads every visible key once
+// per query).  Both products run on v_mfma_f32_16x16x4_f32 (f32 products
+// and sums: results differ from a CPU f32 loop only in the order of the
+// additions); lane l supplies A[l%16][l/16] and B[l/16][l%16], element v of
+// its result is D[4(l/16) + v][l%16].
+//  * S = Q K^T / sqrt(head_dim): wave w owns the 16 x 16 quadrant (rows
+//    16(w&1), keys 16(w>>1)); its Q rows stay in registers for the whole
+//    walk, a lane holding head_dim elements 16g + 4(l/16) .. + 3 of its row
+//    per group g, read as float4 (K the same way from LDS), so the four
+//    MFMA steps of a group take the float4's four components.
+//  * Softmax online (thread t: row t / 8, keys 4 (t % 8) .. + 3): the row's
+//    running max m skips NaN scores (f32::max), a non-finite score gets
+//    weight 0 (standard.rs:119-126), so an +Inf score zeroes every finite
+//    weight and the row's output is 0; when the max grows the row's sum
+//    and output are rescaled by exp(m_old - m_new).
+//  * O += P V: wave w owns rows 16(w&1) and the 16-column tiles w>>1,
+//    (w>>1) + 2, ...; P and V come from LDS.
+// splits > 1: split s takes the keys [s chunk, (s+1) chunk) and writes the
+// row's (m, l, unnormalized output) to part in realm_attention_split's
+// layout, for realm_attention_combine; splits == 1 writes out directly.
+// HD is 32, 64, 128 or 256 (the host checks, and that q and out are 16-byte
+// aligned).
+namespace {
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+constexpr int ATQ = 32, ATK = 32; // query rows, keys per block
+
+template <int HD>
+__device__ void attention_tiled(const float *__restrict__ q, const float *__restrict__ kc,
+                                const float *__restrict__ vc, int seq, int kv_len, int position,
+                                int heads, int kv_heads, float scale, int splits, int chunk,
+                                float *__restrict__ out, float *__restrict__ part)
+{
+    constexpr int LK = HD + 4, LV = HD + 16, LP = ATK + 4; // padded LDS rows (floats)
+    constexpr int NG = HD / 16;             // groups of 16 head_dim elements
+    constexpr int NL = ATK * HD / 4 / 256;  // float4 of K (and of V) per thread and block
+    constexpr int NT = HD / 32;             // 16 x 16 output tiles per wave
+    __shared__ __align__(16) float Ks[ATK * LK];
+    __shared__ __align__(16) float Vs[ATK * LV];
+    __shared__ __align__(16) float Ps[ATQ * LP];
+    __shared__ __align__(16) float Rs[ATQ];
+    __shared__ float Ms[ATQ], Ls[ATQ];
+    const int h = blockIdx.y, q0 = blockIdx.x * ATQ, sp = blockIdx.z;
+    const int kvh = h / (heads / kv_heads), kv_dim = kv_heads * HD;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int lr = lane & 15, lc = lane >> 4;
+    const int nq = min(ATQ, seq - q0);
+    // keys this workgroup walks: its split's, up to the last one any row of
+    // the tile sees
+    const int kb = sp * chunk;
+    const int kl = min(min(kb + chunk, kv_len), position + q0 + nq);
+
+    const int rw = 16 * (wave & 1), cw = 16 * (wave >> 1);
+    floatx4 qv[NG];
+    {
+        const int r = rw + lr;
+        const float *qr = q + ((size_t)(q0 + min(r, nq - 1)) * heads + h) * HD + 4 * lc;
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+            const float4 v = *reinterpret_cast<const float4 *>(qr + 16 * g);
+            qv[g] = r < nq ? floatx4{v.x, v.y, v.z, v.w} : floatx4{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+    floatx4 acc[NT];
+#pragma unroll
+    for (int i = 0; i < NT; ++i)
+        acc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+    const int qi = tid >> 3, kq = tid & 7;
+    const int qpos = position + q0 + qi; // absolute position of softmax row qi
+    float m = -INFINITY, l = 0.f;
+
+    // global -> registers: float4 f = tid + 256 i of the block (row f / (HD/4))
+    float4 kr[NL], vr[NL];
+    auto load_block = [&](int k0, int nk) {
+#pragma unroll
+        for (int i = 0; i < NL; ++i) {
+            const int f = tid + 256 * i, r = f / (HD / 4), c = f % (HD / 4);
+            const size_t at = (size_t)(k0 + min(r, nk - 1)) * kv_dim + (size_t)kvh * HD + 4 * c;
+            kr[i] = *reinterpret_cast<const float4 *>(kc + at);
+            vr[i] = *reinterpret_cast<const float4 *>(vc + at);
+        }
+    };
+    if (kb < kl)
+        load_block(kb, min(ATK, kl - kb));
+    for (int k0 = kb; k0 < kl; k0 += ATK) {
+        const int nk = min(ATK, kl - k0);
+        __syncthreads(); // every wave is done with the previous block's K, V and P
+#pragma unroll
+        for (int i = 0; i < NL; ++i) {
+            const int f = tid + 256 * i, r = f / (HD / 4), c = f % (HD / 4);
+            *reinterpret_cast<float4 *>(Ks + r * LK + 4 * c) = kr[i];
+            // keys past the walk weigh 0; their V rows are zero, so no
+            // 0 x (their value) reaches the sums
+            *reinterpret_cast<float4 *>(Vs + r * LV + 4 * c) =
+                r < nk ? vr[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        __syncthreads();
+        if (k0 + ATK < kl) // the next block's loads fly during this one
+            load_block(k0 + ATK, min(ATK, kl - k0 - ATK));
+        // S quadrant
+        {
+            floatx4 sv = {0.f, 0.f, 0.f, 0.f};
+            const float *kp = Ks + (cw + lr) * LK + 4 * lc;
+#pragma unroll
+            for (int g = 0; g < NG; ++g) {
+                const float4 kk = *reinterpret_cast<const float4 *>(kp + 16 * g);
+                sv = __builtin_amdgcn_mfma_f32_16x16x4f32(qv[g][0], kk.x, sv, 0, 0, 0);
+                sv = __builtin_amdgcn_mfma_f32_16x16x4f32(qv[g][1], kk.y, sv, 0, 0, 0);
+                sv = __builtin_amdgcn_mfma_f32_16x16x4f32(qv[g][2], kk.z, sv, 0, 0, 0);
+                sv = __builtin_amdgcn_mfma_f32_16x16x4f32(qv[g][3], kk.w, sv, 0, 0, 0);
+            }
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+                Ps[(rw + 4 * lc + v) * LP + cw + lr] = sv[v] * scale;
+        }
+        __syncthreads();
+        // online softmax of row qi over keys 4 kq .. 4 kq + 3
+        {
+            float4 s4 = *reinterpret_cast<const float4 *>(Ps + qi * LP + 4 * kq);
+            float sv[4] = {s4.x, s4.y, s4.z, s4.w};
+            bool vis[4];
+            float bmax = -INFINITY;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int j = k0 + 4 * kq + u;
+                vis[u] = qi < nq && j < kl && j <= qpos;
+                if (vis[u])
+                    bmax = fmaxf(bmax, sv[u]);
+            }
+#pragma unroll
+            for (int off = 1; off < 8; off <<= 1)
+                bmax = fmaxf(bmax, __shfl_xor(bmax, off, 64));
+            const float mn = fmaxf(m, bmax);
+            // rescale of what the row holds: 0 while it holds nothing
+            const float rs = m == -INFINITY ? 0.f
+                                            : (mn == INFINITY && m == INFINITY ? 1.f : expf(m - mn));
+            float e[4], ps = 0.f;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                e[u] = vis[u] && __builtin_isfinite(sv[u]) ? expf(sv[u] - mn) : 0.f;
+                ps += e[u];
+            }
+            *reinterpret_cast<float4 *>(Ps + qi * LP + 4 * kq) = make_float4(e[0], e[1], e[2], e[3]);
+#pragma unroll
+            for (int off = 1; off < 8; off <<= 1)
+                ps += __shfl_xor(ps, off, 64);
+            l = l * rs + ps;
+            m = mn;
+            if (kq == 0)
+                Rs[qi] = rs;
+        }
+        __syncthreads();
+        // O = O rs + P V
+        {
+            const float4 r4 = *reinterpret_cast<const float4 *>(Rs + rw + 4 * lc);
+#pragma unroll
+            for (int i = 0; i < NT; ++i) {
+                acc[i][0] *= r4.x;
+                acc[i][1] *= r4.y;
+                acc[i][2] *= r4.z;
+                acc[i][3] *= r4.w;
+            }
+#pragma unroll
+            for (int ks = 0; ks < ATK / 4; ++ks) {
+                const float a = Ps[(rw + lr) * LP + 4 * ks + lc];
+                const float *vp = Vs + (4 * ks + lc) * LV + lr;
+#pragma unroll
+                for (int i = 0; i < NT; ++i)
+                    acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, vp[16 * ((wave >> 1) + 2 * i)],
+                                                                 acc[i], 0, 0, 0);
+            }
+        }
+    }
+    if (kq == 0) {
+        Ms[qi] = m;
+        Ls[qi] = l;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        const int r = rw + 4 * lc + v;
+        if (r >= nq)
+            continue;
+        const size_t th = (size_t)(q0 + r) * heads + h;
+        if (splits == 1) {
+            const float inv = Ls[r] > 0.f ? 1.f / Ls[r] : 0.f;
+            float *orow = out + th * HD + lr;
+#pragma unroll
+            for (int i = 0; i < NT; ++i)
+                orow[16 * ((wave >> 1) + 2 * i)] = acc[i][v] * inv;
+        } else {
+            float *pr = part + (th * splits + sp) * (HD + 2);
+#pragma unroll
+            for (int i = 0; i < NT; ++i)
+                pr[2 + 16 * ((wave >> 1) + 2 * i) + lr] = acc[i][v];
+        }
+    }
+    if (splits > 1 && tid < nq) {
+        float *pr = part + (((size_t)(q0 + tid) * heads + h) * splits + sp) * (HD + 2);
+        pr[0] = Ms[tid];
+        pr[1] = Ls[tid];
+    }
+}
+} // namespace
+
+#define ATT_TILED(HD)                                                                          \
+    extern "C" __global__ __launch_bounds__(256) void realm_attention_tiled_h##HD(             \
+        const float *q, const float *kc, const float *vc, int seq, int kv_len, int position,  \
+        int heads, int kv_heads, float scale, int splits, int chunk, float *out, float *part) \
+    {                                                                                          \
+        attention_tiled<HD>(q, kc, vc, seq, kv_len, position, heads, kv_heads, scale, splits,  \
+                            chunk, out, part);                                                 \
+    }
+ATT_TILED(32)
+ATT_TILED(64)
+ATT_TILED(128)
+ATT_TILED(256)
+
 // Residual add out[i] = a[i] + b[i] (CandleCpuBackend::add as
 // realm_forward_layer uses it, memory64_host.rs:2452-2458), float4 per
 // thread over n4 vectors.

@@ -122,6 +122,58 @@ def test_attention(backend, monkeypatch, seq, kv, pos, heads, kvh, hd, splits):
     assert rel_l2(got, want) < 1e-5
 
 
+TILED_CASES = [  # (seq, kv, pos, heads, kv heads, head_dim, forced tiled, forced splits)
+    (511, 511, 0, 32, 32, 128, None, None),   # the bench prefill chunk (16 query tiles)
+    (70, 100, 30, 8, 2, 128, None, "1"),      # partial tiles, GQA, cache past the visible keys
+    (70, 100, 30, 8, 2, 128, None, "3"),      # the same over 3 key splits
+    (33, 33, 0, 4, 4, 32, None, None),        # one query past a tile
+    (16, 4000, 3984, 4, 1, 256, None, None),  # long cache: 32 splits of 4 blocks
+    (16, 4000, 3984, 4, 1, 256, None, "1"),   # the same walked by one workgroup per head
+    (40, 300, 100, 8, 4, 64, None, "7"),      # splits past the visible keys
+    (5, 20, 15, 16, 4, 64, "1", None),        # forced below its default threshold
+    (1, 40, 39, 2, 2, 64, "1", "1"),          # one token
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", TILED_CASES, ids=[f"s{c[0]}-kv{c[1]}-hd{c[5]}-t{c[6]}-ks{c[7]}" for c in TILED_CASES])
+def test_attention_tiled(backend, monkeypatch, case):
+    """The tiled prefill form (32 queries x 32 keys per step on f32 MFMA,
+    online softmax; keys split over workgroups and combined when the query
+    tiles are few) against the oracle, with the one-workgroup-per-token
+    form on the same inputs as a second check."""
+    seq, kv, pos, heads, kvh, hd, force, ks = case
+    if force:
+        monkeypatch.setenv("REALM_ATT_TILED", force)
+    if ks:
+        monkeypatch.setenv("REALM_ATT_TSPLITS", ks)
+    g = np.random.default_rng(seq * 11 + kv)
+    q = g.standard_normal(seq * heads * hd).astype(np.float32)
+    k = g.standard_normal(kv * kvh * hd).astype(np.float32)
+    v = g.standard_normal(kv * kvh * hd).astype(np.float32)
+    dq, dk, dv = (backend.alloc(a.nbytes).upload(a) for a in (q, k, v))
+    do = backend.alloc(q.nbytes)
+    try:
+        backend.attention_dev(dq.ptr, dk.ptr, dv.ptr, seq, kv, pos, heads, kvh, hd, do.ptr)
+        backend.synchronize()
+        kernel = backend.last_kernel()
+        got = do.download(np.float32, q.size)
+        monkeypatch.setenv("REALM_ATT_TILED", "0")
+        backend.attention_dev(dq.ptr, dk.ptr, dv.ptr, seq, kv, pos, heads, kvh, hd, do.ptr)
+        backend.synchronize()
+        other = do.download(np.float32, q.size)
+    finally:
+        for b in (dq, dk, dv, do):
+            b.close()
+    if ks == "1":
+        assert kernel == f"realm_attention_tiled_h{hd}"
+    else:
+        assert kernel in (f"realm_attention_tiled_h{hd}", "realm_attention_combine")
+    want = oa.attention(q, k, v, seq, kv, pos, heads, kvh, hd)
+    assert rel_l2(got, want) < 1e-5
+    assert rel_l2(got, other) < 1e-5
+
+
 @pytest.mark.gpu
 def test_kv_append_then_attention(backend):
     """Decode three steps into a device cache (append, then attend) against

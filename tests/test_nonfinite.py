@@ -179,11 +179,13 @@ def test_nonfinite_activations(backend, oracle, monkeypatch, case):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("splits", [None, "4"])
+@pytest.mark.parametrize("splits", [None, "4", "tiled"])
 def test_attention_nonfinite_scores(backend, monkeypatch, splits):
     """NaN, +Inf and -Inf attention scores (a NaN query head, keys with
-    +-Inf elements) on the one-workgroup and split-K forms."""
-    if splits:
+    +-Inf elements) on the one-workgroup, split-K and tiled forms."""
+    if splits == "tiled":
+        monkeypatch.setenv("REALM_ATT_TILED", "1")
+    elif splits:
         monkeypatch.setenv("REALM_ATT_SPLITS", splits)
     g = np.random.default_rng(81)
     seq, kv, pos, heads, kvh, hd = 2, 300, 298, 8, 2, 64
