@@ -107,4 +107,48 @@ REALM_DEV float exact_dot(const void *w0, const void *w1, const void *w2, int ro
     return acc;
 }
 
+// The same sum with eight products formed at a time (their loads in flight
+// together), then added in k order: for kernels with registers to spare
+// (the GEMVs' budget of 128 VGPRs would spill).
+template <int FMT>
+REALM_DEV float exact_dot_ilp(const void *w0, const void *w1, const void *w2, int row, int K,
+                              int KX, const void *x, int bf16, int nan_fb, int k0, int step)
+{
+#pragma clang fp contract(off)
+    constexpr int U = 8;
+    float acc = 0.f;
+    int k = k0;
+    for (; k + (U - 1) * step < K; k += U * step) {
+        float p[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            p[u] = dev_weight<FMT>((const uint8_t *)w0, (const uint8_t *)w1, (const uint8_t *)w2,
+                                   row, k + u * step, KX, nan_fb) *
+                   exact_x(x, bf16, (size_t)(k + u * step));
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            acc += p[u];
+    }
+    for (; k < K; k += step)
+        acc += dev_weight<FMT>((const uint8_t *)w0, (const uint8_t *)w1, (const uint8_t *)w2, row,
+                               k, KX, nan_fb) *
+               exact_x(x, bf16, (size_t)k);
+    return acc;
+}
+
+// exact_dot of one (row, token) by the 64 lanes of a wave: lane l sums
+// k = l, l + 64, ... in k order, then a butterfly adds the partial sums
+// (IEEE addition commutes, so every lane ends with the same bits).
+template <int FMT>
+REALM_DEV float exact_dot_wave(const void *w0, const void *w1, const void *w2, int row, int K,
+                               int KX, const void *x, int bf16, int nan_fb, int lane)
+{
+#pragma clang fp contract(off)
+    float s = exact_dot_ilp<FMT>(w0, w1, w2, row, K, KX, x, bf16, nan_fb, lane, 64);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1)
+        s += __shfl_xor(s, off, 64);
+    return s;
+}
+
 } // namespace realm

@@ -711,6 +711,7 @@ REALM_DEV void gemm_tiled(const GemmArgs &g)
                         (FMT == FMT_Q80 && bad[a]) ? __builtin_nanf("") : vals[bb][v / VS][a];
         return;
     }
+    bool flagged = false;
 #pragma unroll
     for (int bb = 0; bb < TM; ++bb)
 #pragma unroll
@@ -718,14 +719,19 @@ REALM_DEV void gemm_tiled(const GemmArgs &g)
             const int tok = m0 + tloc(bb, v);
             if (tok >= g.M)
                 continue;
+            // a token xprep flagged: the wave's exact pass below writes it
+            if (__builtin_expect(__builtin_isnan(ts[bb][v]), 0)) {
+                flagged = true;
+                continue;
+            }
 #pragma unroll
             for (int a = 0; a < TN; ++a) {
                 const int row = row0 + 32 * a;
                 if (row >= mat.N)
                     continue;
                 float out = vals[bb][v / VS][a];
-                // flagged by xprep, or a Q8_0 row with a scale d q in f16 cannot hold
-                if (__builtin_expect(__builtin_isnan(ts[bb][v]) || (FMT == FMT_Q80 && bad[a]), 0))
+                // a Q8_0 row with a scale d q in f16 cannot hold
+                if (__builtin_expect(FMT == FMT_Q80 && bad[a], 0))
                     out = exact_dot<FMT>(mat.w0, mat.w1, mat.w2, row, g.K, g.KX,
                                          (const uint8_t *)g.x +
                                              (size_t)tok * g.K * (g.xbf16 ? 2 : 4),
@@ -733,6 +739,28 @@ REALM_DEV void gemm_tiled(const GemmArgs &g)
                 yseg[(size_t)tok * mat.N + row] = out;
             }
         }
+    // The flagged tokens' rows on the exact f32 path, each (row, token) by
+    // the whole wave (k split over its lanes): one lane walking all of K
+    // alone leaves every weight load's latency exposed, about 0.5 us per
+    // element
+    if (__builtin_expect(__ballot(flagged) != 0, 0)) {
+        for (int tt = 0; tt < TM * TOK; ++tt) {
+            const int tok = m0 + wt * TM * TOK + tt;
+            if (tok >= g.M || !__builtin_isnan(g.tscale[tok]))
+                continue;
+            const uint8_t *xt = (const uint8_t *)g.x + (size_t)tok * g.K * (g.xbf16 ? 2 : 4);
+            for (int a = 0; a < TN; ++a)
+                for (int rr = 0; rr < 32; ++rr) {
+                    const int row = row0 - r32 + 32 * a + rr;
+                    if (row >= mat.N)
+                        break;
+                    const float out = exact_dot_wave<FMT>(mat.w0, mat.w1, mat.w2, row, g.K, g.KX,
+                                                          xt, g.xbf16, g.nan_fb, lane);
+                    if (lane == 0)
+                        yseg[(size_t)tok * mat.N + row] = out;
+                }
+        }
+    }
 }
 
 // realm_gemm_<fmt>_t<WR><WT><TN><TM><p|s|b><NS>: NS pipeline stages; OCC
@@ -814,10 +842,10 @@ REALM_DEV float reduce_base(const GemmArgs &g, const ReduceSite &r, int tile, in
         const uint8_t *x = (const uint8_t *)g.x + (size_t)r.tok * g.K * (g.xbf16 ? 2 : 4);
         // the reduce serves Q4_K, Q6_K and Q8_0 launches: the format from the layout
         sum = g.fmt == FMT_Q4K
-                  ? exact_dot<FMT_Q4K>(w0, w1, w2, r.row, g.K, g.KX, x, g.xbf16, g.nan_fb, 0, 1)
+                  ? exact_dot_ilp<FMT_Q4K>(w0, w1, w2, r.row, g.K, g.KX, x, g.xbf16, g.nan_fb, 0, 1)
               : g.fmt == FMT_Q6K
-                  ? exact_dot<FMT_Q6K>(w0, w1, w2, r.row, g.K, g.KX, x, g.xbf16, g.nan_fb, 0, 1)
-                  : exact_dot<FMT_Q80>(w0, w1, w2, r.row, g.K, g.KX, x, g.xbf16, g.nan_fb, 0, 1);
+                  ? exact_dot_ilp<FMT_Q6K>(w0, w1, w2, r.row, g.K, g.KX, x, g.xbf16, g.nan_fb, 0, 1)
+                  : exact_dot_ilp<FMT_Q80>(w0, w1, w2, r.row, g.K, g.KX, x, g.xbf16, g.nan_fb, 0, 1);
     }
     return sum;
 }
