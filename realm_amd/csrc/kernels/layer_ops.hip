@@ -316,6 +316,24 @@ namespace {
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 constexpr int ATQ = 32, ATK = 32; // query rows, keys per block
 
+// K and V rows k0 .. k0 + nk - 1 of one block into registers (rows past nk:
+// K repeats row nk - 1, V is zero)
+template <int HD, int NL>
+__device__ __forceinline__ void att_load(const float *__restrict__ kc, const float *__restrict__ vc,
+                                         int k0, int nk, int kvh, int kv_dim, int tid,
+                                         float4 (&kr)[NL], float4 (&vr)[NL])
+{
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+        const int f = tid + 256 * i, r = f / (HD / 4), c = f % (HD / 4);
+        const size_t at = (size_t)(k0 + min(r, nk - 1)) * kv_dim + (size_t)kvh * HD + 4 * c;
+        const float4 kk = *reinterpret_cast<const float4 *>(kc + at);
+        const float4 vv = *reinterpret_cast<const float4 *>(vc + at);
+        kr[i] = kk;
+        vr[i] = r < nk ? vv : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+}
+
 template <int HD>
 __device__ void attention_tiled(const float *__restrict__ q, const float *__restrict__ kc,
                                 const float *__restrict__ vc, int seq, int kv_len, int position,
@@ -360,34 +378,23 @@ __device__ void attention_tiled(const float *__restrict__ q, const float *__rest
     const int qpos = position + q0 + qi; // absolute position of softmax row qi
     float m = -INFINITY, l = 0.f;
 
-    // global -> registers: float4 f = tid + 256 i of the block (row f / (HD/4))
+    // global -> registers: float4 f = tid + 256 i of the block (row f / (HD/4));
+    // keys past the walk weigh 0 and get zero V rows, so no 0 x (their
+    // value) reaches the sums
     float4 kr[NL], vr[NL];
-    auto load_block = [&](int k0, int nk) {
-#pragma unroll
-        for (int i = 0; i < NL; ++i) {
-            const int f = tid + 256 * i, r = f / (HD / 4), c = f % (HD / 4);
-            const size_t at = (size_t)(k0 + min(r, nk - 1)) * kv_dim + (size_t)kvh * HD + 4 * c;
-            kr[i] = *reinterpret_cast<const float4 *>(kc + at);
-            vr[i] = *reinterpret_cast<const float4 *>(vc + at);
-        }
-    };
     if (kb < kl)
-        load_block(kb, min(ATK, kl - kb));
+        att_load<HD, NL>(kc, vc, kb, min(ATK, kl - kb), kvh, kv_dim, tid, kr, vr);
     for (int k0 = kb; k0 < kl; k0 += ATK) {
-        const int nk = min(ATK, kl - k0);
         __syncthreads(); // every wave is done with the previous block's K, V and P
 #pragma unroll
         for (int i = 0; i < NL; ++i) {
             const int f = tid + 256 * i, r = f / (HD / 4), c = f % (HD / 4);
             *reinterpret_cast<float4 *>(Ks + r * LK + 4 * c) = kr[i];
-            // keys past the walk weigh 0; their V rows are zero, so no
-            // 0 x (their value) reaches the sums
-            *reinterpret_cast<float4 *>(Vs + r * LV + 4 * c) =
-                r < nk ? vr[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+            *reinterpret_cast<float4 *>(Vs + r * LV + 4 * c) = vr[i];
         }
         __syncthreads();
         if (k0 + ATK < kl) // the next block's loads fly during this one
-            load_block(k0 + ATK, min(ATK, kl - k0 - ATK));
+            att_load<HD, NL>(kc, vc, k0 + ATK, min(ATK, kl - k0 - ATK), kvh, kv_dim, tid, kr, vr);
         // S quadrant
         {
             floatx4 sv = {0.f, 0.f, 0.f, 0.f};
