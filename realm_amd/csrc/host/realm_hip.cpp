@@ -736,8 +736,12 @@ GemmTile gemm_tile(const Weight &w, size_t M, bool bf16)
         return M <= 16 ? GemmTile{"s1", 16, 16, 1024} : GemmTile{"s2", 16, 32, 512};
     if (tiled_ok(w)) {
         GemmTile t;
+        // f32 Q6_K past 448 tokens: the lo part as a second MFMA (`s`)
+        // beat the packed slots by 8-11% at 511 and 1024 tokens (W_down and
+        // 11008 x 4096); it lost at 256 and below, and for Q4_K everywhere
         const char *name = bf16 ? "t4112b2"
-                                : (M <= 16 ? "t4111p2" : "t4112p2");
+                           : M <= 16 ? "t4111p2"
+                           : (w.type == GGML_Q6_K && M > 448) ? "t4112s2" : "t4112p2";
         tiled_tile(name, bf16, 1, &t);
         const size_t tiles = ((w.n + t.rows_per_wg - 1) / t.rows_per_wg) *
                              ((M + t.toks_per_wg - 1) / t.toks_per_wg);

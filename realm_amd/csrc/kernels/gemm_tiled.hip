@@ -676,6 +676,14 @@ REALM_DEV void gemm_tiled(const GemmArgs &g)
                 ts[bb][4 * q4 + 3] = t4.w;
             }
         }
+    // the first 512 tokens' scales for the exact pass at the end, loaded
+    // before the stores too (direct epilogue only)
+    float tsv[8];
+    if (!g.part) {
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+            tsv[c] = g.tscale[min(64 * c + lane, g.M - 1)];
+    }
     // this workgroup's sums: vals[bb][v / VS][a] for token slot(s) v of tile
     // bb (packed: slots v, v + 1 are one token's hi and lo), row tile a
     constexpr int VS = PACK ? 2 : 1, NV = 16 / VS;
@@ -711,7 +719,6 @@ REALM_DEV void gemm_tiled(const GemmArgs &g)
                         (FMT == FMT_Q80 && bad[a]) ? __builtin_nanf("") : vals[bb][v / VS][a];
         return;
     }
-    bool flagged = false;
 #pragma unroll
     for (int bb = 0; bb < TM; ++bb)
 #pragma unroll
@@ -719,11 +726,9 @@ REALM_DEV void gemm_tiled(const GemmArgs &g)
             const int tok = m0 + tloc(bb, v);
             if (tok >= g.M)
                 continue;
-            // a token xprep flagged: the wave's exact pass below writes it
-            if (__builtin_expect(__builtin_isnan(ts[bb][v]), 0)) {
-                flagged = true;
+            // a token xprep flagged: the exact pass below writes it
+            if (__builtin_expect(__builtin_isnan(ts[bb][v]), 0))
                 continue;
-            }
 #pragma unroll
             for (int a = 0; a < TN; ++a) {
                 const int row = row0 + 32 * a;
@@ -739,19 +744,32 @@ REALM_DEV void gemm_tiled(const GemmArgs &g)
                 yseg[(size_t)tok * mat.N + row] = out;
             }
         }
-    // The flagged tokens' rows on the exact f32 path, each (row, token) by
-    // the whole wave (k split over its lanes): one lane walking all of K
-    // alone leaves every weight load's latency exposed, about 0.5 us per
-    // element
-    if (__builtin_expect(__ballot(flagged) != 0, 0)) {
-        for (int tt = 0; tt < TM * TOK; ++tt) {
-            const int tok = m0 + wt * TM * TOK + tt;
-            if (tok >= g.M || !__builtin_isnan(g.tscale[tok]))
-                continue;
-            const uint8_t *xt = (const uint8_t *)g.x + (size_t)tok * g.K * (g.xbf16 ? 2 : 4);
-            for (int a = 0; a < TN; ++a)
-                for (int rr = 0; rr < 32; ++rr) {
-                    const int row = row0 - r32 + 32 * a + rr;
+    // The flagged tokens' rows on the exact f32 path.  Every workgroup of
+    // the row tile takes part, whichever token tile it holds (one flagged
+    // token's rows would otherwise fall to the few workgroups of its own
+    // tile while the rest of the chip idles): workgroup tt of TT takes rows
+    // tt, tt + TT, ... of the tile for every flagged token, each wave every
+    // (WR WT)-th of them, and each (row, token) is summed by one whole wave (k
+    // split over its lanes; one lane walking all of K alone exposes every
+    // weight load's latency, about 0.5 us per element).
+    // The token scales are scanned 512 at a time, their loads issued
+    // together (one memory round trip per 512 tokens; the first 512 were
+    // loaded before the stores).
+    for (int base = 0; base < g.M; base += 512) {
+        if (base > 0) {
+#pragma unroll
+            for (int c = 0; c < 8; ++c)
+                tsv[c] = g.tscale[min(base + 64 * c + lane, g.M - 1)];
+        }
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            unsigned long long fl = __ballot(base + 64 * c + lane < g.M && __builtin_isnan(tsv[c]));
+            while (fl) {
+                const int tok = base + 64 * c + (int)__builtin_ctzll(fl);
+                fl &= fl - 1;
+                const uint8_t *xt = (const uint8_t *)g.x + (size_t)tok * g.K * (g.xbf16 ? 2 : 4);
+                for (int j = tt + TT * wave; j < GROWS; j += WR * WT * TT) {
+                    const int row = rtl * GROWS + j;
                     if (row >= mat.N)
                         break;
                     const float out = exact_dot_wave<FMT>(mat.w0, mat.w1, mat.w2, row, g.K, g.KX,
@@ -759,6 +777,7 @@ REALM_DEV void gemm_tiled(const GemmArgs &g)
                     if (lane == 0)
                         yseg[(size_t)tok * mat.N + row] = out;
                 }
+            }
         }
     }
 }

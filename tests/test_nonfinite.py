@@ -142,6 +142,7 @@ CASES = [  # (format, m, k, group, bf16, forced tile, forced K split, kernel pre
     (GGML_Q4_K, 6, 2048, 1, False, None, None, "realm_gemm_q4k_s1"),
     (GGML_Q4_K, 37, 2048, 1, False, "t4112p2", "1", "realm_gemm_q4k_t4112p2"),
     (GGML_Q6_K, 37, 2048, 2, False, "t4112p2", "4", "realm_gemm_tiled_reduce"),
+    (GGML_Q6_K, 70, 2048, 1, False, "t4112s2", "1", "realm_gemm_q6k_t4112s2"),
     (GGML_Q4_K, 64, 2048, 1, True, "t4112b2", "1", "realm_gemm_q4k_t4112b2"),
     (GGML_Q8_0, 37, 2048, 1, False, None, None, "realm_gemm_tiled_reduce"),
     (GGML_Q8_0, 37, 2048, 1, False, "t4112p2", "1", "realm_gemm_q80_t4112p2"),
