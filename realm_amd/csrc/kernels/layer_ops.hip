@@ -558,6 +558,20 @@ __device__ void attention_split(const float *q, float *kc, const float *vc, int 
     const int j0 = s * chunk, j1 = min(vis, j0 + chunk);
     const int n = max(j1 - j0, 0);
     const float *qr = q + ((size_t)t * heads + h) * head_dim;
+    // V rows of this thread's first VU keys (thread: column d, keys pp,
+    // pp + parts, ...), loaded before anything else: their addresses depend
+    // on nothing, so their latency hides behind the q and K phases
+    constexpr int VU = 32;
+    const int parts = 256 / head_dim;
+    const int d = threadIdx.x % head_dim, pp = threadIdx.x / head_dim;
+    float vv0[VU];
+    if (n > 0) {
+#pragma unroll
+        for (int u = 0; u < VU; ++u) {
+            const int jc = j0 + min(pp + u * parts, n - 1);
+            vv0[u] = vc[(size_t)jc * kv_dim + (size_t)kvh * head_dim + d];
+        }
+    }
     if constexpr (ROPE) {
         const int half = head_dim >> 1;
         for (int pi = threadIdx.x; pi < half; pi += 256) { // (one token: t = 0)
@@ -646,19 +660,30 @@ __device__ void attention_split(const float *q, float *kc, const float *vc, int 
         red[4 + (threadIdx.x >> 6)] = sum;
     __syncthreads();
     sum = red[4] + red[5] + red[6] + red[7];
-    const int parts = 256 / head_dim;
-    const int d = threadIdx.x % head_dim, pp = threadIdx.x / head_dim;
+    // weighted sum of V in key order: the prefetched rows, then rounds of
+    // VU loads issued together; keys past the visible ones add zero
     float a = 0.f;
-    for (int jb = pp; jb < n; jb += 8 * parts) {
-        float vv[8], pw[8];
+    if (n > 0) {
+        float pw[VU];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
+        for (int u = 0; u < VU; ++u) {
+            const int jl = pp + u * parts;
+            pw[u] = jl < n ? sc[min(jl, n - 1)] : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < VU; ++u)
+            a += pw[u] * vv0[u];
+    }
+    for (int jb = pp + VU * parts; jb < n; jb += VU * parts) {
+        float vv[VU], pw[VU];
+#pragma unroll
+        for (int u = 0; u < VU; ++u) {
             const int jl = jb + u * parts, jc = j0 + min(jl, n - 1);
             vv[u] = vc[(size_t)jc * kv_dim + (size_t)kvh * head_dim + d];
             pw[u] = jl < n ? sc[min(jl, n - 1)] : 0.f;
         }
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
+        for (int u = 0; u < VU; ++u)
             a += pw[u] * vv[u];
     }
     acc[threadIdx.x] = a;
@@ -701,15 +726,38 @@ extern "C" __global__ __launch_bounds__(256) void realm_attention_combine(
     if (d >= head_dim)
         return;
     const float *pr = part + (size_t)th * splits * (head_dim + 2);
-    float m = -INFINITY;
-    for (int s = 0; s < splits; ++s)
-        m = fmaxf(m, pr[(size_t)s * (head_dim + 2)]);
-    float l = 0.f, o = 0.f;
-    for (int s = 0; s < splits; ++s) {
-        const float *p = pr + (size_t)s * (head_dim + 2);
-        const float w = p[1] > 0.f ? expf(p[0] - m) : 0.f;
-        l += p[1] * w;
-        o += p[2 + d] * w;
+    float m = -INFINITY, l = 0.f, o = 0.f;
+    if (splits <= 16) {
+        // every split's (m, l, acc[d]) loaded at once (one memory round
+        // trip; split s past `splits` reads the last one and is not used)
+        float ms[16], ls[16], as[16];
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {
+            const float *p = pr + (size_t)min(s, splits - 1) * (head_dim + 2);
+            ms[s] = p[0];
+            ls[s] = p[1];
+            as[s] = p[2 + d];
+        }
+#pragma unroll
+        for (int s = 0; s < 16; ++s)
+            if (s < splits)
+                m = fmaxf(m, ms[s]);
+#pragma unroll
+        for (int s = 0; s < 16; ++s)
+            if (s < splits) {
+                const float w = ls[s] > 0.f ? expf(ms[s] - m) : 0.f;
+                l += ls[s] * w;
+                o += as[s] * w;
+            }
+    } else {
+        for (int s = 0; s < splits; ++s)
+            m = fmaxf(m, pr[(size_t)s * (head_dim + 2)]);
+        for (int s = 0; s < splits; ++s) {
+            const float *p = pr + (size_t)s * (head_dim + 2);
+            const float w = p[1] > 0.f ? expf(p[0] - m) : 0.f;
+            l += p[1] * w;
+            o += p[2 + d] * w;
+        }
     }
     out[(size_t)th * head_dim + d] = l > 0.f ? o / l : 0.f;
 }
