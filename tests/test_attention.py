@@ -175,6 +175,45 @@ def test_attention_tiled(backend, monkeypatch, case):
 
 
 @pytest.mark.gpu
+def test_attention_split_graph_replays(backend):
+    """The split form (8 splits at this decode shape, then the combine)
+    captured once and replayed three times, with eager launches on the same
+    stream in between, every replay against the oracle."""
+    seq, kv, pos, heads, kvh, hd = 1, 512, 511, 32, 32, 128
+    g = np.random.default_rng(5)
+    q = g.standard_normal(seq * heads * hd).astype(np.float32)
+    k = g.standard_normal(kv * kvh * hd).astype(np.float32)
+    v = g.standard_normal(kv * kvh * hd).astype(np.float32)
+    want = oa.attention(q, k, v, seq, kv, pos, heads, kvh, hd)
+    dq, dk, dv = (backend.alloc(a.nbytes).upload(a) for a in (q, k, v))
+    do, de = backend.alloc(q.nbytes), backend.alloc(q.nbytes)
+    s = backend.stream()
+    run = lambda out: backend.attention_dev(dq.ptr, dk.ptr, dv.ptr, seq, kv, pos, heads, kvh, hd,
+                                            out.ptr, stream=s)
+    try:
+        run(do)
+        backend.synchronize()
+        assert backend.last_kernel() == "realm_attention_combine"
+        backend.graph_begin(s)
+        run(do)
+        gr = backend.graph_end(s)
+        try:
+            for _ in range(3):
+                do.upload(np.zeros(q.size, np.float32))
+                backend.graph_launch(gr, s)
+                backend.synchronize()
+                assert rel_l2(do.download(np.float32, q.size), want) < 1e-5
+                run(de)  # eager launch between replays, same scratch
+                backend.synchronize()
+                assert rel_l2(de.download(np.float32, q.size), want) < 1e-5
+        finally:
+            backend.graph_release(gr)
+    finally:
+        for b in (dq, dk, dv, do, de):
+            b.close()
+
+
+@pytest.mark.gpu
 def test_kv_append_then_attention(backend):
     """Decode three steps into a device cache (append, then attend) against
     the oracle's cache; the overflowing append fails with ParseError (4)."""
