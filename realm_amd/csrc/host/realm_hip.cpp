@@ -819,8 +819,13 @@ int prep_x_launch(const Weight &w, const XPrep &p, size_t M, const GemmTile &til
                       dim3((unsigned)(p.rows + (size_t)nshrink)), dim3(1024), 0, s, args);
     }
     void *args[] = {(void *)&d_x, &ibf, &xh, &xl, &xm, &ts, &iM, &iK, &iKX};
-    return launch(std::string("realm_xprep_") + fmt_name(w.type) + ord, dim3((unsigned)p.rows),
-                  dim3(1024), 0, s, args);
+    // threads per token: 256 for K <= 8192, 512 for K <= 16384, else 1024
+    // (four rounds of 8 positions per thread; none idle at 4096, and all of
+    // a thread's loads in one round trip)
+    const int th = w.kx <= 8192 ? 256 : w.kx <= 16384 ? 512 : 1024;
+    return launch(std::string("realm_xprep_") + fmt_name(w.type) + ord +
+                      (th < 1024 ? "_t" + std::to_string(th) : std::string()),
+                  dim3((unsigned)p.rows), dim3(th), 0, s, args);
 }
 
 int prep_x(const Weight &w, const void *d_x, bool bf16, size_t M, const GemmTile &tile,

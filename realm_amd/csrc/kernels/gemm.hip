@@ -46,12 +46,12 @@ using namespace realm;
 #define XPREP_TH 1024
 #define XPREP_R 4 // position-group rounds held in registers: KX <= 32768
 
-template <int FMT, int ORD>
+template <int FMT, int ORD, int TH = XPREP_TH>
 REALM_DEV void xprep(const void *__restrict__ x, int bf16, _Float16 *__restrict__ xh,
                      _Float16 *__restrict__ xl, _Float16 *__restrict__ xm,
                      float *__restrict__ tscale, int M, int K, int KX)
 {
-    __shared__ float red[XPREP_TH / 64];
+    __shared__ float red[TH / 64];
     const int t = blockIdx.x;
     const bool live = t < M;
     const size_t xrow = (size_t)t * K;
@@ -61,7 +61,7 @@ REALM_DEV void xprep(const void *__restrict__ x, int bf16, _Float16 *__restrict_
     float amax = 0.f;
 #pragma unroll
     for (int r = 0; r < XPREP_R; ++r) {
-        const int pg = r * XPREP_TH + threadIdx.x;
+        const int pg = r * TH + threadIdx.x;
         const int k0 = pg < ngroups ? kwin<FMT, ORD>(pg) : 0;
         // a window is 4 + 4 consecutive k (GAP apart): two vector loads when
         // both halves are inside the row (K % 4 == 0 keeps them aligned)
@@ -107,7 +107,7 @@ REALM_DEV void xprep(const void *__restrict__ x, int bf16, _Float16 *__restrict_
     __syncthreads();
     amax = 0.f;
 #pragma unroll
-    for (int w = 0; w < XPREP_TH / 64; ++w)
+    for (int w = 0; w < TH / 64; ++w)
         amax = fmaxf(amax, red[w]);
     const bool exact = exact_needed(amax, !__builtin_isfinite(amax));
     int e = 0;
@@ -124,7 +124,7 @@ REALM_DEV void xprep(const void *__restrict__ x, int bf16, _Float16 *__restrict_
     const int B = K >> 8;
 #pragma unroll
     for (int r = 0; r < XPREP_R; ++r) {
-        const int pg = r * XPREP_TH + threadIdx.x;
+        const int pg = r * TH + threadIdx.x;
         _Float16 hv[8], lv[8];
         float sum = 0.f, shi = 0.f; // of this thread's x * down: all 8 / the upper 4
 #pragma unroll
@@ -197,6 +197,30 @@ REALM_DEV void xprep(const void *__restrict__ x, int bf16, _Float16 *__restrict_
 DEF_XPREP(q4k, FMT_Q4K)
 DEF_XPREP(q6k, FMT_Q6K)
 DEF_XPREP(q80, FMT_Q80)
+
+// The same with 256 threads per token for K <= 8192, 512 for K <= 16384
+// (4 rounds of TH x 8 positions): every thread has work at 4096 (the
+// 1024-thread form leaves half of them idle there), its loads issued
+// together, and the token's max meets over fewer waves.
+#define DEF_XPREP_TH(NAME, FMT, TH)                                                        \
+    extern "C" __global__ __launch_bounds__(TH) void realm_xprep_##NAME##_t##TH(           \
+        const void *x, int bf16, _Float16 *xh, _Float16 *xl, _Float16 *xm, float *tscale, \
+        int M, int K, int KX)                                                              \
+    {                                                                                      \
+        xprep<FMT, 0, TH>(x, bf16, xh, xl, xm, tscale, M, K, KX);                          \
+    }                                                                                      \
+    extern "C" __global__ __launch_bounds__(TH) void realm_xprep_##NAME##_o1_t##TH(        \
+        const void *x, int bf16, _Float16 *xh, _Float16 *xl, _Float16 *xm, float *tscale, \
+        int M, int K, int KX)                                                              \
+    {                                                                                      \
+        xprep<FMT, 1, TH>(x, bf16, xh, xl, xm, tscale, M, K, KX);                          \
+    }
+DEF_XPREP_TH(q4k, FMT_Q4K, 256)
+DEF_XPREP_TH(q6k, FMT_Q6K, 256)
+DEF_XPREP_TH(q80, FMT_Q80, 256)
+DEF_XPREP_TH(q4k, FMT_Q4K, 512)
+DEF_XPREP_TH(q6k, FMT_Q6K, 512)
+DEF_XPREP_TH(q80, FMT_Q80, 512)
 
 // --------------------------------------------------------- LoRA adapter table
 

@@ -224,7 +224,25 @@ def test_graph_survives_workspace_growth(backend, oracle):
     """A graph captured on a stream keeps using the scratch buffers it was
     captured with: a later, larger eager call on that stream gets new ones
     and the old ones are kept (not freed) until the graph is released, so
-    the replay after the growth still writes the right result."""
+    the replay after the growth still writes the right result.  Runs on a
+    thread of its own: the library's stream (and scratch) is per thread, so
+    earlier tests on this thread may have grown the buffers already."""
+    import threading
+    err = []
+
+    def body():
+        try:
+            _graph_survives_workspace_growth(backend, oracle)
+        except BaseException as e:  # re-raised on the test's thread
+            err.append(e)
+    th = threading.Thread(target=body)
+    th.start()
+    th.join()
+    if err:
+        raise err[0]
+
+
+def _graph_survives_workspace_growth(backend, oracle):
     g = synth.rng(7600)
     n, k = 512, 2048
     blocks = synth.blocks(g, GGML_Q4_K, n, k)
