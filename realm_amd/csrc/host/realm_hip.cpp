@@ -1951,14 +1951,21 @@ int layer_steps(const realm_layer *L, const int type[7], const float *x, const f
                                          x_res ? h_in : nullptr, normed, s));
             CHECK(products(qkv, qkv_sets, type, qkv_out, 3));
         }
-        { // RoPE of Q and of this call's K rows in one launch
+        { // RoPE of Q and of this call's K rows in one launch (rotations
+          // from the call's table of these positions when there is one)
             int iq = (int)heads, ik = (int)kvh, is = (int)seq_len, id = (int)hd,
                 ip = (int)position;
             float theta = L->rope_theta;
             const size_t pairs = seq_len * (heads + kvh) * (hd / 2);
-            void *args[] = {&q, &iq, &k_rows, &ik, &is, &id, &ip, &theta};
-            CHECK(launch("realm_rope_qk", dim3((unsigned)((pairs + 255) / 256)), dim3(256), 0, s,
-                         args));
+            if (rope_cs) {
+                void *args[] = {&q, &iq, &k_rows, &ik, &is, &id, (void *)&rope_cs};
+                CHECK(launch("realm_rope_qk_tab", dim3((unsigned)((pairs + 255) / 256)),
+                             dim3(256), 0, s, args));
+            } else {
+                void *args[] = {&q, &iq, &k_rows, &ik, &is, &id, &ip, &theta};
+                CHECK(launch("realm_rope_qk", dim3((unsigned)((pairs + 255) / 256)), dim3(256),
+                             0, s, args));
+            }
         }
         CHECK(realm_hip_attention_dev(q, kc, vc, seq_len, position + seq_len, position, heads,
                                       kvh, hd, att, s));
@@ -2029,7 +2036,7 @@ REALM_API int realm_hip_forward_layers_dev(const realm_layer *layers, size_t n_l
     const size_t sh = align256(seq_len * layers[0].hidden * 4);
     const size_t hd0 = layers[0].head_dim;
     void *ws = nullptr;
-    CHECK(ws_get(s, WS_LAYER, wsize + 3 * sh + align256(hd0 * 4), &ws));
+    CHECK(ws_get(s, WS_LAYER, wsize + 3 * sh + align256(seq_len * hd0 * 4), &ws));
     uint8_t *base = static_cast<uint8_t *>(ws);
     float *h_in = (float *)(base + wsize), *h2 = (float *)(base + wsize + sh),
           *down = (float *)(base + wsize + 2 * sh);
@@ -2046,6 +2053,16 @@ REALM_API int realm_hip_forward_layers_dev(const realm_layer *layers, size_t n_l
         void *args[] = {&rope_tab, &ihd, &ipos, &th};
         CHECK(launch("realm_rope_table", dim3((unsigned)((hd0 / 2 + 255) / 256)), dim3(256), 0, s,
                      args));
+    } else if (seq_len > 1) {
+        // a chunk of tokens: the rotations of its positions, once for every
+        // layer that shares layer 0's head_dim and theta (realm_rope_qk_tab
+        // reads them instead of evaluating powf and sincos per pair)
+        rope_tab = base + wsize + 3 * sh;
+        int ihd = (int)hd0, ipos = (int)position, iseq = (int)seq_len;
+        float th = layers[0].rope_theta;
+        void *args[] = {&rope_tab, &ihd, &ipos, &iseq, &th};
+        CHECK(launch("realm_rope_table_seq",
+                     dim3((unsigned)((seq_len * (hd0 / 2) + 255) / 256)), dim3(256), 0, s, args));
     }
     for (size_t l = 0; l < n_layers; ++l) {
         const bool same = layers[l].head_dim == hd0 && layers[l].rope_theta == layers[0].rope_theta;

@@ -147,6 +147,39 @@ extern "C" __global__ __launch_bounds__(256) void realm_rope_table(float2 *cs, i
         cs[p] = rope_cs(2 * p, pos, head_dim, theta);
 }
 
+// (cos, sin) of every pair angle at positions start .. start + seq - 1, cs[s][p]
+// (a prefill chunk's rotations, once per call for every layer)
+extern "C" __global__ __launch_bounds__(256) void realm_rope_table_seq(float2 *cs, int head_dim,
+                                                                       int start, int seq,
+                                                                       float theta)
+{
+    const int half = head_dim >> 1;
+    const size_t p = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (p < (size_t)seq * half)
+        cs[p] = rope_cs(2 * (int)(p % half), start + (int)(p / half), head_dim, theta);
+}
+
+// realm_rope_qk with the rotations read from a realm_rope_table_seq table of
+// the same positions (no powf or sincos per pair)
+extern "C" __global__ __launch_bounds__(256) void realm_rope_qk_tab(float *q, int q_heads, float *k,
+                                                                    int k_heads, int seq,
+                                                                    int head_dim, const float2 *cs)
+{
+    const int half = head_dim >> 1;
+    const size_t pq = (size_t)seq * q_heads * half, pk = (size_t)seq * k_heads * half;
+    const size_t p = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (p < pq) {
+        const int i = (int)(p % half), t = (int)(p / ((size_t)q_heads * half));
+        float2 *v = reinterpret_cast<float2 *>(q) + p;
+        *v = rope_apply(*v, cs[(size_t)t * half + i]);
+    } else if (p < pq + pk) {
+        const size_t pp = p - pq;
+        const int i = (int)(pp % half), t = (int)(pp / ((size_t)k_heads * half));
+        float2 *v = reinterpret_cast<float2 *>(k) + pp;
+        *v = rope_apply(*v, cs[(size_t)t * half + i]);
+    }
+}
+
 extern "C" __global__ __launch_bounds__(256) void realm_rope_qk(float *q, int q_heads, float *k,
                                                                 int k_heads, int seq, int head_dim,
                                                                 int start, float theta)

@@ -71,5 +71,6 @@ def test_code_object_is_embedded_for_gfx950():
               b"realm_dense_f32_m64", b"realm_gemv_q4k_l64_u1_d1_m4_n",
               b"realm_gemv_q6k_l64_u3_d2_m1_s", b"realm_gemv_q80_l16_u1_d3_m4_n",
               b"realm_attention_tiled_h32", b"realm_attention_tiled_h256",
-              b"realm_xprep_q4k_o1_t256", b"realm_xprep_q80_t256", b"realm_xprep_q6k_o1_t512"):
+              b"realm_xprep_q4k_o1_t256", b"realm_xprep_q80_t256", b"realm_xprep_q6k_o1_t512",
+              b"realm_rope_qk_tab", b"realm_rope_table_seq"):
         assert k in blobs
