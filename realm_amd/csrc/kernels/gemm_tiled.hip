@@ -845,12 +845,28 @@ REALM_DEV ReduceSite reduce_site(const GemmArgs &g, int grows, int gtok, int til
 // The base product of one element: the parts in split order, or the exact
 // f32 dot product for a token xprep flagged and for a NaN sum (a Q8_0 row
 // the tiled kernel flagged, or a NaN that the exact product reproduces).
+// The sum of an element's ks parts (TILE apart) in split order, their loads
+// issued 8 at a time (one memory round trip per 8 parts, not per part).
+REALM_DEV float sum_parts(const float *p, int ks, int TILE)
+{
+    float sum = 0.f;
+    for (int c0 = 0; c0 < ks; c0 += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (c0 + u < ks)
+                v[u] = p[(size_t)(c0 + u) * TILE];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (c0 + u < ks)
+                sum = c0 + u == 0 ? v[u] : sum + v[u];
+    }
+    return sum;
+}
+
 REALM_DEV float reduce_base(const GemmArgs &g, const ReduceSite &r, int tile, int e, int TILE)
 {
-    const float *p = g.part + (size_t)tile * g.ksplit * TILE + e;
-    float sum = p[0];
-    for (int c = 1; c < g.ksplit; ++c)
-        sum += p[(size_t)c * TILE];
+    float sum = sum_parts(g.part + (size_t)tile * g.ksplit * TILE + e, g.ksplit, TILE);
     if (__builtin_expect(__builtin_isnan(g.tscale[r.tok]) || __builtin_isnan(sum), 0)) {
         auto pick = [&](auto a0, auto a1, auto a2, auto a3) {
             return r.seg == 0 ? a0 : r.seg == 1 ? a1 : r.seg == 2 ? a2 : a3;
@@ -912,10 +928,7 @@ extern "C" __global__ __launch_bounds__(256) void realm_gemm_tiled_reduce_lora(G
     // the base product's parts
     float sum = 0.f;
     if (live) {
-        const float *pp = g.part + (size_t)tile * g.ksplit * TILE + e;
-        sum = pp[0];
-        for (int c = 1; c < g.ksplit; ++c)
-            sum += pp[(size_t)c * TILE];
+        sum = sum_parts(g.part + (size_t)tile * g.ksplit * TILE + e, g.ksplit, TILE);
     }
     // this element's adapter and its B row: up to 256 bytes in registers
     // when the row is 16-byte aligned (f16: ranks to 128, f32: to 64)
