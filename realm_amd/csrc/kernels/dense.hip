@@ -171,9 +171,19 @@ extern "C" __global__ __launch_bounds__(256) void realm_dense_reduce(const float
     const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
     if (i >= n)
         return;
-    float s = part[i];
-    for (int z = 1; z < ks; ++z)
-        s += part[(size_t)z * n + i];
+    // the parts' loads 8 at a time (one memory round trip per 8 parts)
+    float s = 0.f;
+    for (int z0 = 0; z0 < ks; z0 += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (z0 + u < ks)
+                v[u] = part[(size_t)(z0 + u) * n + i];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (z0 + u < ks)
+                s = z0 + u == 0 ? v[u] : s + v[u];
+    }
     C[i] = s;
 }
 
