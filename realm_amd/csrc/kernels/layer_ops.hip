@@ -389,8 +389,9 @@ __device__ void attention_tiled(const float *__restrict__ q, const float *__rest
     const int nq = min(ATQ, seq - q0);
     // keys this workgroup walks: its split's, up to the last one any row of
     // the tile sees
-    const int kb = sp * chunk;
-    const int kl = min(min(kb + chunk, kv_len), position + q0 + nq);
+    const int kb = (int)min((long long)sp * chunk, (long long)kv_len);
+    const int kl = (int)min(min((long long)kb + chunk, (long long)kv_len),
+                            (long long)position + q0 + nq);
 
     const int rw = 16 * (wave & 1), cw = 16 * (wave >> 1);
     floatx4 qv[NG];
