@@ -322,18 +322,18 @@ extern "C" __global__ __launch_bounds__(ATT_TH) void realm_attention(
 
 // Causal attention for many query tokens (prefill), tiled: one workgroup
 // of 4 waves per (32 query tokens, head, key split) walks its visible keys
-// in blocks of 32, each block's K and V staged once in LDS for all 32
+// in blocks of ATK (64, or 32 for head_dim 256), each block's K and V staged once in LDS for all 32
 // queries (the one-workgroup-per-token kernel reads every visible key once
 // per query).  Both products run on v_mfma_f32_16x16x4_f32 (f32 products
 // and sums: results differ from a CPU f32 loop only in the order of the
 // additions); lane l supplies A[l%16][l/16] and B[l/16][l%16], element v of
 // its result is D[4(l/16) + v][l%16].
-//  * S = Q K^T / sqrt(head_dim): wave w owns the 16 x 16 quadrant (rows
-//    16(w&1), keys 16(w>>1)); its Q rows stay in registers for the whole
+//  * S = Q K^T / sqrt(head_dim): wave w owns rows 16(w&1) and keys
+//    (ATK/2)(w>>1) .. + ATK/2 - 1; its Q rows stay in registers for the whole
 //    walk, a lane holding head_dim elements 16g + 4(l/16) .. + 3 of its row
 //    per group g, read as float4 (K the same way from LDS), so the four
 //    MFMA steps of a group take the float4's four components.
-//  * Softmax online (thread t: row t / 8, keys 4 (t % 8) .. + 3): the row's
+//  * Softmax online (thread t: row t / 8, keys (ATK/8)(t % 8) ..): the row's
 //    running max m skips NaN scores (f32::max), a non-finite score gets
 //    weight 0 (standard.rs:119-126), so an +Inf score zeroes every finite
 //    weight and the row's output is 0; when the max grows the row's sum
@@ -347,7 +347,7 @@ extern "C" __global__ __launch_bounds__(ATT_TH) void realm_attention(
 // aligned).
 namespace {
 typedef float floatx4 __attribute__((ext_vector_type(4)));
-constexpr int ATQ = 32, ATK = 32; // query rows, keys per block
+constexpr int ATQ = 32; // query rows per workgroup
 
 // K and V rows k0 .. k0 + nk - 1 of one block into registers (rows past nk:
 // K repeats row nk - 1, V is zero)
@@ -367,7 +367,10 @@ __device__ __forceinline__ void att_load(const float *__restrict__ kc, const flo
     }
 }
 
-template <int HD>
+// ATK keys per block (32 or 64): each wave's S tile is 16 rows x ATK / 2
+// keys (ATK / 32 MFMA tiles side by side), each softmax thread takes ATK / 8
+// keys of its row
+template <int HD, int ATK>
 __device__ void attention_tiled(const float *__restrict__ q, const float *__restrict__ kc,
                                 const float *__restrict__ vc, int seq, int kv_len, int position,
                                 int heads, int kv_heads, float scale, int splits, int chunk,
@@ -377,6 +380,8 @@ __device__ void attention_tiled(const float *__restrict__ q, const float *__rest
     constexpr int NG = HD / 16;             // groups of 16 head_dim elements
     constexpr int NL = ATK * HD / 4 / 256;  // float4 of K (and of V) per thread and block
     constexpr int NT = HD / 32;             // 16 x 16 output tiles per wave
+    constexpr int SJ = ATK / 32;            // 16 x 16 S tiles per wave
+    constexpr int KPT = ATK / 8;            // keys per softmax thread
     __shared__ __align__(16) float Ks[ATK * LK];
     __shared__ __align__(16) float Vs[ATK * LV];
     __shared__ __align__(16) float Ps[ATQ * LP];
@@ -393,7 +398,7 @@ __device__ void attention_tiled(const float *__restrict__ q, const float *__rest
     const int kl = (int)min(min((long long)kb + chunk, (long long)kv_len),
                             (long long)position + q0 + nq);
 
-    const int rw = 16 * (wave & 1), cw = 16 * (wave >> 1);
+    const int rw = 16 * (wave & 1), cw = (ATK / 2) * (wave >> 1);
     floatx4 qv[NG];
     {
         const int r = rw + lr;
@@ -429,32 +434,46 @@ __device__ void attention_tiled(const float *__restrict__ q, const float *__rest
         __syncthreads();
         if (k0 + ATK < kl) // the next block's loads fly during this one
             att_load<HD, NL>(kc, vc, k0 + ATK, min(ATK, kl - k0 - ATK), kvh, kv_dim, tid, kr, vr);
-        // S quadrant
+        // this wave's S tiles
         {
-            floatx4 sv = {0.f, 0.f, 0.f, 0.f};
-            const float *kp = Ks + (cw + lr) * LK + 4 * lc;
+            floatx4 sv[SJ];
 #pragma unroll
-            for (int g = 0; g < NG; ++g) {
-                const float4 kk = *reinterpret_cast<const float4 *>(kp + 16 * g);
-                sv = __builtin_amdgcn_mfma_f32_16x16x4f32(qv[g][0], kk.x, sv, 0, 0, 0);
-                sv = __builtin_amdgcn_mfma_f32_16x16x4f32(qv[g][1], kk.y, sv, 0, 0, 0);
-                sv = __builtin_amdgcn_mfma_f32_16x16x4f32(qv[g][2], kk.z, sv, 0, 0, 0);
-                sv = __builtin_amdgcn_mfma_f32_16x16x4f32(qv[g][3], kk.w, sv, 0, 0, 0);
-            }
+            for (int j = 0; j < SJ; ++j)
+                sv[j] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int v = 0; v < 4; ++v)
-                Ps[(rw + 4 * lc + v) * LP + cw + lr] = sv[v] * scale;
+            for (int g = 0; g < NG; ++g)
+#pragma unroll
+                for (int j = 0; j < SJ; ++j) {
+                    const float4 kk = *reinterpret_cast<const float4 *>(
+                        Ks + (cw + 16 * j + lr) * LK + 4 * lc + 16 * g);
+                    sv[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv[g][0], kk.x, sv[j], 0, 0, 0);
+                    sv[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv[g][1], kk.y, sv[j], 0, 0, 0);
+                    sv[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv[g][2], kk.z, sv[j], 0, 0, 0);
+                    sv[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv[g][3], kk.w, sv[j], 0, 0, 0);
+                }
+#pragma unroll
+            for (int j = 0; j < SJ; ++j)
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+                    Ps[(rw + 4 * lc + v) * LP + cw + 16 * j + lr] = sv[j][v] * scale;
         }
         __syncthreads();
-        // online softmax of row qi over keys 4 kq .. 4 kq + 3
+        // online softmax of row qi over keys KPT kq .. KPT kq + KPT - 1
         {
-            float4 s4 = *reinterpret_cast<const float4 *>(Ps + qi * LP + 4 * kq);
-            float sv[4] = {s4.x, s4.y, s4.z, s4.w};
-            bool vis[4];
+            float sv[KPT];
+#pragma unroll
+            for (int c4 = 0; c4 < KPT / 4; ++c4) {
+                const float4 s4 = *reinterpret_cast<const float4 *>(Ps + qi * LP + KPT * kq + 4 * c4);
+                sv[4 * c4] = s4.x;
+                sv[4 * c4 + 1] = s4.y;
+                sv[4 * c4 + 2] = s4.z;
+                sv[4 * c4 + 3] = s4.w;
+            }
+            bool vis[KPT];
             float bmax = -INFINITY;
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int j = k0 + 4 * kq + u;
+            for (int u = 0; u < KPT; ++u) {
+                const int j = k0 + KPT * kq + u;
                 vis[u] = qi < nq && j < kl && j <= qpos;
                 if (vis[u])
                     bmax = fmaxf(bmax, sv[u]);
@@ -466,13 +485,16 @@ __device__ void attention_tiled(const float *__restrict__ q, const float *__rest
             // rescale of what the row holds: 0 while it holds nothing
             const float rs = m == -INFINITY ? 0.f
                                             : (mn == INFINITY && m == INFINITY ? 1.f : expf(m - mn));
-            float e[4], ps = 0.f;
+            float e[KPT], ps = 0.f;
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
+            for (int u = 0; u < KPT; ++u) {
                 e[u] = vis[u] && __builtin_isfinite(sv[u]) ? expf(sv[u] - mn) : 0.f;
                 ps += e[u];
             }
-            *reinterpret_cast<float4 *>(Ps + qi * LP + 4 * kq) = make_float4(e[0], e[1], e[2], e[3]);
+#pragma unroll
+            for (int c4 = 0; c4 < KPT / 4; ++c4)
+                *reinterpret_cast<float4 *>(Ps + qi * LP + KPT * kq + 4 * c4) =
+                    make_float4(e[4 * c4], e[4 * c4 + 1], e[4 * c4 + 2], e[4 * c4 + 3]);
 #pragma unroll
             for (int off = 1; off < 8; off <<= 1)
                 ps += __shfl_xor(ps, off, 64);
@@ -540,8 +562,8 @@ __device__ void attention_tiled(const float *__restrict__ q, const float *__rest
         const float *q, const float *kc, const float *vc, int seq, int kv_len, int position,  \
         int heads, int kv_heads, float scale, int splits, int chunk, float *out, float *part) \
     {                                                                                          \
-        attention_tiled<HD>(q, kc, vc, seq, kv_len, position, heads, kv_heads, scale, splits,  \
-                            chunk, out, part);                                                 \
+        attention_tiled<HD, HD <= 128 ? 64 : 32>(q, kc, vc, seq, kv_len, position, heads,     \
+                                                 kv_heads, scale, splits, chunk, out, part);   \
     }
 ATT_TILED(32)
 ATT_TILED(64)
